@@ -1,0 +1,90 @@
+// Host-side helpers shared by the C-ABI launchers: return codes, device facts, a per-(device, stream) workspace and
+// the tuning overrides used by parameter sweeps.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <utility>
+
+namespace rw_host {
+
+// Return codes of every launcher: 0 = success (also the no-op of an empty problem), -1 = invalid or unsupported
+// argument, anything else = the hipError_t the runtime reported.
+constexpr int kOk = 0;
+constexpr int kInvalid = -1;
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Compute units of the current device, queried once per device.
+inline int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    n = 256;
+  }
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// A device buffer of at least `bytes` owned by the library for (current device, stream). Launches on one stream are
+// ordered, so a buffer reused by consecutive launches on its stream is never read and written by two of them at once.
+// It grows by reallocation (the runtime waits for work that may still use the old buffer) and lives until the process
+// ends. Returns nullptr with *err set on failure.
+inline void* stream_workspace(hipStream_t stream, size_t bytes, int* err) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> buffers;
+  *err = kOk;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *err = (int)e;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  auto& slot = buffers[std::make_pair(dev, stream)];
+  if (slot.second >= bytes && slot.first) return slot.first;
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  if (slot.first) {
+    e = hipFree(slot.first);
+    slot = {nullptr, 0};
+    if (e != hipSuccess) {
+      *err = (int)e;
+      return nullptr;
+    }
+  }
+  void* p = nullptr;
+  e = hipMalloc(&p, want);
+  if (e != hipSuccess) {
+    *err = (int)e;
+    return nullptr;
+  }
+  slot = {p, want};
+  return p;
+}
+
+// Tuning overrides: slot i holds 0 (automatic choice) or a value the launcher uses instead of its own choice. They are
+// process-wide and meant for parameter sweeps; the automatic choices are the tuned defaults.
+constexpr int kTuneSlots = 16;
+inline std::atomic<int>* tune_table() {
+  static std::atomic<int> table[kTuneSlots];
+  return table;
+}
+inline int tune_get(int slot) { return tune_table()[slot].load(std::memory_order_relaxed); }
+inline int tune_set(int slot, int value) {
+  if (slot < 0 || slot >= kTuneSlots) return kInvalid;
+  tune_table()[slot].store(value, std::memory_order_relaxed);
+  return kOk;
+}
+
+}  // namespace rw_host

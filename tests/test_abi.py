@@ -1,0 +1,93 @@
+"""CPU checks of the drop-in boundary: every library loads and exports exactly the entry points include/<op>.h
+declares, the argument checks return the reference's codes without touching a GPU, and the wrappers reject what the
+reference's wrappers reject (with ValueError) before any launch.
+"""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+OPS = ("softmax", "rmsnorm", "rope", "topk")
+
+
+def declared(op):
+    text = open(os.path.join(ROOT, "include", op + ".h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:int|long long)\s+(\w+)\s*\(", text, flags=re.M)
+
+
+def exported(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+@pytest.mark.parametrize("op", OPS)
+def test_library_exports_the_header(pkg, op):
+    path = pkg.lib_path(op)
+    assert os.path.exists(path), f"{path} not built"
+    lib = ctypes.CDLL(path)
+    names = declared(op)
+    assert "launch" in names
+    for name in names:
+        assert hasattr(lib, name), f"{op}: {name} declared in include/{op}.h but not exported"
+    # nothing beyond the header is exported with C linkage
+    c_symbols = {s for s in exported(path) if not s.startswith("_Z") and not s.startswith("_")}
+    assert c_symbols == set(names), f"{op}: exported {sorted(c_symbols)} vs declared {sorted(names)}"
+
+
+def test_softmax_codes_without_gpu(pkg):
+    lib = ctypes.CDLL(pkg.lib_path("softmax"))
+    assert lib.launch(None, None, ctypes.c_longlong(0), ctypes.c_longlong(5), 0, 256, 1024, None) == 0
+    assert lib.launch(None, None, ctypes.c_longlong(5), ctypes.c_longlong(0), 0, 256, 1024, None) == 0
+    assert lib.launch(None, None, ctypes.c_longlong(5), ctypes.c_longlong(5), 2, 256, 1024, None) == -1
+    assert lib.softmax_tune(99, 1) == -1 and lib.softmax_tune(0, 0) == 0
+
+
+def test_rmsnorm_codes_without_gpu(pkg):
+    lib = ctypes.CDLL(pkg.lib_path("rmsnorm"))
+    lib.launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
+                           ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
+    assert lib.launch(None, None, 0, 8, 1, 1e-6, 256, None) == 0          # no rows: no-op
+    assert lib.launch(None, None, 1 << 31, 8, 1, 1e-6, 256, None) == -1   # rows beyond int32
+    assert lib.launch(None, None, 4, 0, 1, 1e-6, 256, None) == -1         # cols
+    assert lib.launch(None, None, 4, 8, 1, 1e-6, 48, None) == -1          # threads not a multiple of 32
+    assert lib.launch(None, None, 4, 8, 1, 1e-6, 2048, None) == -1        # threads > 1024
+    assert lib.launch(None, None, 4, 8, 0, 1e-6, 256, None) == -1         # fp32 is not served
+    lib.rmsnorm_launch_weighted.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
+                                                                     ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
+    assert lib.rmsnorm_launch_weighted(None, 1, None, 4, 8, 3, 1e-6, 256, None) == -1
+    assert lib.rmsnorm_launch_weighted(None, 1, None, 0, 8, 1, 1e-6, 256, None) == 0
+
+
+def test_rope_codes_without_gpu(pkg):
+    lib = ctypes.CDLL(pkg.lib_path("rope"))
+    lib.launch.argtypes = [ctypes.c_void_p] * 7 + [ctypes.c_longlong] + [ctypes.c_int] * 7 + [ctypes.c_void_p]
+    n = [None] * 7
+    assert lib.launch(*n, 0, 1, 1, 128, 1, 0, 40, 1, None) == 0
+    assert lib.launch(*n, 1 << 31, 1, 1, 128, 1, 0, 40, 1, None) == -1
+    assert lib.launch(*n, 4, 1, 1, 127, 1, 0, 40, 1, None) == -1
+    assert lib.launch(*n, 4, 1, 0, 128, 1, 0, 40, 1, None) == -1
+    assert lib.launch(*n, 4, 1, 1, 128, 0, 0, 40, 1, None) == -1
+    assert lib.launch(*n, 4, 1, 1, 128, 1, 3, 40, 1, None) == -1
+    assert lib.launch(*n, 4, 1, 1, 128, 1, 0, 40, 0, None) == -1
+
+
+def test_wrappers_reject_bad_inputs_before_launch(pkg):
+    with pytest.raises(ValueError):
+        pkg.softmax(torch.zeros(4, 4, dtype=torch.float64))
+    with pytest.raises(ValueError):
+        pkg.softmax(torch.zeros(4, 4))  # a CPU tensor: no CPU path
+    with pytest.raises(ValueError):
+        pkg.rmsnorm(torch.zeros(4, 8))  # fp32 is not an RMSNorm dtype of the reference
+    with pytest.raises(ValueError):
+        pkg.rmsnorm(torch.zeros(4, 8, dtype=torch.bfloat16))
+    q = torch.zeros(1, 2, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        pkg.rope(q, q, torch.zeros(1, 2, dtype=torch.int32), cos=torch.zeros(4, 64), sin=torch.zeros(4, 64))
+    with pytest.raises(ValueError):
+        pkg.rope(q, q, torch.zeros(1, 2, dtype=torch.int64), cos=torch.zeros(4, 64), sin=torch.zeros(4, 64))

@@ -1,0 +1,128 @@
+"""GPU parity of RoPE (build/rope/libkernel.so: the reference ABI `launch` with a cos/sin cache, and the on-the-fly
+`rope_launch_freq`) against the oracle, bit for bit: the kernel evaluates exactly the oracle's fp32 operations (no
+contraction) and, on the fly, the same correctly rounded cos/sin. Against a cache built by torch (whose cos/sin may be
+an fp32 ulp off) the on-the-fly result is identical almost everywhere and within the error such an ulp explains.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import bits16, ulp16
+
+pytestmark = pytest.mark.gpu
+
+DT = {torch.bfloat16: "bf16", torch.float16: "fp16"}
+CDT = {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp16"}
+
+
+def inputs(B, S, Hq, Hk, D, dtype, seed, max_pos=8192):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, S, Hq, D, generator=g).to(dtype)
+    k = torch.randn(B, S, Hk, D, generator=g).to(dtype)
+    pos = torch.randint(0, max_pos, (B, S), generator=g)
+    return q, k, pos
+
+
+def flat(t):
+    return bits16(t).reshape(-1, t.shape[2], t.shape[3])
+
+
+def cache_np(t):
+    return t.numpy() if t.dtype == torch.float32 else bits16(t)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cdtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(1, 5, 4, 2, 64), (2, 33, 32, 8, 128), (1, 7, 3, 1, 256), (1, 9, 2, 2, 40)])
+def test_cache_path(pkg, oracle, dev, dtype, cdtype, shape):
+    from oracle import torch_paths
+    B, S, Hq, Hk, D = shape
+    q, k, pos = inputs(B, S, Hq, Hk, D, dtype, sum(shape))
+    cos, sin = torch_paths.rope_cache(8192, D, dtype=cdtype)
+    print(f"[rope cache] {shape} {dtype} cache {cdtype}", flush=True)
+    qo, ko = pkg.rope(q.to(dev), k.to(dev), pos.to(dev), cos=cos.to(dev), sin=sin.to(dev))
+    rq, rk = oracle.rope_cache(flat(q), flat(k), cache_np(cos), cache_np(sin), pos.view(-1).numpy(), DT[dtype],
+                               CDT[cdtype])
+    assert np.array_equal(flat(qo), rq) and np.array_equal(flat(ko), rk)
+    # out of place: the inputs are untouched
+    assert np.array_equal(bits16(q), bits16(q)) and qo.data_ptr() != q.data_ptr()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(1, 5, 4, 2, 64), (2, 33, 32, 8, 128), (1, 3, 64, 64, 128), (1, 9, 2, 2, 40),
+                                   (1, 4, 1, 1, 1024)])
+def test_freq_path_inplace(pkg, oracle, dev, dtype, shape):
+    B, S, Hq, Hk, D = shape
+    q, k, pos = inputs(B, S, Hq, Hk, D, dtype, 7 * sum(shape))
+    inv_freq = pkg.workloads.rope_inv_freq(D)
+    print(f"[rope freq] {shape} {dtype}", flush=True)
+    qd, kd = q.to(dev), k.to(dev)
+    qo, ko = pkg.rope(qd, kd, pos.to(dev), inv_freq=inv_freq.to(dev), inplace=True)
+    assert qo.data_ptr() == qd.data_ptr() and ko.data_ptr() == kd.data_ptr()
+    rq, rk = oracle.rope_freq(flat(q), flat(k), pos.view(-1).numpy(), inv_freq.numpy(), DT[dtype])
+    assert np.array_equal(flat(qd), rq) and np.array_equal(flat(kd), rk)
+
+
+def test_cache_path_inplace_through_abi(pkg, oracle, dev):
+    from oracle import torch_paths
+    q, k, pos = inputs(2, 17, 8, 2, 128, torch.bfloat16, 99)
+    cos, sin = torch_paths.rope_cache(8192, 128)
+    qd, kd = q.to(dev), k.to(dev)
+    qo, ko = pkg.rope(qd, kd, pos.to(dev), cos=cos.to(dev), sin=sin.to(dev), inplace=True)
+    rq, rk = oracle.rope_cache(flat(q), flat(k), cos.numpy(), sin.numpy(), pos.view(-1).numpy())
+    assert np.array_equal(flat(qd), rq) and np.array_equal(flat(kd), rk)
+
+
+def test_position_zero_is_identity_and_large_positions(pkg, oracle, dev):
+    q, k, _ = inputs(1, 6, 4, 2, 128, torch.bfloat16, 5)
+    pos = torch.tensor([[0, 0, 1, 65535, 1 << 20, (1 << 24) + 1]])
+    inv_freq = pkg.workloads.rope_inv_freq(128)
+    qo, ko = pkg.rope(q.to(dev), k.to(dev), pos.to(dev), inv_freq=inv_freq.to(dev))
+    assert np.array_equal(flat(qo)[:2], flat(q)[:2])
+    rq, rk = oracle.rope_freq(flat(q), flat(k), pos.view(-1).numpy(), inv_freq.numpy())
+    assert np.array_equal(flat(qo), rq) and np.array_equal(flat(ko), rk)
+
+
+def test_invalid_arguments(pkg, dev):
+    lib = pkg.candidate("rope")._lib
+    s = torch.cuda.current_stream().cuda_stream
+    x = torch.zeros(4, 128, dtype=torch.bfloat16, device=dev)
+    p = x.data_ptr()
+    assert lib.launch(p, p, p, p, p, p, p, 0, 1, 1, 128, 1, 0, 40, 1, s) == 0       # no tokens: no-op
+    assert lib.launch(p, p, p, p, p, p, p, 1, 1, 1, 127, 1, 0, 40, 1, s) == -1      # odd head_dim
+    assert lib.launch(p, p, p, p, p, p, p, 1, 0, 1, 128, 1, 0, 40, 1, s) == -1      # no q heads
+    assert lib.launch(p, p, p, p, p, p, p, 1, 1, 1, 128, 3, 0, 40, 1, s) == -1      # qk dtype
+    assert lib.launch(p, p, p, p, p, p, p, 1, 1, 1, 128, 1, 5, 40, 1, s) == -1      # cache dtype
+    assert lib.launch(p, p, p, p, p, p, p, 1, 1, 1, 128, 1, 0, 0, 1, s) == -1       # rows < 1
+    assert lib.launch(p, p, p, p, p, p, p, 1, 1, 1, 128, 1, 0, 40, 70000, s) == -1  # splits
+    assert lib.rope_launch_freq(p, p, p, None, p, p, 1, 1, 1, 128, 1, s) == -1      # no inv_freq
+
+
+def test_config_rope_4x4096_32q_8kv_128(pkg, oracle, dev):
+    inp = pkg.workloads.rope_4x4096_32q_8kv_128()
+    q, k, pos, inv_freq = inp["q"], inp["k"], inp["position_ids"], inp["inv_freq"]
+    qd, kd = q.to(dev), k.to(dev)
+    print("[rope] config in place, on the fly", flush=True)
+    pkg.rope(qd, kd, pos.to(dev), inv_freq=inv_freq.to(dev), inplace=True)
+    rq, rk = oracle.rope_freq(flat(q), flat(k), pos.view(-1).numpy(), inv_freq.numpy())
+    assert np.array_equal(flat(qd), rq) and np.array_equal(flat(kd), rk)
+    # against the reference path with a cache built by torch, whose cos/sin may be an fp32 ulp off the correctly
+    # rounded values: identical almost everywhere; where a * cos and b * sin nearly cancel, that fp32 ulp can move
+    # the result by a few bf16 ulps, so the bound is on the absolute error it can cause
+    from oracle import torch_paths
+    cos, sin = torch_paths.rope_cache(4096, 128)
+    tq = bits16(torch_paths.rope(q[:1, :1024], cos, sin, pos[:1, :1024]))
+    got = bits16(qd.cpu()[:1, :1024])
+    d = ulp16(got, tq)
+    assert (d == 0).mean() > 0.99
+    gf = torch.from_numpy(got.view(np.int16)).view(torch.bfloat16).float()
+    tf = torch.from_numpy(tq.view(np.int16)).view(torch.bfloat16).float()
+    xa = q[:1, :1024].float().abs()
+    pair = xa + torch.cat((xa[..., 64:], xa[..., :64]), -1)
+    assert ((gf - tf).abs() <= tf.abs() * 2 ** -7 + pair * 2 ** -22).all()
+    # the cache form of the same call agrees with the on-the-fly form over the oracle's table
+    ct, st = oracle.rope_table(inv_freq.numpy(), 4096, 128)
+    qo, ko = pkg.rope(q.to(dev), k.to(dev), pos.to(dev), cos=torch.from_numpy(ct).to(dev),
+                      sin=torch.from_numpy(st).to(dev))
+    assert np.array_equal(flat(qo), rq) and np.array_equal(flat(ko), rk)

@@ -1,0 +1,127 @@
+"""GPU parity of softmax (build/softmax/libkernel.so through the reference ABI `launch`) against the oracle.
+
+fp32: |y - oracle| <= 1e-5 |oracle| elementwise (the oracle is the fp64 softmax rounded once); bf16: within 1 ulp.
+Shapes cover every tier: wave-per-row and workgroup-per-row rows (full and ragged), the split tier for long rows, and
+the generic tier for lengths that are not a multiple of the vector width and for misaligned pointers.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_rel, assert_ulp, bits16
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+
+
+def run_fp32(pkg, oracle, dev, x, what):
+    print(f"[softmax fp32] {what} shape={tuple(x.shape)}", flush=True)
+    y = pkg.softmax(x.to(dev)).cpu()
+    assert_rel(y.numpy(), oracle.softmax(x.numpy(), "fp32"), FP32_TOL, what)
+    return y
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 4), (3, 256), (5, 1000), (64, 1024), (9, 2048), (7, 4096),
+                                       (33, 8192), (3, 12288), (2, 32768), (2, 32772), (3, 65536),
+                                       (2, 131072 + 4), (5, 1), (4, 7), (6, 1001), (2, 40001)])
+def test_fp32_shapes(pkg, oracle, dev, rows, cols):
+    g = torch.Generator().manual_seed(rows * 100003 + cols)
+    run_fp32(pkg, oracle, dev, torch.randn(rows, cols, generator=g) * 3, f"{rows}x{cols}")
+
+
+@pytest.mark.parametrize("rows,cols", [(3, 512), (64, 2048), (7, 8192), (2, 65536), (2, 131072), (4, 1003)])
+def test_bf16_shapes(pkg, oracle, dev, rows, cols):
+    g = torch.Generator().manual_seed(rows * 7 + cols)
+    x = (torch.randn(rows, cols, generator=g) * 3).bfloat16()
+    print(f"[softmax bf16] {rows}x{cols}", flush=True)
+    y = pkg.softmax(x.to(dev))
+    assert_ulp(bits16(y), oracle.softmax(bits16(x), "bf16"), 1, f"bf16 {rows}x{cols}")
+
+
+def test_many_rows_persistent(pkg, oracle, dev):
+    # more rows than resident workgroups: every workgroup walks several rows
+    g = torch.Generator().manual_seed(5)
+    run_fp32(pkg, oracle, dev, torch.randn(20000, 256, generator=g), "20000x256")
+    run_fp32(pkg, oracle, dev, torch.randn(5000, 1024, generator=g), "5000x1024")
+
+
+def test_misaligned_and_special_values(pkg, oracle, dev):
+    g = torch.Generator().manual_seed(6)
+    base = torch.randn(4 * 1024 + 1, generator=g).to(dev)
+    x = base[1:].view(4, 1024)  # data pointer 4 bytes past a 16-byte boundary: the generic tier
+    y = torch.empty_like(x)
+    lib = pkg.candidate("softmax")._lib
+    assert lib.launch(x.data_ptr(), y.data_ptr(), 4, 1024, 0, 256, 1024, torch.cuda.current_stream().cuda_stream) == 0
+    assert_rel(y.cpu().numpy(), oracle.softmax(x.cpu().numpy(), "fp32"), FP32_TOL, "misaligned")
+    s = torch.randn(4, 1024, generator=g)
+    s[0, 10] = float("-inf")
+    s[1, :] = float("-inf")
+    s[2, 5] = float("nan")
+    s[3, ::3] = float("-inf")
+    y = pkg.softmax(s.to(dev)).cpu()
+    assert y[0, 10] == 0 and torch.isnan(y[1]).all() and torch.isnan(y[2]).all() and (y[3, ::3] == 0).all()
+    ref = oracle.softmax(s.numpy(), "fp32")
+    assert_rel(y[[0, 3]].numpy(), ref[[0, 3]], FP32_TOL, "special values")
+
+
+def test_long_rows_with_infinite_chunks(pkg, oracle, dev):
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(3, 70000, generator=g)
+    x[0, :40000] = float("-inf")  # whole chunks of -inf must not poison the merge
+    x[1, :] = float("-inf")
+    y = pkg.softmax(x.to(dev)).cpu()
+    assert torch.isnan(y[1]).all()
+    ref = oracle.softmax(x.numpy(), "fp32")
+    assert_rel(y[[0, 2]].numpy(), ref[[0, 2]], FP32_TOL, "long rows")
+
+
+def test_empty_is_noop(pkg, dev):
+    lib = pkg.candidate("softmax")._lib
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib.launch(None, None, 0, 10, 0, 256, 1024, s) == 0
+    assert lib.launch(None, None, 10, 0, 1, 256, 1024, s) == 0
+    x = torch.empty(0, 5, device=dev)
+    assert pkg.softmax(x).shape == (0, 5)
+
+
+def test_config_softmax_4096x4096(pkg, oracle, dev):
+    x = pkg.workloads.softmax_4096x4096()["x"]
+    y = run_fp32(pkg, oracle, dev, x, "softmax_4096x4096")
+    s = y.double().sum(-1)
+    assert torch.allclose(s, torch.ones_like(s), atol=1e-5)
+
+
+def test_config_softmax_64x262144(pkg, oracle, dev):
+    x = pkg.workloads.softmax_64x262144()["x"]
+    y = run_fp32(pkg, oracle, dev, x, "softmax_64x262144")
+    # the reference's own path (torch fp32) agrees within the same tolerance
+    assert_rel(y.numpy(), torch.softmax(x, -1).numpy(), 2 * FP32_TOL, "vs torch fp32")
+
+
+def test_tuning_overrides_keep_results(pkg, oracle, dev):
+    """Every row-tier shape the tuning slots can force computes the same row."""
+    lib = pkg.candidate("softmax")._lib
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(300, 4096, generator=g)
+    ref = oracle.softmax(x.numpy(), "fp32")
+    xd = x.to(dev)
+    try:
+        for waves, nv in [(2, 8), (4, 4), (8, 2), (16, 1)]:
+            lib.softmax_tune(0, waves)
+            lib.softmax_tune(1, nv)
+            for per_cu in (1, 2):
+                lib.softmax_tune(2, per_cu)
+                print(f"[softmax tune] waves={waves} nv={nv} per_cu={per_cu}", flush=True)
+                assert_rel(pkg.softmax(xd).cpu().numpy(), ref, FP32_TOL, f"w{waves} nv{nv}")
+        lib.softmax_tune(0, 0), lib.softmax_tune(1, 0), lib.softmax_tune(2, 0)
+        for tier in (2, 3):
+            lib.softmax_tune(5, tier)
+            print(f"[softmax tune] tier={tier}", flush=True)
+            assert_rel(pkg.softmax(xd).cpu().numpy(), ref, FP32_TOL, f"tier {tier}")
+    finally:
+        for slot in range(7):
+            lib.softmax_tune(slot, 0)
