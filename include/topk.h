@@ -1,0 +1,38 @@
+/* topk: the k largest entries of each row of x[rows, cols] in fp32 (dtype 0) or bf16 (dtype 1), sorted descending with
+ * ties broken by the lowest index (+0 above -0, +NaN above +inf, -NaN at the bottom: the composite order of the
+ * reference), 1 <= k <= 1024. Library: build/topk/libkernel.so. Replaces the reference's topk/kernel.cu:520-570 (ctypes
+ * binding topk/candidate.py:31-36). Device pointers; asynchronous on `stream`; no allocation: the caller owns the
+ * workspace and counters. */
+#ifndef ROWKERN_TOPK_H
+#define ROWKERN_TOPK_H
+#include <hip/hip_runtime_api.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* topk/kernel.cu:520: columns per workgroup for a rows x cols launch (the row's chunk count is ceil(cols / chunk)),
+ * sized so the grid is resident at once; chunks of at least max(min_chunk, 4096) columns, a multiple of 4 when a row is
+ * split. `threads` and `depth` are the reference's CUDA tuning knobs, accepted and unused. */
+long long plan(long long rows, long long cols, int dtype, int threads, int depth, int min_chunk);
+
+/* topk/kernel.cu:549: values [rows, k] in x's dtype, indices [rows, k] int64; work: u64 [rows * nchunks * k]
+ * (nchunks = ceil(cols / chunk), only used when nchunks > 1); counters: u32 [>= rows], zero on entry, left zero.
+ * Returns 0 (rows <= 0 or k <= 0 is a no-op), -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0,
+ * a split row with chunk % 4 != 0 or nchunks * k > INT_MAX / 2, threads not 128/256/512, depth not 2/4/8 or an unknown
+ * dtype, otherwise the hipError_t of the launch. Launches sharing work/counters must be ordered (one stream). */
+int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows, long long cols,
+           int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream);
+
+/* No counterpart in the reference (whose counters self-reset only when a launch completes): zeroes counters[0, rows)
+ * on `stream`, for a caller recovering from a launch that did not complete. Returns 0, -1 (NULL counters) or the
+ * hipError_t of the memset. */
+int topk_reset(void* counters, long long rows, hipStream_t stream);
+
+/* No counterpart in the reference: tuning override for parameter sweeps. Slot 0: resident workgroups per CU assumed by
+ * plan(). Returns 0 or -1. */
+int topk_tune(int slot, int value);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

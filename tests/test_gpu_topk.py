@@ -1,0 +1,162 @@
+"""GPU parity of top-k (build/topk/libkernel.so: `plan`, `launch`, `topk_reset`) against the oracle, bit for bit:
+values (the element bits) and int64 indices, sorted descending with ties by the lowest index.
+
+Covers single- and multi-chunk rows (the last-workgroup merge), every k class (1, the lane-maxima seed up to 64, the
+general path up to 1024), ties and special values, bf16, unaligned and ragged rows, workspace reuse and the counters'
+self-reset, adversarial orders that force many prunes, and the top-k workload at k = 1, 50 and 1024.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import bits16
+
+pytestmark = pytest.mark.gpu
+
+
+def lib(pkg):
+    return pkg.candidate("topk")._lib
+
+
+def run_abi(pkg, x, k, chunk=None):
+    """Launch through the C-ABI with an explicit chunk (None: plan's)."""
+    cand = pkg.candidate("topk")
+    L = lib(pkg)
+    rows, cols = x.shape
+    dtype = 0 if x.dtype == torch.float32 else 1
+    if chunk is None:
+        chunk = L.plan(rows, cols, dtype, 256, 4, max(4096, 16 * k))
+    nchunks = -(-cols // chunk)
+    work = torch.empty(max(1, rows * nchunks * k), dtype=torch.int64, device=x.device)
+    counters = torch.zeros(max(rows, 1), dtype=torch.int32, device=x.device)
+    vals = torch.empty(rows, k, dtype=x.dtype, device=x.device)
+    idx = torch.empty(rows, k, dtype=torch.int64, device=x.device)
+    err = L.launch(x.data_ptr(), vals.data_ptr(), idx.data_ptr(), work.data_ptr(), counters.data_ptr(), rows, cols, k,
+                   dtype, 256, 4, chunk, torch.cuda.current_stream().cuda_stream)
+    assert err == 0
+    torch.cuda.synchronize()
+    assert (counters == 0).all(), "the row counters must be left at zero"
+    return vals, idx, nchunks
+
+
+def expect(oracle, x, k):
+    if x.dtype == torch.float32:
+        return oracle.topk(x.cpu().numpy(), k, "fp32")
+    return oracle.topk(bits16(x), k, "bf16")
+
+
+def check(pkg, oracle, x_cpu, k, dev, chunk=None, what=""):
+    print(f"[topk] {what} {tuple(x_cpu.shape)} {x_cpu.dtype} k={k} chunk={chunk}", flush=True)
+    vals, idx, nchunks = run_abi(pkg, x_cpu.to(dev), k, chunk)
+    rv, ri = expect(oracle, x_cpu, k)
+    got_i = idx.cpu().numpy()
+    got_v = vals.cpu().numpy() if x_cpu.dtype == torch.float32 else bits16(vals)
+    if not np.array_equal(got_i, ri):
+        bad = np.argwhere(got_i != ri)
+        r, j = bad[0]
+        raise AssertionError(f"{what}: indices differ at {len(bad)} places (nchunks={nchunks}); first row {r} "
+                             f"pos {j}: got {got_i[r, max(0, j - 2):j + 3]} ref {ri[r, max(0, j - 2):j + 3]}")
+    assert np.array_equal(got_v.view(np.uint32) if got_v.dtype == np.float32 else got_v,
+                          rv.view(np.uint32) if rv.dtype == np.float32 else rv), f"{what}: values differ"
+    return nchunks
+
+
+@pytest.mark.parametrize("k", [1, 2, 7, 50, 64, 65, 128, 300, 1024])
+def test_k_classes_single_and_split(pkg, oracle, dev, k):
+    g = torch.Generator().manual_seed(k)
+    x = torch.randn(6, 20000, generator=g) * 2
+    check(pkg, oracle, x, k, dev, chunk=None, what="planned")
+    check(pkg, oracle, x, k, dev, chunk=20000, what="one chunk")
+    assert check(pkg, oracle, x, k, dev, chunk=4096, what="five chunks") == 5
+    check(pkg, oracle, x, k, dev, chunk=2052, what="ten chunks")
+
+
+@pytest.mark.parametrize("rows,cols,k", [(1, 128256, 50), (64, 151936, 50), (512, 32000, 50), (3, 1000, 50),
+                                         (2, 50, 50), (4, 1024, 1024), (1, 4097, 1024), (7, 10001, 13)])
+def test_shapes(pkg, oracle, dev, rows, cols, k):
+    g = torch.Generator().manual_seed(rows * 31 + cols + k)
+    check(pkg, oracle, torch.randn(rows, cols, generator=g) * 2, k, dev, what="shape")
+
+
+def test_ties_and_special_values(pkg, oracle, dev):
+    g = torch.Generator().manual_seed(3)
+    x = torch.randint(0, 6, (5, 30000), generator=g).float()  # massive ties: lowest indices win
+    for k in (1, 50, 1024):
+        check(pkg, oracle, x, k, dev, chunk=4096, what="ties")
+    e = torch.full((3, 9000), 1.25)  # all equal
+    check(pkg, oracle, e, 1024, dev, chunk=4096, what="all equal")
+    check(pkg, oracle, e, 40, dev, what="all equal")
+    s = torch.randn(2, 5000, generator=g)
+    s[0, 10], s[0, 20], s[0, 30], s[0, 40] = 0.0, -0.0, float("inf"), float("-inf")
+    s[1, 11], s[1, 12] = float("nan"), -float("nan")
+    s[1, 100:200] = float("inf")
+    check(pkg, oracle, s, 150, dev, what="special")
+    check(pkg, oracle, s, 7, dev, chunk=1000, what="special split")
+
+
+def test_adversarial_orders(pkg, oracle, dev):
+    # ascending rows: every tile beats the threshold so far (many prunes); descending: the first tile is the answer
+    a = torch.arange(40000, dtype=torch.float32).view(1, -1).repeat(2, 1)
+    a[1] = a[1].flip(0)
+    for k in (1, 50, 1024):
+        check(pkg, oracle, a, k, dev, chunk=8192, what="monotone")
+        check(pkg, oracle, a, k, dev, chunk=40000, what="monotone one chunk")
+    # a cluster of near-equal large values that a coarse histogram cannot split
+    g = torch.Generator().manual_seed(4)
+    c = torch.randn(2, 30000, generator=g)
+    c[:, ::3] = 5.0 + torch.arange(10000).float() * 1e-7
+    check(pkg, oracle, c, 1024, dev, what="cluster")
+
+
+def test_bf16_and_unaligned(pkg, oracle, dev):
+    g = torch.Generator().manual_seed(5)
+    xb = torch.randn(8, 50000, generator=g).bfloat16()
+    for k in (1, 50, 1024):
+        check(pkg, oracle, xb, k, dev, what="bf16")
+    check(pkg, oracle, xb[:, :49999].contiguous(), 50, dev, what="bf16 ragged")
+    base = torch.randn(3 * 20000 + 1, generator=g).to(dev)
+    x = base[1:].view(3, 20000)  # 4 bytes past a 16-byte boundary: scalar loads
+    vals, idx, _ = run_abi(pkg, x, 50, 4096)
+    rv, ri = oracle.topk(x.cpu().numpy(), 50)
+    assert np.array_equal(idx.cpu().numpy(), ri) and np.array_equal(vals.cpu().numpy(), rv)
+
+
+def test_workspace_reuse_and_wrapper(pkg, oracle, dev):
+    g = torch.Generator().manual_seed(6)
+    for i in range(3):  # the wrapper caches plan, workspace and counters across calls of one shape
+        x = torch.randn(16, 60000, generator=g)
+        v, ix = pkg.topk(x.to(dev), 50)
+        rv, ri = oracle.topk(x.numpy(), 50)
+        assert np.array_equal(ix.cpu().numpy(), ri) and np.array_equal(v.cpu().numpy(), rv)
+    counters = pkg.candidate("topk")._counters[dev]
+    assert (counters == 0).all()
+    assert lib(pkg).topk_reset(counters.data_ptr(), counters.numel(), torch.cuda.current_stream().cuda_stream) == 0
+
+
+def test_invalid_arguments(pkg, dev):
+    L = lib(pkg)
+    s = torch.cuda.current_stream().cuda_stream
+    p = torch.zeros(16, device=dev).data_ptr()
+    assert L.launch(p, p, p, p, p, 0, 100, 5, 0, 256, 4, 100, s) == 0      # no rows
+    assert L.launch(p, p, p, p, p, 2, 100, 0, 0, 256, 4, 100, s) == 0      # k = 0
+    assert L.launch(p, p, p, p, p, 2, 100, 101, 0, 256, 4, 100, s) == -1   # k > cols
+    assert L.launch(p, p, p, p, p, 2, 5000, 1025, 0, 256, 4, 5000, s) == -1
+    assert L.launch(p, p, p, p, p, 70000, 100, 5, 0, 256, 4, 100, s) == -1
+    assert L.launch(p, p, p, p, p, 2, 100, 5, 0, 256, 4, 0, s) == -1      # chunk
+    assert L.launch(p, p, p, p, p, 2, 100, 5, 0, 256, 4, 50, s) == -1     # split with chunk % 4
+    assert L.launch(p, p, p, p, p, 2, 100, 5, 0, 100, 4, 100, s) == -1    # threads
+    assert L.launch(p, p, p, p, p, 2, 100, 5, 0, 256, 3, 100, s) == -1    # depth
+    assert L.launch(p, p, p, p, p, 2, 100, 5, 2, 256, 4, 100, s) == -1    # dtype
+
+
+@pytest.mark.parametrize("k", [1, 50, 1024])
+def test_config_topk_128x128256(pkg, oracle, dev, k):
+    x = pkg.workloads.topk_128x128256()["x"]
+    nchunks = check(pkg, oracle, x, k, dev, what="topk_128x128256")
+    print(f"[topk] chunks per row: {nchunks}", flush=True)
+    # the reference's own path: a stable descending sort
+    from oracle import torch_paths
+    v, i = pkg.topk(x.to(dev), k)
+    sv, si = torch_paths.topk(x, k)
+    assert torch.equal(i.cpu(), si) and torch.equal(v.cpu(), sv)
