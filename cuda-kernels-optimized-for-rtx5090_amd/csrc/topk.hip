@@ -470,13 +470,22 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
-// ---- wave kernels (k <= 64) ---------------------------------------------------------------------------------------
+// ---- tile kernels (k <= 64) ---------------------------------------------------------------------------------------
 
-constexpr int kWaveCap = 512;                // wave-private candidate list (4 KB of LDS)
-constexpr int kWaveM = kWaveCap / kWave;     // list entries per lane while pruning (held in registers)
-constexpr int kWaveE = 32;                   // elements per lane per register block
-constexpr int kWaveSub = kWave * kWaveE;     // 2048 elements per register block
-constexpr int kWavePruneAt = kWaveCap / 2;   // prune after a block that leaves more than this
+constexpr int kTileE = 64;      // elements per lane of a register tile (16384 per workgroup)
+constexpr int kTileSeg = 512;   // each wave's list segment (composites)
+constexpr int kTileKeep = 128;  // a list holding more than this after a batch is pruned to its k largest
+constexpr int kTileSort = 256;  // rank-sort capacity (one composite per thread)
+static_assert(kTileKeep <= kTileSort && kTileKeep <= 2 * kWave, "a kept list must fit the sort and two per lane");
+static_assert(kTileSort == kThreads, "the rank sort and the merge heads use one composite per thread");
+
+struct TileSmem {
+  u64 seg[kWaves][kTileSeg];
+  u64 sorted[kTileSort];
+  uint32_t red[2][kWaves];
+  int cnt[kWaves];
+  u64 pick;
+};
 
 // Order-preserving 32-bit key of fp32 bits u (the upper half of a composite).
 __device__ __forceinline__ uint32_t key_of(uint32_t u) { return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u); }
@@ -497,331 +506,395 @@ __device__ __forceinline__ uint32_t wave_kth32(uint32_t v, bool ok, int k) {
   return p;
 }
 
-// A wave's candidate list: composites buf[0, count) in LDS (count wave-uniform) and the admission key (composites
-// whose key is below it cannot reach the row's top k). The row's waves share admission keys through a per-row word
-// (`shared`, an atomic maximum): any wave's k-th key bounds the row's k-th key from below.
-struct WaveList {
-  u64* buf;
-  int count;
-  uint32_t thr_key;
+// Block-wide reductions of wave-uniform values through two alternating rows of LDS slots: one barrier each (a row is
+// rewritten only after the barrier of the other row's use, which every reader of the first has passed). Every wave of
+// the block makes the same sequence of calls.
+struct BlockRed {
+  uint32_t (*slot)[kWaves];
+  int phase;
 
-  // Appends c where keep (positions from a ballot; no atomics).
+  template <typename Op>
+  __device__ __forceinline__ uint32_t all(uint32_t v, Op op) {
+    if (lane_id() == 0) slot[phase][wave_id()] = v;
+    __syncthreads();
+    uint32_t r = slot[phase][0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) r = op(r, slot[phase][i]);
+    phase ^= 1;
+    return r;
+  }
+  __device__ __forceinline__ uint32_t sum(uint32_t v) {
+    return all(v, [](uint32_t a, uint32_t b) { return a + b; });
+  }
+  __device__ __forceinline__ uint32_t max(uint32_t v) {
+    return all(v, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+  }
+  __device__ __forceinline__ uint32_t min(uint32_t v) {
+    return all(v, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+  }
+};
+
+// The exact k-th largest composite among the block's slots: slot(i, key, lo) for i < N fills in slot i of this lane
+// and says whether it is occupied; at least k slots are. A bitwise search for the k-th key from the common prefix of
+// the keys' range (a block count per candidate bit), then, among the composites with that key, for the lower word.
+// Every thread returns it.
+template <int N, typename F>
+__device__ u64 block_kth(const F& slot, int k, BlockRed& red) {
+  uint32_t kmx = 0, kmn = 0xffffffffu;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    uint32_t kk, lw;
+    if (slot(i, kk, lw)) {
+      kmx = kk > kmx ? kk : kmx;
+      kmn = kk < kmn ? kk : kmn;
+    }
+  }
+  kmx = red.max((uint32_t)wave_ext64<true>(kmx));
+  kmn = red.min((uint32_t)wave_ext64<false>(kmn));
+  uint32_t K = kmx;
+  if (kmx != kmn) {
+    const int top = 31 - __builtin_clz(kmx ^ kmn);
+    K = kmx & ~((2u << top) - 1u);
+    for (int b = top; b >= 0; --b) {
+      const uint32_t cand = K | (1u << b);
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        uint32_t kk, lw;
+        const bool ok = slot(i, kk, lw);
+        c += __popcll(__ballot(ok && kk >= cand));
+      }
+      if ((int)red.sum((uint32_t)c) >= k) K = cand;
+    }
+  }
+  int gt = 0, eq = 0;
+  uint32_t lmx = 0, lmn = 0xffffffffu;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    uint32_t kk, lw;
+    const bool ok = slot(i, kk, lw);
+    const bool e = ok && kk == K;
+    gt += __popcll(__ballot(ok && kk > K));
+    eq += __popcll(__ballot(e));
+    lmx = e && lw > lmx ? lw : lmx;
+    lmn = e && lw < lmn ? lw : lmn;
+  }
+  gt = (int)red.sum((uint32_t)gt);
+  eq = (int)red.sum((uint32_t)eq);
+  lmx = red.max((uint32_t)wave_ext64<true>(lmx));
+  lmn = red.min((uint32_t)wave_ext64<false>(lmn));
+  const int r = k - gt;  // 1 <= r <= eq
+  uint32_t L = lmn;
+  if (r < eq) {
+    const int top = 31 - __builtin_clz(lmx ^ lmn);
+    L = lmx & ~((2u << top) - 1u);
+    for (int b = top; b >= 0; --b) {
+      const uint32_t cand = L | (1u << b);
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        uint32_t kk, lw;
+        const bool ok = slot(i, kk, lw);
+        c += __popcll(__ballot(ok && kk == K && lw >= cand));
+      }
+      if ((int)red.sum((uint32_t)c) >= r) L = cand;
+    }
+  }
+  return ((u64)K << 32) | L;
+}
+
+// A workgroup's candidate list: wave w appends to its own LDS segment (positions from a ballot, no atomics). cnt may
+// pass kTileSeg within an overflowing batch, whose excess is not stored; the batch is then settled from registers.
+struct TileList {
+  u64* seg;
+  int cnt;  // wave-uniform
+
   __device__ __forceinline__ void push(u64 c, bool keep) {
     const u64 m = __ballot(keep);
-    if (keep) buf[count + lanes_below(m)] = c;
-    count += __popcll(m);
+    if (m) {
+      const int pos = cnt + lanes_below(m);
+      if (keep && pos < kTileSeg) seg[pos] = c;
+      cnt += __popcll(m);
+    }
   }
 
-  // Keeps exactly the k largest (when more are held) and raises thr_key to the k-th's key. The list is held in
-  // registers (8 per lane) for a bitwise search of the k-th key from the common prefix of the keys' range, then, only
-  // when equal keys straddle it, of the k-th lower word (~index) among them; then it is rewritten in place.
-  __device__ __forceinline__ void prune(int k) {
-    __syncthreads();  // one-wave workgroup: orders the list's LDS writes before these reads
-    if (count <= k) return;
-    u64 v[kWaveM];
-    bool ok[kWaveM];
-    uint32_t kmx = 0, kmn = 0xffffffffu;
-#pragma unroll
-    for (int i = 0; i < kWaveM; ++i) {
-      const int at = i * kWave + lane_id();
-      ok[i] = at < count;
-      v[i] = ok[i] ? buf[at] : 0ull;
-      const uint32_t kk = (uint32_t)(v[i] >> 32);
-      kmx = ok[i] && kk > kmx ? kk : kmx;
-      kmn = ok[i] && kk < kmn ? kk : kmn;
-    }
-    kmx = (uint32_t)wave_ext64<true>(kmx);
-    kmn = (uint32_t)wave_ext64<false>(kmn);
-    uint32_t K = kmx;
-    if (kmx != kmn) {
-      const int top = 31 - __builtin_clz(kmx ^ kmn);
-      K = kmx & ~((2u << top) - 1u);
-      for (int b = top; b >= 0; --b) {
-        const uint32_t cand = K | (1u << b);
-        int cnt = 0;
-#pragma unroll
-        for (int i = 0; i < kWaveM; ++i) cnt += __popcll(__ballot(ok[i] && (uint32_t)(v[i] >> 32) >= cand));
-        if (cnt >= k) K = cand;
-      }
-    }
-    int gt = 0, eq = 0;
-    uint32_t lmx = 0, lmn = 0xffffffffu;
-#pragma unroll
-    for (int i = 0; i < kWaveM; ++i) {
-      const uint32_t kk = (uint32_t)(v[i] >> 32), lw = (uint32_t)v[i];
-      const bool e = ok[i] && kk == K;
-      gt += __popcll(__ballot(ok[i] && kk > K));
-      eq += __popcll(__ballot(e));
-      lmx = e && lw > lmx ? lw : lmx;
-      lmn = e && lw < lmn ? lw : lmn;
-    }
-    lmx = (uint32_t)wave_ext64<true>(lmx);
-    lmn = (uint32_t)wave_ext64<false>(lmn);
-    const int r = k - gt;  // 1 <= r <= eq
-    uint32_t L = lmn;
-    if (r < eq) {
-      const int top = 31 - __builtin_clz(lmx ^ lmn);
-      L = lmx & ~((2u << top) - 1u);
-      for (int b = top; b >= 0; --b) {
-        const uint32_t cand = L | (1u << b);
-        int cnt = 0;
-#pragma unroll
-        for (int i = 0; i < kWaveM; ++i)
-          cnt += __popcll(__ballot(ok[i] && (uint32_t)(v[i] >> 32) == K && (uint32_t)v[i] >= cand));
-        if (cnt >= r) L = cand;
-      }
-    }
-    const u64 kth = ((u64)K << 32) | L;
-    __syncthreads();
-    count = 0;
-#pragma unroll
-    for (int i = 0; i < kWaveM; ++i) push(v[i], ok[i] && v[i] >= kth);
-    thr_key = K > thr_key ? K : thr_key;
-    __syncthreads();
-  }
-
-  // Writes the list (at most k <= 64 composites, one per lane) as a sorted output row or as a workspace list whose
-  // smallest composite comes first (0 first when fewer than k are held).
-  template <typename T>
-  __device__ __forceinline__ void finish(void* values, long long* indices, u64* wr, long long row, int k,
-                                         bool to_output) {
-    __syncthreads();
-    const int n = count;
+  // Keeps exactly the k largest of the list (which holds more, none dropped); returns the k-th.
+  __device__ u64 prune(BlockRed& red, int k) {
+    constexpr int PER = kTileSeg / kWave;
     const int lane = lane_id();
-    const u64 mine = lane < n ? buf[lane] : 0ull;
-    if (to_output) {
-      int rank = 0;
-      for (int j = 0; j < n; ++j) rank += readlane64(mine, j) > mine;
-      if (lane < n) {
+    const int n = cnt;
+    u64 c[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) c[i] = lane + i * kWave < n ? seg[lane + i * kWave] : 0ull;
+    const u64 kth = block_kth<PER>(
+        [&](int i, uint32_t& kk, uint32_t& lw) {
+          kk = (uint32_t)(c[i] >> 32);
+          lw = (uint32_t)c[i];
+          return lane + i * kWave < n;
+        },
+        k, red);
+    cnt = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) push(c[i], lane + i * kWave < n && c[i] >= kth);
+    return kth;
+  }
+
+  // After a batch of pushes onto a list whose waves held cnt0 each: a list longer than kTileKeep is pruned to its k
+  // largest. If a segment overflowed, the batch is dropped and pushed again in `steps` steps from `floor` (a lower
+  // bound of the k-th): step(s, floor, check) pushes step s's composites >= floor, calling check() after each group of
+  // at most 256 per wave, and check() prunes whenever the list passes kTileKeep, raising floor to the k-th. Returns
+  // the new k-th, or 0.
+  template <typename S>
+  __device__ u64 settle(BlockRed& red, int k, int cnt0, int steps, u64 floor, const S& step) {
+    const uint32_t v = red.sum((uint32_t)cnt + (cnt > kTileSeg ? (1u << 24) : 0u));
+    if (!(v >> 24)) return (int)(v & 0xffffffu) > kTileKeep ? prune(red, k) : 0ull;
+    cnt = cnt0;
+    u64 kth = 0;
+    auto check = [&] {
+      if ((int)red.sum((uint32_t)cnt) > kTileKeep) {
+        kth = prune(red, k);
+        floor = kth > floor ? kth : floor;
+      }
+    };
+    for (int st = 0; st < steps; ++st) step(st, floor, check);
+    return kth;
+  }
+};
+
+// Ranks the block's list (at most kTileSort composites) and writes its k largest, in order, as the output row (a
+// list holding at least k) or to the chunk list wr (0 past the end of a shorter list).
+template <typename T>
+__device__ void finish_list(TileSmem& s, const TileList& L, void* values, long long* indices, u64* wr,
+                            long long row, int k, bool to_output) {
+  const int wave = wave_id(), lane = lane_id(), t = threadIdx.x;
+  if (lane == 0) s.cnt[wave] = L.cnt;
+  __syncthreads();
+  int pre = 0, n = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int c = s.cnt[w];
+    pre += w < wave ? c : 0;
+    n += c;
+  }
+  for (int i = lane; i < L.cnt; i += kWave) s.sorted[pre + i] = L.seg[i];
+  __syncthreads();
+  if (t < n) {
+    const u64 mine = s.sorted[t];
+    int rank = 0;
+    int j = 0;
+    for (; j + 4 <= n; j += 4)
+      rank += (s.sorted[j] > mine) + (s.sorted[j + 1] > mine) + (s.sorted[j + 2] > mine) + (s.sorted[j + 3] > mine);
+    for (; j < n; ++j) rank += s.sorted[j] > mine;
+    if (rank < k) {
+      if (to_output) {
         if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + rank] = composite_bits(mine);
         else static_cast<uint16_t*>(values)[row * k + rank] = (uint16_t)(composite_bits(mine) >> 16);
         indices[row * k + rank] = composite_index(mine);
+      } else {
+        wr[rank] = mine;
       }
-      return;
     }
-    const u64 mn = wave_ext64<false>(lane < n ? mine : ~0ull);
-    const int at = n < k ? n : (int)__builtin_ctzll(__ballot(lane < n && mine == mn));
-    const u64 first_val = readlane64(mine, 0);
-    const u64 at_val = at < n ? readlane64(mine, at) : 0ull;
-    if (lane < k) wr[lane] = lane == 0 ? at_val : (lane == at ? first_val : (lane < n ? mine : 0ull));
   }
-};
-
-struct ListState {
-  int count;
-  uint32_t thr_key;
-};
-
-// The rare path: admits the row's elements [e0, e1) with key >= the admission key straight from memory, 64 at a time,
-// pruning whenever the next 64 might not fit. Elements of [e0, e0 + 64 w) whose offset modulo w is below `done` were
-// admitted already and are skipped. Out of line, so its code exists once.
-template <typename T>
-__device__ __noinline__ ListState admit_range(u64* buf, ListState st, const T* row, int e0, int e1, int w, int done,
-                                              int k) {
-  WaveList L;
-  L.buf = buf;
-  L.count = st.count;
-  L.thr_key = st.thr_key;
-  const int skip_end = e0 + kWave * w;
-  for (int base = e0; base < e1; base += kWave) {
-    if (L.count > kWaveCap - kWave) L.prune(k);
-    const int e = base + lane_id();
-    const bool ok = e < e1 && !(e < skip_end && (e - e0) % w < done);
-    uint32_t u = 0;
-    if (ok) {
-      if constexpr (sizeof(T) == 4) u = reinterpret_cast<const uint32_t*>(row)[e];
-      else u = (uint32_t)reinterpret_cast<const uint16_t*>(row)[e] << 16;
-    }
-    const uint32_t kk = key_of(u);
-    L.push(((u64)kk << 32) | (u64)(~(uint32_t)e), ok && kk >= L.thr_key);
-  }
-  return ListState{L.count, L.thr_key};
+  if (!to_output)
+    for (int j = n + t; j < k; j += kThreads) wr[j] = 0ull;
 }
 
-// A register block of one wave: lane t holds vectors v * 64 + t (v < NV) of elements [b0, b1) of a row, W each;
-// vector v covers the contiguous elements [b0 + 64 W v, b0 + 64 W (v + 1)).
+// A register tile: thread t holds vectors v * 256 + t (v < NV) of elements [b0, b1) of a row, W each. fp32 registers
+// are turned into keys in place (prepare); bf16 keys are formed from the packed halves when used.
 template <typename T, bool VEC>
-struct WaveBlock {
+struct Tile {
   static constexpr int W = Fmt<T>::W;
-  static constexpr int NV = kWaveE / W;
+  static constexpr int NV = kTileE / W;
   u32x4 r[NV];
   int b0, b1;
+  int lane0;  // b0 + threadIdx.x * W, the first element of vector 0 (kept opaque with the registers)
 
-  __device__ __forceinline__ int first(int v) const { return b0 + (v * kWave + lane_id()) * W; }
+  __device__ __forceinline__ int first(int v) const { return lane0 + v * kThreads * W; }
   __device__ __forceinline__ bool valid(int v, int j) const { return VEC ? first(v) < b1 : first(v) + j < b1; }
   __device__ __forceinline__ uint32_t key(int v, int j) const {
-    uint32_t u;
     if constexpr (sizeof(T) == 4) {
-      u = r[v][j];
+      return r[v][j];
     } else {
       const uint32_t w = r[v][j >> 1];
-      u = (j & 1) ? (w & 0xffff0000u) : (w << 16);
+      return key_of((j & 1) ? (w & 0xffff0000u) : (w << 16));
     }
-    return key_of(u);
   }
-  // Loads vector v of the block [nb0, nb1) (an in-range duplicate when nb0 >= nb1: loaded, never used).
-  __device__ __forceinline__ void load_vec(const T* row, int v, int nb0, int nb1) {
-    const int e0 = nb0 + (v * kWave + lane_id()) * W;
-    if constexpr (VEC) {
-      const int last = nb1 - W;
-      r[v] = load16<true>(row + (e0 < nb1 ? e0 : (last > 0 ? last : 0)), 0);
-    } else {
-      uint32_t u[W];
+  __device__ __forceinline__ u64 comp(int v, int j) const {
+    return ((u64)key(v, j) << 32) | (u64)(~(uint32_t)(first(v) + j));
+  }
+
+  __device__ __forceinline__ void load(const T* row) {
+    lane0 = b0 + (int)threadIdx.x * W;
 #pragma unroll
-      for (int j = 0; j < W; ++j) {
-        const int e = e0 + j;
-        if constexpr (sizeof(T) == 4) u[j] = e < nb1 ? reinterpret_cast<const uint32_t*>(row)[e] : 0u;
-        else u[j] = e < nb1 ? (uint32_t)reinterpret_cast<const uint16_t*>(row)[e] : 0u;
+    for (int v = 0; v < NV; ++v) {
+      const int e0 = first(v);
+      if constexpr (VEC) {
+        r[v] = load16<true>(row + (e0 < b1 ? e0 : b1 - W), 0);  // an in-range duplicate past the end, never used
+      } else {
+        uint32_t u[W];
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+          const int e = e0 + j;
+          if constexpr (sizeof(T) == 4) u[j] = e < b1 ? reinterpret_cast<const uint32_t*>(row)[e] : 0u;
+          else u[j] = e < b1 ? (uint32_t)reinterpret_cast<const uint16_t*>(row)[e] : 0u;
+        }
+        if constexpr (sizeof(T) == 4) r[v] = (u32x4){u[0], u[1], u[2], u[3]};
+        else r[v] = (u32x4){u[0] | (u[1] << 16), u[2] | (u[3] << 16), u[4] | (u[5] << 16), u[6] | (u[7] << 16)};
       }
-      if constexpr (sizeof(T) == 4) r[v] = (u32x4){u[0], u[1], u[2], u[3]};
-      else r[v] = (u32x4){u[0] | (u[1] << 16), u[2] | (u[3] << 16), u[4] | (u[5] << 16), u[6] | (u[7] << 16)};
     }
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int j = 0; j < W; ++j) r[v][j] = key_of(r[v][j]);
+    }
+    opaque();
+  }
+
+  // Pushes the elements of vector v, held in r[0], with composites >= floor, calling check() after every 4 per lane;
+  // then moves the later vectors down one place (the overflow path walks the tile in order this way, so that the
+  // registers are indexed statically).
+  template <typename Lst, typename C>
+  __device__ __forceinline__ void push_first(Lst& L, int v, u64 floor, const C& check) {
+    const int e0 = first(v);
+#pragma unroll
+    for (int g = 0; g < W; g += 4) {
+#pragma unroll
+      for (int j = g; j < g + 4; ++j) {
+        const u64 c = ((u64)key(0, j) << 32) | (u64)(~(uint32_t)(e0 + j));
+        L.push(c, (VEC ? e0 < b1 : e0 + j < b1) && c >= floor);
+      }
+      check();
+    }
+#pragma unroll
+    for (int i = 0; i + 1 < NV; ++i) r[i] = r[i + 1];
+  }
+
+  // Makes the registers opaque to the compiler, so that it keeps the tile as 16-byte register quads instead of
+  // widening every key into the upper half of a 64-bit composite ahead of its use.
+  __device__ __forceinline__ void opaque() {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) asm volatile("" : "+v"(r[v]));
+    asm volatile("" : "+v"(lane0));
   }
 };
 
-__device__ __forceinline__ uint32_t load_shared_key(const unsigned* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void publish_key(unsigned* p, uint32_t key) {
-  if (lane_id() == 0) __hip_atomic_fetch_max(p, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// k <= 64: one 64-lane workgroup (one wave) per (chunk, row). The wave streams its chunk in register blocks of 2048
-// elements through a single register set: as soon as a 16-byte slice has been filtered, its registers load the same
-// slice of the next block, so the next block is in flight while the rest of this one is filtered. Admission compares
-// 32-bit keys against the admission key -- the largest of the wave's own bound, the first block's lane-maxima seed
-// (the k-th largest lane maximum has k distinct elements at or above it) and the row's shared word, which every wave
-// of the row raises to its k-th key -- and builds composites only for admitted elements. `shared` (the caller's
-// per-row counter, zero on entry) is left at the row's bound; the merge (or the single wave of an unsplit row)
-// zeroes it.
+// k <= 64: one 256-thread workgroup per (chunk, row). The chunk is taken in register tiles of 16384 elements, all of a
+// tile's loads in flight at once. Per tile: each wave takes the ceil(k / 4)-th largest of its 64 lane maxima, which
+// has that many distinct elements at or above it, and the smallest of the four waves' keys has at least k; with the
+// k-th of the earlier tiles it is the admission key. Admitted elements (about k * 1.5 per tile on continuous data)
+// are appended to the waves' LDS segments; a list beyond kTileKeep is pruned to k, and an overflowing tile (ties, or
+// adversarial orders) is pushed again in index order with a prune whenever the list passes kTileKeep. The list is then rank-sorted:
+// written out for an unsplit row, or as the chunk's k largest, descending, for the merge.
 template <typename T, bool VEC>
-__global__ void __launch_bounds__(kWave)
-    topk_wave(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
-              u64* __restrict__ work, unsigned* __restrict__ shared, long long cols, long long chunk, int nchunks,
-              int k) {
-  __shared__ u64 list[kWaveCap];
+__global__ void __launch_bounds__(kThreads)
+    topk_tile(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
+              u64* __restrict__ work, long long cols, long long chunk, int nchunks, int k) {
+  __shared__ TileSmem s;
   const long long row = blockIdx.y;
   const int part = blockIdx.x;
   const int begin = (int)((long long)part * chunk);
   const int end = (int)(begin + chunk < cols ? begin + chunk : cols);
   const T* xr = x + row * cols;
-  unsigned* row_key = shared + row;
-  WaveList L;
-  L.buf = list;
-  L.count = 0;
-  L.thr_key = 0u;
-  using B = WaveBlock<T, VEC>;
-  B blk;
-  blk.b0 = begin;
-  blk.b1 = end - begin > kWaveSub ? begin + kWaveSub : end;
+  BlockRed red{s.red, 0};
+  TileList L{s.seg[wave_id()], 0};
+  uint32_t thr = 0;
+  const int kw = (k + kWaves - 1) / kWaves;
+  using TL = Tile<T, VEC>;
+  constexpr int TE = kThreads * kTileE;
+  for (int t0 = begin; t0 < end; t0 += TE) {
+    TL tile;
+    tile.b0 = t0;
+    tile.b1 = end - t0 > TE ? t0 + TE : end;
+    tile.load(xr);
+    uint32_t m = 0;
+    bool has = false;
 #pragma unroll
-  for (int v = 0; v < B::NV; ++v) blk.load_vec(xr, v, blk.b0, blk.b1);
-  bool seeded = false;
-  uint32_t row_bound = load_shared_key(row_key);
-  while (true) {
-    if (!seeded) {
-      uint32_t m = 0;
-      bool has = false;
+    for (int v = 0; v < TL::NV; ++v)
 #pragma unroll
-      for (int v = 0; v < B::NV; ++v)
+      for (int j = 0; j < TL::W; ++j)
+        if (tile.valid(v, j)) {
+          const uint32_t kk = tile.key(v, j);
+          m = kk > m ? kk : m;
+          has = true;
+        }
+    const uint32_t tw = __popcll(__ballot(has)) >= kw ? wave_kth32(m, has, kw) : 0u;
+    const uint32_t tb = red.min(tw);
+    thr = tb > thr ? tb : thr;
+    const int cnt0 = L.cnt;
+    tile.opaque();
 #pragma unroll
-        for (int j = 0; j < B::W; ++j)
-          if (blk.valid(v, j)) {
-            const uint32_t kk = blk.key(v, j);
-            m = kk > m ? kk : m;
-            has = true;
-          }
-      if (__popcll(__ballot(has)) >= k) {
-        const uint32_t seed = wave_kth32(m, has, k);
-        L.thr_key = seed > L.thr_key ? seed : L.thr_key;
-        publish_key(row_key, seed);
-        seeded = true;
-      }
-    }
-    L.thr_key = row_bound > L.thr_key ? row_bound : L.thr_key;
-    row_bound = load_shared_key(row_key);  // used at the next block (in flight meanwhile)
-    const uint32_t thr = L.thr_key;
-    const int nb0 = blk.b1, nb1 = end - nb0 > kWaveSub ? nb0 + kWaveSub : end;
-    bool slow = false;
+    for (int v = 0; v < TL::NV; ++v)
 #pragma unroll
-    for (int v = 0; v < B::NV; ++v) {
-      // four elements per lane (256 per wave) at a time, so that a group always fits when its check passes
+      for (int g = 0; g < TL::W; g += 4) {
+        bool any = false;
 #pragma unroll
-      for (int g = 0; g < B::W; g += 4) {
-        if (!slow) {
-          if (L.count > kWaveCap - 4 * kWave) {
-            // the group might not fit: admit the rest of the block from memory, pruning as it goes
-            const ListState st = admit_range<T>(list, ListState{L.count, L.thr_key}, xr, blk.b0 + v * kWave * B::W,
-                                                blk.b1, B::W, g, k);
-            L.count = st.count;
-            L.thr_key = st.thr_key;
-            slow = true;
-          } else {
-            bool any = false;
+        for (int j = g; j < g + 4; ++j) any |= tile.valid(v, j) && tile.key(v, j) >= thr;
+        if (__ballot(any)) {
 #pragma unroll
-            for (int j = g; j < g + 4; ++j) any |= blk.valid(v, j) && blk.key(v, j) >= thr;
-            if (__ballot(any)) {
-#pragma unroll
-              for (int j = g; j < g + 4; ++j) {
-                const uint32_t kk = blk.key(v, j);
-                L.push(((u64)kk << 32) | (u64)(~(uint32_t)(blk.first(v) + j)), blk.valid(v, j) && kk >= thr);
-              }
-            }
-          }
+          for (int j = g; j < g + 4; ++j) L.push(tile.comp(v, j), tile.valid(v, j) && tile.key(v, j) >= thr);
         }
       }
-      blk.load_vec(xr, v, nb0, nb1);
-    }
-    if (L.count > kWavePruneAt) {
-      L.prune(k);
-      publish_key(row_key, L.thr_key);
-    }
-    if (nb0 >= end) break;
-    blk.b0 = nb0;
-    blk.b1 = nb1;
+    const u64 kth = L.settle(red, k, cnt0, TL::NV, (u64)thr << 32,
+                             [&](int v, const u64& floor, const auto& check) { tile.push_first(L, v, floor, check); });
+    const uint32_t kk = (uint32_t)(kth >> 32);
+    thr = kk > thr ? kk : thr;
   }
-  L.prune(k);
-  if (nchunks == 1 && lane_id() == 0)  // the row's only wave: leave the counter zero
-    __hip_atomic_store(row_key, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  L.finish<T>(values, indices, work + (row * nchunks + part) * (long long)k, row, k, nchunks == 1);
+  finish_list<T>(s, L, values, indices, work + (row * nchunks + part) * (long long)k, row, k, nchunks == 1);
 }
 
-// k <= 64 merge: one wave per split row streams the row's nchunks lists (k composites each, smallest first) through
-// its list from the largest list minimum, writes the sorted row and zeroes the row's shared word.
+// k <= 64 merge, one 256-thread workgroup per split row. Every chunk list holds its chunk's k largest, descending, so
+// the first h = ceil(k / nchunks) entries of the lists give nchunks * h >= k distinct composites: the k-th largest of
+// these heads bounds the row's k-th from below and, the row's top k being spread over the chunks, admits little
+// beyond the answer. The lists are then streamed through the list from that floor, settled as in topk_tile.
 template <typename T>
-__global__ void __launch_bounds__(kWave)
-    topk_merge_wave(void* __restrict__ values, long long* __restrict__ indices, const u64* __restrict__ work,
-                    unsigned* __restrict__ shared, int nchunks, int k) {
-  __shared__ u64 list[kWaveCap];
+__global__ void __launch_bounds__(kThreads)
+    topk_tile_merge(void* __restrict__ values, long long* __restrict__ indices, const u64* __restrict__ work,
+                    int nchunks, int k) {
+  __shared__ TileSmem s;
   const long long row = blockIdx.x;
   const u64* wr = work + row * (long long)nchunks * k;
-  u64 fl = 0;
-  for (int c = lane_id(); c < nchunks; c += kWave) {
-    const u64 v = wr[(long long)c * k];
-    fl = v > fl ? v : fl;
-  }
-  fl = wave_ext64<true>(fl);
-  const u64 floor = fl > 1 ? fl : 1;
-  WaveList L;
-  L.buf = list;
-  L.count = 0;
-  L.thr_key = shared[row];  // the row's bound: every top-k key is at least this
-  const int total = nchunks * k;
-  for (int base = 0; base < total; base += 4 * kWave) {
-    u64 c[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = base + j * kWave + lane_id();
-      c[j] = i < total ? wr[i] : 0ull;
+  const int t = threadIdx.x;
+  BlockRed red{s.red, 0};
+  TileList L{s.seg[wave_id()], 0};
+  const int h = (k + nchunks - 1) / nchunks;
+  const int nh = h * nchunks;
+  u64 floor = 1;
+  if (nh <= kTileSort) {
+    const u64 hv = t < nh ? wr[(long long)(t / h) * k + t % h] : 0ull;
+    s.sorted[t] = hv;
+    const int real = (int)red.sum((uint32_t)__popcll(__ballot(hv != 0)));
+    if (real >= k) {
+      if (hv != 0) {
+        int rank = 0;
+        for (int j = 0; j < nh; ++j) rank += s.sorted[j] > hv;
+        if (rank == k - 1) s.pick = hv;
+      }
+      __syncthreads();
+      floor = s.pick;
     }
-    if (L.count > kWaveCap - 4 * kWave) L.prune(k);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) L.push(c[j], c[j] >= floor && (uint32_t)(c[j] >> 32) >= L.thr_key);
   }
-  L.prune(k);
-  __syncthreads();
-  if (lane_id() == 0) shared[row] = 0u;
-  L.finish<T>(values, indices, nullptr, row, k, true);
+  constexpr int PER = 8;
+  const int total = nchunks * k;
+  for (int base = 0; base < total; base += kThreads * PER) {
+    u64 c[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int at = base + i * kThreads + t;
+      c[i] = at < total ? wr[at] : 0ull;
+    }
+    const int cnt0 = L.cnt;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) L.push(c[i], c[i] >= floor);
+    const u64 kth = L.settle(red, k, cnt0, PER, floor, [&](int, const u64& f, const auto& check) {
+      L.push(c[0], c[0] >= f);
+      check();
+#pragma unroll
+      for (int i = 0; i + 1 < PER; ++i) c[i] = c[i + 1];
+    });
+    floor = kth > floor ? kth : floor;
+  }
+  finish_list<T>(s, L, values, indices, nullptr, row, k, true);
 }
 
 // ---- merge kernel ----------------------------------------------------------------------------------------------------
@@ -882,13 +955,13 @@ int lane_elems() {
 }
 
 template <typename T, bool VEC>
-int launch_chunks(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
-                  long long cols, long long chunk, int nchunks, int k, hipStream_t stream) {
+int launch_chunks(const void* x, void* values, void* indices, void* work, long long rows, long long cols,
+                  long long chunk, int nchunks, int k, hipStream_t stream) {
   const dim3 grid((unsigned)nchunks, (unsigned)rows);
   const int e = VEC ? lane_elems() : 16;
   if (k <= kSeedMaxK)
-    hipLaunchKernelGGL((topk_wave<T, VEC>), grid, dim3(kWave), 0, stream, (const T*)x, values, (long long*)indices,
-                       (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k);
+    hipLaunchKernelGGL((topk_tile<T, VEC>), grid, dim3(kThreads), 0, stream, (const T*)x, values, (long long*)indices,
+                       (u64*)work, cols, chunk, nchunks, k);
   else if (e == 16)
     hipLaunchKernelGGL((topk_chunks<T, VEC, 16>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
                        (long long*)indices, (u64*)work, cols, chunk, nchunks, k);
@@ -900,8 +973,8 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, void* 
                        (long long*)indices, (u64*)work, cols, chunk, nchunks, k);
   if (nchunks > 1) {
     if (k <= kSeedMaxK)
-      hipLaunchKernelGGL((topk_merge_wave<T>), dim3((unsigned)rows), dim3(kWave), 0, stream, values,
-                         (long long*)indices, (const u64*)work, (unsigned*)counters, nchunks, k);
+      hipLaunchKernelGGL((topk_tile_merge<T>), dim3((unsigned)rows), dim3(kThreads), 0, stream, values,
+                         (long long*)indices, (const u64*)work, nchunks, k);
     else
       hipLaunchKernelGGL((topk_merge<T>), dim3((unsigned)rows), dim3(kThreads), 0, stream, values,
                          (long long*)indices, (const u64*)work, nchunks, k);
@@ -911,37 +984,36 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, void* 
 
 }  // namespace
 
-// topk/kernel.cu:520 `plan`: the chunk length (columns per workgroup) for a rows x cols launch, chosen so the grid of
-// chunks fills the GPU's resident slots once (CUs x resident one-wave workgroups of the k <= 64 kernel per CU), never
-// shorter than max(min_chunk, 2048); a multiple of 8 when a row is split. The caller's min_chunk carries the k
-// dependence (larger k, longer chunks: fewer lists of k to merge). `threads` and `depth` are the reference's CUDA
-// tuning knobs, accepted and not used.
+// topk/kernel.cu:520 `plan`: the chunk length (columns per workgroup) for a rows x cols launch. The grid of chunks
+// fills the GPU's resident workgroup slots (CUs x resident workgroups of the k <= 64 kernel per CU) about once; a chunk
+// longer than one register tile (16384 elements) is rounded up to whole tiles; never shorter than min_chunk, which
+// carries the caller's k dependence (longer chunks for larger k: fewer lists of k to merge); a multiple of 8 when a
+// row is split. `threads` and `depth` are the reference's CUDA tuning knobs, accepted and not used.
 extern "C" long long plan(long long rows, long long cols, int dtype, int threads, int depth, int min_chunk) {
   (void)threads;
   (void)depth;
+  (void)dtype;
   if (rows <= 0 || cols <= 0) return cols > 0 ? cols : 1;
-  static int occ[2] = {0, 0};
-  const int d = dtype == 1 ? 1 : 0;
+  static int occ = 0;
   int per_cu = rw_host::tune_get(kTuneBlocksPerCu);
   if (per_cu <= 0) {
-    if (occ[d] <= 0) {
+    if (occ <= 0) {
       int n = 0;
-      const hipError_t e = d ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_wave<uint16_t, true>, kWave, 0)
-                             : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_wave<float, true>, kWave, 0);
-      if (e != hipSuccess || n <= 0) {
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_tile<float, true>, kThreads, 0) != hipSuccess ||
+          n <= 0) {
         (void)hipGetLastError();
-        n = 8;
+        n = 4;
       }
-      occ[d] = n;
+      occ = n;
     }
-    per_cu = occ[d];
+    per_cu = occ;
   }
-  long long len = min_chunk > kWaveSub ? min_chunk : kWaveSub;
-  const long long slots = (long long)rw_host::device_cus() * per_cu;
-  long long per_row = slots / rows;
+  const long long tile = (long long)kThreads * kTileE;
+  long long per_row = (long long)rw_host::device_cus() * per_cu / rows;
   if (per_row < 1) per_row = 1;
-  const long long fill = (cols + per_row - 1) / per_row;
-  if (fill > len) len = fill;
+  long long len = (cols + per_row - 1) / per_row;
+  if (len > tile) len = (len + tile - 1) / tile * tile;
+  if (len < min_chunk) len = min_chunk;
   if (len >= cols) return cols;
   return (len + 7) / 8 * 8;
 }
@@ -954,6 +1026,7 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
 // nchunks * k > INT_MAX / 2, threads not 128, 256 or 512, depth not 2, 4 or 8, or a dtype other than 0 and 1.
 extern "C" int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
                       long long cols, int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream) {
+  (void)counters;
   if (rows <= 0 || k <= 0) return rw_host::kOk;
   if (k > cols || k > kMaxK || cols > INT_MAX / 2 || rows > 65535 || chunk <= 0) return rw_host::kInvalid;
   const long long nchunks = (cols + chunk - 1) / chunk;
@@ -962,13 +1035,13 @@ extern "C" int launch(const void* x, void* values, void* indices, void* work, vo
     return rw_host::kInvalid;
   if (dtype == 0) {
     if (cols % 4 == 0 && rw_host::aligned16(x))
-      return launch_chunks<float, true>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
-    return launch_chunks<float, false>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
+      return launch_chunks<float, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
+    return launch_chunks<float, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
   }
   if (dtype == 1) {
     if (cols % 8 == 0 && (chunk % 8 == 0 || nchunks == 1) && rw_host::aligned16(x))
-      return launch_chunks<uint16_t, true>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
-    return launch_chunks<uint16_t, false>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
+      return launch_chunks<uint16_t, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
+    return launch_chunks<uint16_t, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
   }
   return rw_host::kInvalid;
 }
