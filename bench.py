@@ -1,21 +1,30 @@
 """Benchmark of the row-wise kernels on one MI355X: per-kernel us/call and achieved HBM GB/s against the 8 TB/s peak.
 
-    python bench.py [--steps K] [--warmup W] [--workload NAME] [--all] [--warm] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cold] [--no-cpu]
+    python bench.py --copy-calibration          # plain kernels of known traffic, for the counter scaling
+    python bench.py --traffic-from DIR          # turn FETCH_SIZE / WRITE_SIZE counter runs into profiles/traffic.json
 
-A step is one launch of the op over its whole workload with the inputs already resident in HBM. Before every timed
-step the 256 MB Infinity Cache and the L2s are flushed by reading a 1 GiB buffer (reads leave no dirty lines, so the
-timed launch pays for no write-back of the flush), then the launch is bracketed by HIP events recorded on the stream it
-runs on (torch's current stream, which the C-ABI is handed). The K durations give the mean (reported as ms_per_step
-and used for `value`), median, p10 and p90. `value` = algorithmic bytes / mean duration: every input element read once
-and every output element written once (workloads.algorithmic_bytes).
+A step is one launch of the op over its whole workload with the inputs already resident in HBM. Each workload is
+instantiated R times (R copies of its inputs and outputs, more bytes in all than the 256 MB Infinity Cache and the L2s
+hold), and the K timed launches cycle through the copies back to back, bracketed by one pair of HIP events recorded on
+the stream the launches run on (torch's current stream, which the C-ABI is handed): a launch never finds its data in
+a cache, and the per-launch mean is the kernels' own duration plus the gaps between dependent launches -- the figure
+the rocprofv3 kernel trace of the same command reports. `value` = algorithmic bytes / that mean: every input element
+read once and every output element written once (workloads.algorithmic_bytes).
+
+--cold (the default; --no-cold skips it) also times single launches one at a time, each after reading a 1 GiB buffer
+(which evicts the caches without leaving dirty lines) and between its own pair of events: that adds the dispatch
+latency of an isolated launch (a few microseconds) to every figure.
 
 The JSON line is printed for the headline workload (RMSNorm bf16 [16384, 4096] with weight); `per_workload` carries
-the other named workloads measured the same way (--all, the default, or just the headline with --workload). The CPU
-baseline times the reference's PyTorch path for the headline on this host's cores (oracle/torch_paths, test
-infrastructure used here only as the timed baseline) on a bounded sample of rows.
+every named workload measured the same way. The CPU baseline times the reference's PyTorch path for the headline on
+this host's cores (oracle/torch_paths, test infrastructure used here only as the timed baseline) on a bounded sample of
+rows.
 """
 
 import argparse
+import glob
+import csv
 import json
 import os
 import sys
@@ -28,6 +37,14 @@ METRIC = "per-kernel µs/call + achieved HBM GB/s (% of MI355X peak) at named sh
 PEAK_GBS = 8000.0
 HEADLINE = "rmsnorm_16384x4096"
 FLUSH_BYTES = 1 << 30
+ROTATE_BYTES = 1280 << 20  # the copies of one workload together (at least 4): five times the Infinity Cache
+COPY_BYTES = 256 << 20     # the calibration kernels: 256 MiB read by one, 256 MiB written by the other
+TRAFFIC_PATH = os.path.join(ROOT, "profiles", "traffic.json")
+# the kernels whose counters give each workload's traffic: a name fragment; the dispatches of one launch that contain
+# it are summed (the whole launch for the two-kernel paths)
+KERNELS = {"rmsnorm_16384x4096": "rmsnorm_rows", "softmax_4096x4096": "softmax_rows",
+           "softmax_64x262144": "softmax_split", "rope_4x4096_32q_8kv_128": "rope_vec",
+           "topk_128x128256_k50": "topk_tile"}
 
 
 def parse():
@@ -36,15 +53,21 @@ def parse():
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default=None, help="measure only this workload (default: all)")
-    p.add_argument("--all", action="store_true", help="measure every named workload (the default)")
-    p.add_argument("--warm", action="store_true", help="also time back-to-back launches without flushing")
+    p.add_argument("--k", type=int, default=None, help="top-k: measure only this k (default: 1, 50 and 1024)")
+    p.add_argument("--no-cold", action="store_true", help="skip the flushed single-launch timing")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only launch a 256 MiB read-only and a 256 MiB write-only kernel --steps times (for the "
+                        "counter scaling)")
+    p.add_argument("--traffic-from", default=None,
+                   help="directory with rocprofv3 counter CSVs (fetch/ and write/ runs of this script and of "
+                        "--copy-calibration); writes profiles/traffic.json")
     return p.parse_args()
 
 
 class Case:
-    """One workload bound to device tensors: `launch()` runs the op once; `kernel` names the dominant kernel."""
+    """One workload bound to R device copies: `launch(i)` runs the op once on copy i % R."""
 
     def __init__(self, pkg, name, dev, k=None):
         import torch
@@ -52,89 +75,116 @@ class Case:
         w = pkg.workloads
         self.bytes = w.algorithmic_bytes(name, k or 50)
         inp = w.WORKLOADS[name]()
+        stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
         if name.startswith("softmax"):
-            x = inp["x"].to(dev)
-            y = torch.empty_like(x)
             lib = pkg.candidate("softmax")._lib
-            rows, cols = x.shape
-            self.launch = lambda: lib.launch(x.data_ptr(), y.data_ptr(), rows, cols, 0, 256, 1024,
-                                             torch.cuda.current_stream().cuda_stream)
+            rows, cols = inp["x"].shape
             self.dtype = "fp32"
+
+            def make():
+                x = inp["x"].to(dev)
+                y = torch.empty_like(x)
+                return lambda: lib.launch(x.data_ptr(), y.data_ptr(), rows, cols, 0, 256, 1024, stream())
+            footprint = 2 * inp["x"].numel() * 4
         elif name.startswith("rmsnorm"):
-            x, wt = inp["x"].to(dev), inp["weight"].to(dev)
-            y = torch.empty_like(x)
             lib = pkg.candidate("rmsnorm")._lib
-            rows, cols = x.shape
+            rows, cols = inp["x"].shape
             eps = inp["eps"]
-            self.launch = lambda: lib.rmsnorm_launch_weighted(x.data_ptr(), wt.data_ptr(), y.data_ptr(), rows, cols, 1,
-                                                              eps, 256, torch.cuda.current_stream().cuda_stream)
+            wt = inp["weight"].to(dev)
             self.dtype = "bf16"
+
+            def make():
+                x = inp["x"].to(dev)
+                y = torch.empty_like(x)
+                return lambda: lib.rmsnorm_launch_weighted(x.data_ptr(), wt.data_ptr(), y.data_ptr(), rows, cols, 1,
+                                                           eps, 256, stream())
+            footprint = 2 * inp["x"].numel() * 2
         elif name.startswith("rope"):
-            q, kk = inp["q"].to(dev), inp["k"].to(dev)
-            pos, inv = inp["position_ids"].to(dev), inp["inv_freq"].to(dev)
             lib = pkg.candidate("rope")._lib
-            B, S, Hq, D = q.shape
-            # in place: every call rotates the same buffers again (the traffic is the same every time)
-            self.launch = lambda: lib.rope_launch_freq(q.data_ptr(), kk.data_ptr(), pos.data_ptr(), inv.data_ptr(),
-                                                       q.data_ptr(), kk.data_ptr(), B * S, Hq, kk.shape[2], D, 1,
-                                                       torch.cuda.current_stream().cuda_stream)
+            B, S, Hq, D = inp["q"].shape
+            Hk = inp["k"].shape[2]
+            pos, inv = inp["position_ids"].to(dev), inp["inv_freq"].to(dev)
             self.dtype = "bf16"
+
+            def make():
+                # in place: every call rotates the same buffers again (the traffic is the same every time)
+                q, kk = inp["q"].to(dev), inp["k"].to(dev)
+                return lambda: lib.rope_launch_freq(q.data_ptr(), kk.data_ptr(), pos.data_ptr(), inv.data_ptr(),
+                                                    q.data_ptr(), kk.data_ptr(), B * S, Hq, Hk, D, 1, stream())
+            footprint = 2 * (inp["q"].numel() + inp["k"].numel()) * 2
         elif name.startswith("topk"):
             cand = pkg.candidate("topk")
-            x = inp["x"].to(dev)
-            rows, cols = x.shape
-            _, chunk, work_ptr, counters_ptr, _, _ = cand._plan(x, rows, cols, 0, k)
-            vals = torch.empty(rows, k, device=dev)
-            idx = torch.empty(rows, k, dtype=torch.int64, device=dev)
             lib = cand._lib
-            self.launch = lambda: lib.launch(x.data_ptr(), vals.data_ptr(), idx.data_ptr(), work_ptr, counters_ptr,
-                                             rows, cols, k, 0, cand._THREADS, cand._DEPTH, chunk,
-                                             torch.cuda.current_stream().cuda_stream)
+            rows, cols = inp["x"].shape
+            chunk = cand._plan(inp["x"].to(dev), rows, cols, 0, k)[1]
+            nchunks = -(-cols // chunk)
             self.dtype = "fp32"
+
+            def make():
+                x = inp["x"].to(dev)
+                vals = torch.empty(rows, k, device=dev)
+                idx = torch.empty(rows, k, dtype=torch.int64, device=dev)
+                work = torch.empty(max(1, rows * nchunks * k), dtype=torch.int64, device=dev)
+                counters = torch.zeros(rows, dtype=torch.int32, device=dev)
+                keep = (x, vals, idx, work, counters)
+                return lambda: lib.launch(keep[0].data_ptr(), vals.data_ptr(), idx.data_ptr(), work.data_ptr(),
+                                          counters.data_ptr(), rows, cols, k, 0, cand._THREADS, cand._DEPTH, chunk,
+                                          stream())
+            footprint = inp["x"].numel() * 4
         else:
             raise KeyError(name)
+        self.copies = max(4, -(-ROTATE_BYTES // footprint))
+        self.launchers = [make() for _ in range(self.copies)]
         self.inputs = inp
+
+    def launch(self, i=0):
+        return self.launchers[i % self.copies]()
 
     @property
     def label(self):
         return self.name if self.k is None else f"{self.name}_k{self.k}"
 
 
-def time_case(case, steps, warmup, flush, warm):
+def check(err, label):
+    if err:
+        raise RuntimeError(f"{label}: launch returned {err}")
+
+
+def time_rotating(case, steps, warmup):
+    """K launches back to back over the rotating copies between one pair of events: the mean per launch."""
     import torch
-    for _ in range(warmup):
-        assert case.launch() == 0
+    for i in range(warmup):
+        check(case.launch(i), case.label)
     torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record()
+    for i in range(steps):
+        check(case.launch(warmup + i), case.label)
+    b.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    us = a.elapsed_time(b) * 1e3 / steps
+    return {"us_mean": us, "bytes": case.bytes, "wall_s": wall, "copies": case.copies,
+            "gbs": case.bytes / (us * 1e-6) / 1e9, "pct_peak": 100.0 * case.bytes / (us * 1e-6) / 1e9 / PEAK_GBS}
+
+
+def time_cold(case, steps, flush):
+    """Single launches, each after a cache-evicting read and between its own events: median and p10/p90."""
+    import torch
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for i in range(steps):
         flush()
         starts[i].record()
-        err = case.launch()
+        err = case.launch(i)
         ends[i].record()
-        if err:
-            raise RuntimeError(f"{case.label}: launch returned {err}")
+        check(err, case.label)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     us = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))
-    mean = sum(us) / len(us)
-    out = {"us_mean": mean, "us_median": us[len(us) // 2], "us_p10": us[len(us) // 10],
-           "us_p90": us[(9 * len(us)) // 10], "bytes": case.bytes, "wall_s": wall}
-    out["gbs"] = case.bytes / (mean * 1e-6) / 1e9
-    out["pct_peak"] = 100.0 * out["gbs"] / PEAK_GBS
-    if warm:
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(steps):
-            case.launch()
-        b.record()
-        torch.cuda.synchronize()
-        wus = a.elapsed_time(b) * 1e3 / steps
-        out["warm_us"] = wus
-        out["warm_gbs"] = case.bytes / (wus * 1e-6) / 1e9
-    return out
+    return {"cold_us_median": us[len(us) // 2], "cold_us_p10": us[len(us) // 10],
+            "cold_us_p90": us[(9 * len(us)) // 10]}
 
 
 def cpu_baseline(pkg, seconds):
@@ -159,30 +209,116 @@ def cpu_baseline(pkg, seconds):
     med = times[len(times) // 2]
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{rows} of 16384 rows (x[{rows}, 4096] bf16 + weight), median of {len(times)} calls of the "
-                      f"torch path after 2 warm-ups, {med * 1e3:.2f} ms/call; cpu_count={os.cpu_count()}"}
+                      f"torch path after 2 warm-ups, {med * 1e3:.2f} ms/call; cpu_count={os.cpu_count()}, "
+                      f"cpu={cpu_model()}"}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def roofline_entry(res, label):
     traffic = None
-    path = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(path):
-        with open(path) as f:
+    if os.path.exists(TRAFFIC_PATH):
+        with open(TRAFFIC_PATH) as f:
             traffic = json.load(f).get(label, {}).get("bytes_per_launch")
     return {"bound": "hbm", "achieved": round(res["gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
             "frac": round(res["gbs"] / PEAK_GBS, 4), "traffic": traffic}
 
 
+def copy_calibration(steps):
+    """Plain streaming kernels of known traffic, each launched `steps` times over 4 rotating buffers of COPY_BYTES:
+    torch's sum of an fp32 buffer (reads COPY_BYTES; its counter FETCH_SIZE scales the reads) and torch's fill_ of one
+    (writes COPY_BYTES; its WRITE_SIZE scales the writes)."""
+    import torch
+    dev = torch.device("cuda:0")
+    n = COPY_BYTES // 4
+    bufs = [torch.ones(n, device=dev) for _ in range(4)]
+    sink = torch.empty((), device=dev)
+    for i in range(steps):
+        torch.sum(bufs[i % 4], dim=0, out=sink)
+        bufs[(i + 2) % 4].fill_(1.0)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_bytes": COPY_BYTES, "launches": steps}))
+
+
+def counter_means(run_dir, counter):
+    """Mean per dispatch of `counter` for each kernel name in the rocprofv3 counter CSVs under run_dir."""
+    sums, counts = {}, {}
+    for path in glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] != counter:
+                    continue
+                key = (r["Kernel_Name"], r.get("Dispatch_Id") or r.get("Correlation_Id"))
+                sums[key] = sums.get(key, 0.0) + float(r["Counter_Value"])
+    per_kernel = {}
+    for (name, _), v in sums.items():
+        per_kernel.setdefault(name, []).append(v)
+    return {name: sum(v) / len(v) for name, v in per_kernel.items()}
+
+
+def traffic_from(run_dir):
+    """FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of each workload's dominant kernel, scaled by the ratio of the
+    calibration copy's known bytes to its counted bytes, into profiles/traffic.json."""
+    fetch = {}
+    write = {}
+    for sub in sorted(os.listdir(run_dir)):
+        d = os.path.join(run_dir, sub)
+        if os.path.isdir(d):
+            fetch.update({(sub, n): v for n, v in counter_means(d, "FETCH_SIZE").items()})
+            write.update({(sub, n): v for n, v in counter_means(d, "WRITE_SIZE").items()})
+
+    def pick(table, sub, pattern):
+        hits = [v for (s, n), v in table.items() if s == sub and pattern in n]
+        return sum(hits) if hits else None
+
+    cf, cw = pick(fetch, "copy_fetch", "reduce_kernel"), pick(write, "copy_write", "FillFunctor")
+    f_scale = COPY_BYTES / (cf * 1024) if cf else 1.0
+    w_scale = COPY_BYTES / (cw * 1024) if cw else 1.0
+    out = {"_method": "rocprofv3 --pmc FETCH_SIZE, then --pmc WRITE_SIZE, in separate runs of bench.py --workload W "
+                      "(KiB per dispatch, mean over dispatches of the named kernels, summed over the kernels of one "
+                      "launch), each scaled by the known bytes of the matching kernel of bench.py --copy-calibration "
+                      "(a 256 MiB sum for FETCH_SIZE, a 256 MiB fill for WRITE_SIZE) over its counted bytes",
+           "calibration_fetch_kib": cf and round(cf, 1), "calibration_write_kib": cw and round(cw, 1),
+           "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}
+    for label, kernel in KERNELS.items():
+        f = pick(fetch, f"{label}_fetch", kernel)
+        w = pick(write, f"{label}_write", kernel)
+        if f is None or w is None:
+            continue
+        out[label] = {"kernel": kernel, "fetch_kib": round(f, 1), "write_kib": round(w, 1),
+                      "bytes_per_launch": int(round(f * 1024 * f_scale + w * 1024 * w_scale))}
+    os.makedirs(os.path.dirname(TRAFFIC_PATH), exist_ok=True)
+    with open(TRAFFIC_PATH, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
+    if args.traffic_from:
+        traffic_from(args.traffic_from)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.steps)
+        return
     import torch
     from __graft_entry__ import load_package
     pkg = load_package()
     dev = torch.device("cuda:0")
-    flush_buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    flush_buf = None if args.no_cold else torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
     sink = torch.empty((), device=dev)
 
     def flush():
@@ -192,19 +328,21 @@ def main():
     cases = []
     for name in names:
         if name.startswith("topk"):
-            if not os.path.exists(pkg.lib_path("topk")):
-                continue
-            cases += [(name, k) for k in (1, 50, 1024)]
+            cases += [(name, k) for k in ([args.k] if args.k else (1, 50, 1024))]
         else:
             cases.append((name, None))
     results = {}
     for name, k in cases:
         case = Case(pkg, name, dev, k)
-        print(f"[bench] {case.label}: {args.warmup} warm-up + {args.steps} timed launches", file=sys.stderr, flush=True)
-        res = time_case(case, args.steps, args.warmup, flush, args.warm)
+        print(f"[bench] {case.label}: {args.warmup} warm-up + {args.steps} timed launches over {case.copies} copies",
+              file=sys.stderr, flush=True)
+        res = time_rotating(case, args.steps, args.warmup)
+        if not args.no_cold:
+            res.update(time_cold(case, args.steps, flush))
         results[case.label] = res
         print(f"[bench] {case.label}: {res['us_mean']:.2f} us/call  {res['gbs']:.0f} GB/s  "
-              f"{res['pct_peak']:.1f}% of peak" + (f"  (warm {res['warm_us']:.2f} us)" if args.warm else ""),
+              f"{res['pct_peak']:.1f}% of peak" +
+              (f"  (single flushed launch: median {res['cold_us_median']:.2f} us)" if not args.no_cold else ""),
               file=sys.stderr, flush=True)
         del case
         torch.cuda.empty_cache()
@@ -214,19 +352,17 @@ def main():
     line = {
         "metric": METRIC, "value": round(hr["gbs"], 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(hr["us_mean"] / 1e3, 6), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if head.startswith(("rmsnorm", "rope")) else "fp32",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if head.startswith(("rmsnorm", "rope")) else "fp32",
         "data": "synthetic: seeded torch.Generator inputs of the named shapes (workloads.py), resident in HBM; "
-                "L2 and Infinity Cache flushed before every timed launch",
-        "config": {"workload": head, "us_per_call": round(hr["us_mean"], 3), "us_median": round(hr["us_median"], 3),
-                   "pct_of_peak": round(hr["pct_peak"], 2), "algorithmic_bytes": hr["bytes"]},
+                "timed launches rotate over copies larger than the caches",
+        "config": {"workload": head, "us_per_call": round(hr["us_mean"], 3), "pct_of_peak": round(hr["pct_peak"], 2),
+                   "algorithmic_bytes": hr["bytes"], "copies": hr["copies"]},
         "roofline": roofline_entry(hr, head),
         "cpu_baseline": None,
-        "per_workload": {k: {"us_mean": round(v["us_mean"], 3), "us_median": round(v["us_median"], 3),
-                             "us_p10": round(v["us_p10"], 3), "us_p90": round(v["us_p90"], 3),
-                             "gbs": round(v["gbs"], 1), "pct_peak": round(v["pct_peak"], 2),
-                             **({"warm_us": round(v["warm_us"], 3), "warm_gbs": round(v["warm_gbs"], 1)}
-                                if "warm_us" in v else {})}
-                         for k, v in results.items()},
+        "per_workload": {lab: {key: (round(v, 3) if isinstance(v, float) else v) for key, v in r.items()
+                               if key not in ("wall_s", "bytes")}
+                         for lab, r in results.items()},
     }
     if not args.no_cpu and head == HEADLINE:
         print("[bench] CPU baseline (torch path on the host cores)", file=sys.stderr, flush=True)

@@ -479,9 +479,11 @@ constexpr int kTileSort = 256;  // rank-sort capacity (one composite per thread)
 static_assert(kTileKeep <= kTileSort && kTileKeep <= 2 * kWave, "a kept list must fit the sort and two per lane");
 static_assert(kTileSort == kThreads, "the rank sort and the merge heads use one composite per thread");
 
+typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+
 struct TileSmem {
   u64 seg[kWaves][kTileSeg];
-  u64 sorted[kTileSort];
+  alignas(16) u64 sorted[kTileSort];
   uint32_t red[2][kWaves];
   int cnt[kWaves];
   u64 pick;
@@ -661,6 +663,20 @@ struct TileList {
   }
 };
 
+// The number of composites of list[0, n16) greater than c; n16 is a multiple of 16 and the list is zero-padded to it.
+// Sixteen entries (eight 16-byte LDS reads, all broadcasts) per step keep the reads in flight together.
+__device__ __forceinline__ int rank_in(const u64* list, int n16, u64 c) {
+  int r = 0;
+  for (int j = 0; j < n16; j += 16) {
+    u64x2 p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = *reinterpret_cast<const u64x2*>(list + j + 2 * i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r += (p[i].x > c) + (p[i].y > c);
+  }
+  return r;
+}
+
 // Ranks the block's list (at most kTileSort composites) and writes its k largest, in order, as the output row (a
 // list holding at least k) or to the chunk list wr (0 past the end of a shorter list).
 template <typename T>
@@ -677,14 +693,12 @@ __device__ void finish_list(TileSmem& s, const TileList& L, void* values, long l
     n += c;
   }
   for (int i = lane; i < L.cnt; i += kWave) s.sorted[pre + i] = L.seg[i];
+  const int n16 = (n + 15) & ~15;
+  if (t >= n && t < n16) s.sorted[t] = 0ull;
   __syncthreads();
   if (t < n) {
     const u64 mine = s.sorted[t];
-    int rank = 0;
-    int j = 0;
-    for (; j + 4 <= n; j += 4)
-      rank += (s.sorted[j] > mine) + (s.sorted[j + 1] > mine) + (s.sorted[j + 2] > mine) + (s.sorted[j + 3] > mine);
-    for (; j < n; ++j) rank += s.sorted[j] > mine;
+    const int rank = rank_in(s.sorted, n16, mine);
     if (rank < k) {
       if (to_output) {
         if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + rank] = composite_bits(mine);
@@ -859,30 +873,30 @@ __global__ void __launch_bounds__(kThreads)
   TileList L{s.seg[wave_id()], 0};
   const int h = (k + nchunks - 1) / nchunks;
   const int nh = h * nchunks;
-  u64 floor = 1;
-  if (nh <= kTileSort) {
-    const u64 hv = t < nh ? wr[(long long)(t / h) * k + t % h] : 0ull;
-    s.sorted[t] = hv;
-    const int real = (int)red.sum((uint32_t)__popcll(__ballot(hv != 0)));
-    if (real >= k) {
-      if (hv != 0) {
-        int rank = 0;
-        for (int j = 0; j < nh; ++j) rank += s.sorted[j] > hv;
-        if (rank == k - 1) s.pick = hv;
-      }
-      __syncthreads();
-      floor = s.pick;
-    }
-  }
   constexpr int PER = 8;
   const int total = nchunks * k;
-  for (int base = 0; base < total; base += kThreads * PER) {
-    u64 c[PER];
+  u64 c[PER];
+  auto load = [&](int base) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int at = base + i * kThreads + t;
       c[i] = at < total ? wr[at] : 0ull;
     }
+  };
+  load(0);  // in flight together with the heads
+  u64 floor = 1;
+  if (nh <= kTileSort) {
+    const u64 hv = t < nh ? wr[(long long)(t / h) * k + t % h] : 0ull;
+    s.sorted[t] = hv;  // zero past nh: the padding rank_in reads
+    const int real = (int)red.sum((uint32_t)__popcll(__ballot(hv != 0)));
+    if (real >= k) {
+      if (hv != 0 && rank_in(s.sorted, (nh + 15) & ~15, hv) == k - 1) s.pick = hv;
+      __syncthreads();
+      floor = s.pick;
+    }
+  }
+  for (int base = 0; base < total; base += kThreads * PER) {
+    if (base > 0) load(base);
     const int cnt0 = L.cnt;
 #pragma unroll
     for (int i = 0; i < PER; ++i) L.push(c[i], c[i] >= floor);
