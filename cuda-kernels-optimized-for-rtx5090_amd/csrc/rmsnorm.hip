@@ -193,8 +193,10 @@ int launch_k(const Args& a) {
   auto kern = rmsnorm_rows<T, WAVES, NV, FULL, HAS_W, NTL, true>;
   static int occ = 0;
   if (occ <= 0) occ = blocks_per_cu(kern, BW * kWave);
+  // about 8 resident waves per CU by default (more waves only contend for the memory queues; measured on MI355X)
   int per_cu = rw_host::tune_get(kTuneBlocksPerCu);
-  if (per_cu <= 0 || per_cu > occ) per_cu = occ;
+  if (per_cu <= 0) per_cu = 8 / BW > 1 ? 8 / BW : 1;
+  if (per_cu > occ) per_cu = occ;
   const long long need = (a.rows + GROUPS - 1) / GROUPS;
   long long grid = (long long)rw_host::device_cus() * per_cu;
   if (grid > need) grid = need;
@@ -240,14 +242,16 @@ int launch_typed(const void* x, const void* w, void* y, long long rows, int cols
   if (vec && rw_host::tune_get(kTuneGeneric) != 1 && nvec <= (long long)kMaxWaves * kWave * kMaxNv) {
     int waves = rw_host::tune_get(kTuneWaves), nv = rw_host::tune_get(kTuneNv);
     if (waves <= 0) {
-      // One wave per row up to 8 vectors per lane (4096 two-byte columns), then more waves at 8 vectors per lane.
-      waves = pow2_at_least((nvec + (long long)kWave * kMaxNv - 1) / ((long long)kWave * kMaxNv));
+      // One wave per row up to 4 vectors per lane (2048 two-byte columns), then more waves at 4 vectors per lane
+      // (and 8 per lane once 16 waves are not enough).
+      waves = pow2_at_least((nvec + (long long)kWave * 4 - 1) / ((long long)kWave * 4));
       if (waves > kMaxWaves) waves = kMaxWaves;
     }
     if (nv <= 0) nv = pow2_at_least((nvec + (long long)waves * kWave - 1) / ((long long)waves * kWave));
     if ((long long)waves * kWave * nv >= nvec) {
       const Args a{x, w, y, rows, nvec, cols, eps, stream};
-      return rw_host::tune_get(kTuneNtLoads) == 1 ? launch_rows<T, HAS_W, true>(waves, nv, a)
+      // non-temporal loads unless switched off (2): x is read once
+      return rw_host::tune_get(kTuneNtLoads) != 2 ? launch_rows<T, HAS_W, true>(waves, nv, a)
                                                   : launch_rows<T, HAS_W, false>(waves, nv, a);
     }
   }

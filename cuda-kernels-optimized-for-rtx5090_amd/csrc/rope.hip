@@ -262,7 +262,8 @@ int launch_vec_k(const Ptrs& p, const Shape& s, int threads, hipStream_t stream)
   auto kern = rope_vec<T, C, FREQ, IPT>;
   int occ = blocks_per_cu(kern, threads);
   int per_cu = rw_host::tune_get(kTuneBlocksPerCu);
-  if (per_cu <= 0 || per_cu > occ) per_cu = occ;
+  if (per_cu <= 0) per_cu = 8;  // 8 resident token blocks per CU by default (measured on MI355X)
+  if (per_cu > occ) per_cu = occ;
   long long grid = (long long)rw_host::device_cus() * per_cu;
   if (grid > s.tokens) grid = s.tokens;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), 0, stream, p.q, p.k, p.cos_rows, p.sin_rows,
@@ -276,7 +277,14 @@ int launch_shape(const Ptrs& p, const Shape& s, bool vec, hipStream_t stream) {
   if (vec && rw_host::tune_get(kTuneScalar) != 1) {
     const long long items = (long long)heads * (s.head_dim >> 4);
     int threads = rw_host::tune_get(kTuneThreads);
-    if (threads <= 0) threads = (int)(items < 1024 ? (items + 63) / 64 * 64 : 1024);
+    if (threads <= 0) {
+      // at most 256 threads per token block, the items spread evenly over them (e.g. 320 items: 192 threads, 2 each);
+      // beyond 4 items per thread, up to 1024 threads
+      long long per = (items + 255) / 256;
+      if (per > 4) per = (items + 1023) / 1024;
+      threads = (int)(((items + per - 1) / per + 63) / 64 * 64);
+      if (threads > 1024) threads = 1024;
+    }
     const long long ipt = (items + threads - 1) / threads;
     if (ipt <= 1) return launch_vec_k<T, C, FREQ, 1>(p, s, threads, stream);
     if (ipt <= 2) return launch_vec_k<T, C, FREQ, 2>(p, s, threads, stream);

@@ -253,8 +253,11 @@ int launch_rows_k(const void* x, void* y, long long rows, long long nvec, hipStr
   auto kern = softmax_rows<T, WAVES, NV, FULL, NTL, true>;
   static int occ = 0;  // resident blocks per CU of this instantiation (idempotent cache)
   if (occ <= 0) occ = blocks_per_cu(kern, BW * kWave);
+  // about 8 resident waves per CU by default: with two register sets per wave that keeps enough loads in flight,
+  // and more waves only contend (measured on MI355X)
   int per_cu = rw_host::tune_get(kTuneBlocksPerCu);
-  if (per_cu <= 0 || per_cu > occ) per_cu = occ;
+  if (per_cu <= 0) per_cu = 8 / BW > 1 ? 8 / BW : 1;
+  if (per_cu > occ) per_cu = occ;
   const long long need = (rows + GROUPS - 1) / GROUPS;
   long long grid = (long long)rw_host::device_cus() * per_cu;
   if (grid > need) grid = need;
