@@ -19,7 +19,7 @@ int rmsnorm_launch_weighted(const void* x, const void* weight, void* y, long lon
                             float eps, int threads, hipStream_t stream);
 
 /* No counterpart in the reference: tuning override for parameter sweeps. Slots: 0 waves per row, 1 vectors per lane,
- * 2 resident blocks per CU, 3 forced generic kernel (1), 4 non-temporal loads (1 on). Returns 0 or -1. */
+ * 2 resident blocks per CU, 3 forced generic kernel (1), 4 non-temporal loads (default on; 2 off). Returns 0 or -1. */
 int rmsnorm_tune(int slot, int value);
 
 #ifdef __cplusplus

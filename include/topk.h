@@ -11,12 +11,14 @@ extern "C" {
 #endif
 
 /* topk/kernel.cu:520: columns per workgroup for a rows x cols launch (the row's chunk count is ceil(cols / chunk)),
- * sized so the grid is resident at once; chunks of at least max(min_chunk, 4096) columns, a multiple of 4 when a row is
- * split. `threads` and `depth` are the reference's CUDA tuning knobs, accepted and unused. */
+ * sized so the grid is resident about once; a chunk longer than one 16384-element register tile is rounded up to whole
+ * tiles, never shorter than min_chunk, a multiple of 8 when a row is split. `threads` and `depth` are the reference's
+ * CUDA tuning knobs, accepted and unused. */
 long long plan(long long rows, long long cols, int dtype, int threads, int depth, int min_chunk);
 
 /* topk/kernel.cu:549: values [rows, k] in x's dtype, indices [rows, k] int64; work: u64 [rows * nchunks * k]
- * (nchunks = ceil(cols / chunk), only used when nchunks > 1); counters: u32 [>= rows], zero on entry, left zero.
+ * (nchunks = ceil(cols / chunk), only used when nchunks > 1); counters: u32 [>= rows], zero on entry, left zero (the
+ * chunk lists are merged by a second kernel in stream order, so this build does not touch them).
  * Returns 0 (rows <= 0 or k <= 0 is a no-op), -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0,
  * a split row with chunk % 4 != 0 or nchunks * k > INT_MAX / 2, threads not 128/256/512, depth not 2/4/8 or an unknown
  * dtype, otherwise the hipError_t of the launch. Launches sharing work/counters must be ordered (one stream). */
@@ -29,7 +31,7 @@ int launch(const void* x, void* values, void* indices, void* work, void* counter
 int topk_reset(void* counters, long long rows, hipStream_t stream);
 
 /* No counterpart in the reference: tuning override for parameter sweeps. Slot 0: resident workgroups per CU assumed by
- * plan(). Returns 0 or -1. */
+ * plan(); slot 1: elements per lane of the k > 64 kernel's register block (16, 32 or 64). Returns 0 or -1. */
 int topk_tune(int slot, int value);
 
 #ifdef __cplusplus
