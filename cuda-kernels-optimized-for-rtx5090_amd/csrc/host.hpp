@@ -41,9 +41,11 @@ inline int device_cus() {
 // ordered, so a buffer reused by consecutive launches on its stream is never read and written by two of them at once.
 // It grows by reallocation (the runtime waits for work that may still use the old buffer) and lives until the process
 // ends. Returns nullptr with *err set on failure.
-inline void* stream_workspace(hipStream_t stream, size_t bytes, int* err) {
+// `purpose` keeps separate buffers for users that must not share one (a buffer whose contents carry over between
+// launches); with `zeroed` a new buffer is cleared on `stream` before first use.
+inline void* stream_workspace(hipStream_t stream, size_t bytes, int* err, int purpose = 0, bool zeroed = false) {
   static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> buffers;
+  static std::map<std::pair<std::pair<int, int>, hipStream_t>, std::pair<void*, size_t>> buffers;
   *err = kOk;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -52,7 +54,7 @@ inline void* stream_workspace(hipStream_t stream, size_t bytes, int* err) {
     return nullptr;
   }
   std::lock_guard<std::mutex> lock(mu);
-  auto& slot = buffers[std::make_pair(dev, stream)];
+  auto& slot = buffers[std::make_pair(std::make_pair(dev, purpose), stream)];
   if (slot.second >= bytes && slot.first) return slot.first;
   size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
   if (slot.first) {
@@ -68,6 +70,14 @@ inline void* stream_workspace(hipStream_t stream, size_t bytes, int* err) {
   if (e != hipSuccess) {
     *err = (int)e;
     return nullptr;
+  }
+  if (zeroed) {
+    e = hipMemsetAsync(p, 0, want, stream);
+    if (e != hipSuccess) {
+      (void)hipFree(p);
+      *err = (int)e;
+      return nullptr;
+    }
   }
   slot = {p, want};
   return p;

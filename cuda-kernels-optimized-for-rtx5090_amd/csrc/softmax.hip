@@ -9,12 +9,14 @@
 //    group (DPP inside each wave, one LDS slot per wave across waves) and y = exp(x - max) / sum is written from the
 //    registers: one HBM read and one write per element. Workgroups are persistent: each walks the rows with a stride
 //    of the grid and loads its next row while it reduces and stores the current one.
-//  - split tier (longer rows): a row is split into chunks of WAVES x 64 x NV vectors, one workgroup each. Pass 1 reduces
-//    each chunk to its online-softmax pair (m, s = sum of exp(x - m)) in a workspace; pass 2 merges the row's pairs
-//    (M = max m, S = sum of s * exp(m - M)) in every wave and writes exp(x - M) / S for its chunk, re-reading the chunk
-//    (64 MiB rows are resident in the 256 MB Infinity Cache between the passes).
+//  - co-resident tier (longer rows, when all of their chunks fit on the GPU at once): one pass; see softmax_coop.
+//  - split tier (longer rows otherwise): a row is split into chunks of WAVES x 64 x NV vectors, one workgroup each.
+//    Pass 1 reduces each chunk to its online-softmax pair (m, s = sum of exp(x - m)) in a workspace; pass 2 merges the
+//    row's pairs (M = max m, S = sum of s * exp(m - M)) in every wave and writes exp(x - M) / S for its chunk,
+//    re-reading the chunk (2R + 1W).
 //  - generic tier (any length or alignment): one workgroup per row, three scalar passes (max, sum, write).
-// The division is the IEEE fp32 division, as in the reference (softmax/kernel.cu:240).
+// The normalisation multiplies by the fp32 reciprocal of the row sum (the reference divides, softmax/kernel.cu:240;
+// the two differ by at most 1.5 ulp in fp32 and are within the 1e-5 relative tolerance of the fp64 oracle).
 #include <climits>
 #include <cmath>
 
@@ -75,15 +77,18 @@ __device__ __forceinline__ float lane_max(const Regs<NV>& r, float (&f)[NV][T::V
   return m;
 }
 
+// y = f * (1 / s): one division per row and a product per element (within 1.5 ulp of f / s; an element-wise fp32
+// division is a multi-instruction sequence that made these kernels compute-bound).
 template <typename T, int G, int NV, bool FULL, bool NTS>
 __device__ __forceinline__ void scale_store(float (&f)[NV][T::V], float s, void* base, long long first,
                                             long long count, int t, bool active) {
+  const float inv = 1.0f / s;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const long long i = (long long)k * G + t;
     if (active && (FULL || i < count)) {
 #pragma unroll
-      for (int e = 0; e < T::V; ++e) f[k][e] = f[k][e] / s;
+      for (int e = 0; e < T::V; ++e) f[k][e] = f[k][e] * inv;
       store16<NTS>(base, first + i, pack<T>(f[k]));
     }
   }
@@ -203,6 +208,144 @@ __global__ void __launch_bounds__(WAVES * 64)
   scale_store<T, G, NV, false, NTS>(f, S, y, row * nvec + first, count, t, true);
 }
 
+// Co-resident tier, for long rows whose chunks all fit on the GPU at once: the split tier's chunks, each held in its
+// workgroup's registers across the exchange of the row's chunk pairs, so x is read once (1R + 1W). For fp32 the
+// registers hold exp(x - m) after the first pass and the output is exp(x - m) * (exp(m - M) / S), within 3 ulp of
+// the once-rounded value (outputs in the fp32 subnormal range, below 2^-126, are within a few 2^-149). The grid never
+// exceeds what the GPU holds at once, so every workgroup of a row is resident (or waits only for other kernels to
+// drain). A workgroup publishes its pair (m, s) as one device-coherent 64-bit store into the row's slot for it; a slot
+// holding 0 is unpublished (no pair is 0: a chunk's s is >= 1 for a finite max, an all -inf chunk stores (-inf, 0)
+// and a NaN chunk NaNs). Wave 0 polls the row's slots with device-coherent loads until all are published, merges them
+// (the same lanes and order in every workgroup of the row, so all agree bit for bit) and hands M and S to the other
+// waves; the chunk is then written from the registers. Last, a departure counter finds the row's last workgroup, which
+// zeroes the row's slots and the counter for the next launch (the workspace starts zeroed). The wait is bounded: it
+// always ends, even if a row's workgroups could not all run.
+constexpr unsigned kSpinLimit = 1u << 22;
+constexpr int kCoopMaxChunks = 64;  // slots a row may have (one per lane of the polling wave)
+
+__device__ __forceinline__ unsigned long long pair_bits(float m, float s) {
+  return ((unsigned long long)__float_as_uint(s) << 32) | __float_as_uint(m);
+}
+
+template <typename T, int WAVES, int NV, bool NTL, bool NTS>
+__global__ void __launch_bounds__(WAVES * 64)
+    softmax_coop(const void* __restrict__ x, void* __restrict__ y, unsigned long long* __restrict__ pairs,
+                 unsigned* __restrict__ departs, long long nvec, long long chunks) {
+  constexpr int G = WAVES * kWave;
+  constexpr long long CH = (long long)G * NV;
+  constexpr int PER = kCoopMaxChunks / kWave;
+  __shared__ float slots[2][WAVES];
+  __shared__ float ms[2];
+  const long long b = blockIdx.x;
+  const long long row = b / chunks, c = b - row * chunks;
+  const long long first = c * CH;
+  const long long count = nvec - first < CH ? nvec - first : CH;
+  const int t = (int)threadIdx.x;
+  Regs<NV> r;
+  load_vectors<G, NV, false, NTL>(r, x, row * nvec + first, count, t);
+  // the chunk's pair; exp(x - m) is not kept (the registers keep x for the second use)
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float f[T::V];
+    unpack<T>(r.v[k], f);
+    const bool ok = (long long)k * G + t < count;
+#pragma unroll
+    for (int i = 0; i < T::V; ++i) m = ok ? fmaxf(m, f[i]) : m;
+  }
+  m = group_reduce<WAVES>(m, OpMax{}, slots[0], wave_id(), 0);
+  // fp32: the registers now take e = exp(x - m) (0 for an all -inf chunk) in place of x, and the output is e * (exp(m -
+  // M) / S): one exp per element. bf16 (twice the elements per register) keeps x and evaluates exp(x - M) again.
+  constexpr bool KEEP = T::V == 4;
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float f[T::V];
+    unpack<T>(r.v[k], f);
+    const bool ok = (long long)k * G + t < count;
+#pragma unroll
+    for (int i = 0; i < T::V; ++i) {
+      const float e = ok && m != -INFINITY ? expf(f[i] - m) : 0.0f;
+      s += e;
+      if constexpr (KEEP) r.v[k][i] = __float_as_uint(e);
+    }
+  }
+  s = group_reduce<WAVES>(s, OpSum{}, slots[1], wave_id(), 0);
+  unsigned long long* row_pairs = pairs + row * chunks;
+  if (t == 0)  // an all -inf chunk has s = 0 and contributes nothing to the merge
+    __hip_atomic_store(row_pairs + c, pair_bits(m, s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (wave_id() == 0) {
+    const int lane = lane_id();
+    unsigned long long v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = 0;
+    for (unsigned n = 0; n < kSpinLimit; ++n) {
+      bool ready = true;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const long long at = (long long)i * kWave + lane;
+        if (at < chunks && v[i] == 0)
+          v[i] = __hip_atomic_load(row_pairs + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ready = ready && (at >= chunks || v[i] != 0);
+      }
+      if (__ballot(!ready) == 0) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    float pm = -INFINITY, ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if ((long long)i * kWave + lane < chunks) {
+        const float qm = __uint_as_float((unsigned)v[i]), qs = __uint_as_float((unsigned)(v[i] >> 32));
+        const float mm = fmaxf(pm, qm);
+        if (mm != -INFINITY) {
+          ps = ps * expf(pm - mm) + qs * expf(qm - mm);
+          pm = mm;
+        }
+      }
+    }
+    const float M = wave_max(pm);
+    const float S = wave_sum(M == -INFINITY ? ps : ps * expf(pm - M));
+    if (lane == 0) {
+      ms[0] = M;
+      ms[1] = S;
+    }
+  }
+  __syncthreads();
+  const float M = ms[0], S = ms[1];
+  if constexpr (KEEP) {
+    // y = e * exp(m - M) / S; an all -inf chunk (e = 0) gives 0, or NaN when the whole row is -inf (M = -inf)
+    const float scale = m == -INFINITY ? (M == -INFINITY ? NAN : 0.0f) : expf(m - M) / S;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const long long i = (long long)k * G + t;
+      if (i < count) {
+        float f[T::V];
+#pragma unroll
+        for (int e = 0; e < T::V; ++e) f[e] = __uint_as_float(r.v[k][e]) * scale;
+        store16<NTS>(y, row * nvec + first + i, pack<T>(f));
+      }
+    }
+  } else {
+    float f[NV][T::V];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      unpack<T>(r.v[k], f[k]);
+#pragma unroll
+      for (int e = 0; e < T::V; ++e) f[k][e] = expf(f[k][e] - M);
+    }
+    scale_store<T, G, NV, false, NTS>(f, S, y, row * nvec + first, count, t, true);
+  }
+  if (wave_id() == 0) {
+    unsigned old = 0;
+    if (lane_id() == 0) old = __hip_atomic_fetch_add(departs + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__builtin_amdgcn_readfirstlane(old) == (unsigned)chunks - 1) {  // the row's last workgroup: clear for reuse
+      for (long long at = lane_id(); at < chunks; at += kWave)
+        __hip_atomic_store(row_pairs + at, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane_id() == 0) __hip_atomic_store(departs + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 // Generic tier: any row length and alignment; one 256-thread block per row (grid-strided), three scalar passes.
 template <typename T>
 __global__ void __launch_bounds__(256)
@@ -225,8 +368,8 @@ __global__ void __launch_bounds__(256)
 // ---- host side -------------------------------------------------------------------------------------------------------
 
 // Tuning slots (0 = automatic): row-tier waves per row, row-tier vectors per lane, row-tier resident blocks per CU,
-// split-tier waves, split-tier vectors per lane, forced tier (1 row, 2 split, 3 generic), non-temporal loads (1 on,
-// 2 off).
+// split-tier waves, split-tier vectors per lane, forced tier (1 row, 2 split, 3 generic, 4 co-resident), non-temporal
+// loads (1 on, 2 off).
 enum { kTuneWaves = 0, kTuneNv = 1, kTuneBlocksPerCu = 2, kTuneSplitWaves = 3, kTuneSplitNv = 4, kTuneTier = 5,
        kTuneNtLoads = 6 };
 
@@ -330,6 +473,32 @@ int launch_split(int waves, int nv, const void* x, void* y, long long rows, long
   }
 }
 
+// Co-resident tier: chunks of 4 waves x 64 lanes x 16 vectors (16384 fp32 / 32768 bf16 elements), up to kCoopRows
+// rows of up to kCoopMaxChunks chunks. Returns 1, launching nothing, when the rows' chunks do not all fit on the GPU
+// at once. Workspace: the departure counters (a fixed region, so that launches of any shape agree on it), then the
+// pair slots.
+constexpr long long kCoopRows = 4096;
+constexpr size_t kCoopCounterBytes = (size_t)kCoopRows * sizeof(unsigned);
+
+template <typename T, bool NTL>
+int launch_coop(const void* x, void* y, long long rows, long long nvec, hipStream_t stream) {
+  constexpr int WAVES = 4, NV = 16;
+  constexpr long long CH = (long long)WAVES * kWave * NV;
+  long long chunks = (nvec + CH - 1) / CH;
+  auto kern = softmax_coop<T, WAVES, NV, NTL, true>;
+  static int occ = 0;  // resident blocks per CU of this instantiation (idempotent cache)
+  if (occ <= 0) occ = blocks_per_cu(kern, WAVES * kWave);
+  const long long blocks = rows * chunks;
+  if (rows > kCoopRows || chunks > kCoopMaxChunks || blocks > (long long)rw_host::device_cus() * occ) return 1;
+  int err = 0;
+  char* ws = (char*)rw_host::stream_workspace(stream, kCoopCounterBytes + (size_t)blocks * 8, &err, 1, true);
+  if (!ws) return err;
+  unsigned* departs = (unsigned*)ws;
+  unsigned long long* pairs = (unsigned long long*)(ws + kCoopCounterBytes);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(WAVES * kWave), 0, stream, x, y, pairs, departs, nvec, chunks);
+  return (int)hipGetLastError();
+}
+
 template <typename T>
 int launch_generic(const void* x, void* y, long long rows, long long cols, hipStream_t stream) {
   long long grid = (long long)rw_host::device_cus() * 8;
@@ -359,6 +528,11 @@ int launch_typed(const void* x, void* y, long long rows, long long cols, hipStre
                  : launch_rows<T, false>(waves, nv, x, y, rows, nvec, stream);
     }
     if (tier == 1) return rw_host::kInvalid;
+  }
+  if (tier == 0 || tier == 4) {
+    const int rc = ntl ? launch_coop<T, true>(x, y, rows, nvec, stream) : launch_coop<T, false>(x, y, rows, nvec, stream);
+    if (rc != 1) return rc;
+    if (tier == 4) return rw_host::kInvalid;
   }
   int waves = rw_host::tune_get(kTuneSplitWaves), nv = rw_host::tune_get(kTuneSplitNv);
   if (waves <= 0) waves = 4;

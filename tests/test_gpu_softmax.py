@@ -1,8 +1,9 @@
 """GPU parity of softmax (build/softmax/libkernel.so through the reference ABI `launch`) against the oracle.
 
 fp32: |y - oracle| <= 1e-5 |oracle| elementwise (the oracle is the fp64 softmax rounded once); bf16: within 1 ulp.
-Shapes cover every tier: wave-per-row and workgroup-per-row rows (full and ragged), the split tier for long rows, and
-the generic tier for lengths that are not a multiple of the vector width and for misaligned pointers.
+Shapes cover every tier: wave-per-row and workgroup-per-row rows (full and ragged), the single-pass co-resident tier
+and the two-pass split tier for long rows, and the generic tier for lengths that are not a multiple of the vector width
+and for misaligned pointers.
 """
 
 import ctypes
@@ -77,6 +78,45 @@ def test_long_rows_with_infinite_chunks(pkg, oracle, dev):
     assert torch.isnan(y[1]).all()
     ref = oracle.softmax(x.numpy(), "fp32")
     assert_rel(y[[0, 2]].numpy(), ref[[0, 2]], FP32_TOL, "long rows")
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(64, 262144, "fp32"), (3, 70000, "fp32"), (1, 1 << 20, "fp32"),
+                                             (100, 40000, "fp32"), (8, 131072, "bf16"), (2, 300000, "bf16")])
+def test_long_rows_single_pass_and_split(pkg, oracle, dev, rows, cols, dtype):
+    """Long rows through the co-resident single-pass tier (4) and the two-pass split tier (2), forced in turn."""
+    lib = pkg.candidate("softmax")._lib
+    g = torch.Generator().manual_seed(rows + cols)
+    x = torch.randn(rows, cols, generator=g) * 4
+    x[0, : cols // 3] = float("-inf")  # whole chunks of -inf in the first row
+    if dtype == "bf16":
+        x = x.bfloat16()
+        ref = oracle.softmax(bits16(x), "bf16")
+    else:
+        ref = oracle.softmax(x.numpy(), "fp32")
+    xd = x.to(dev)
+    try:
+        for tier in (4, 2):
+            lib.softmax_tune(5, tier)
+            print(f"[softmax long] {rows}x{cols} {dtype} tier={tier}", flush=True)
+            y = pkg.softmax(xd)
+            if dtype == "bf16":
+                assert_ulp(bits16(y), ref, 1, f"tier {tier}")
+            else:
+                assert_rel(y.cpu().numpy(), ref, FP32_TOL, f"tier {tier}")
+    finally:
+        lib.softmax_tune(5, 0)
+
+
+def test_single_pass_back_to_back_shapes(pkg, oracle, dev):
+    """Consecutive single-pass launches of different shapes on one stream: each leaves its row counters at zero."""
+    g = torch.Generator().manual_seed(9)
+    xs = [torch.randn(64, 262144, generator=g), torch.randn(5, 50000, generator=g),
+          torch.randn(16, 1 << 18, generator=g), torch.randn(5, 50000, generator=g)]
+    ds = [x.to(dev) for x in xs]
+    ys = [pkg.softmax(d) for d in ds + ds]  # queued back to back, then checked
+    for i, y in enumerate(ys):
+        print(f"[softmax back-to-back] launch {i} shape={tuple(xs[i % 4].shape)}", flush=True)
+        assert_rel(y.cpu().numpy(), oracle.softmax(xs[i % 4].numpy(), "fp32"), FP32_TOL, f"launch {i}")
 
 
 def test_empty_is_noop(pkg, dev):
