@@ -6,9 +6,10 @@
 // distinct, a larger one comes first, and composite 0 means "no element". Values are decoded from the composites bit
 // for bit, so x is read once.
 //
-// Two kernels on the caller's stream (the stream order publishes the first kernel's workspace writes to the second;
-// a same-kernel hand-off would need an agent-scope release and acquire per workgroup, i.e. an L2 write-back and
-// invalidate of an XCD per workgroup, which costs far more than a second launch):
+// k <= 64: topk_tile, one kernel (see its comment); the row's last workgroup merges the chunk lists, handed over
+// through device-coherent stores and loads and the caller's per-row counter, as the reference's last-block merge.
+//
+// k > 64: two kernels on the caller's stream (the stream order publishes the first kernel's workspace to the second):
 //  - topk_chunks, one 256-thread workgroup per (chunk, row): the workgroup loads a block of its chunk (E elements per
 //    lane, 16-byte loads, all in flight at once) into registers and admits the block's top-k into an LDS buffer:
 //      seed   - for k <= 64 each wave ranks its 64 lane maxima (v_readlane broadcasts, no barrier) and takes the k-th;
@@ -474,9 +475,10 @@ __global__ void __launch_bounds__(kThreads)
 
 constexpr int kTileE = 64;      // elements per lane of a register tile (16384 per workgroup)
 constexpr int kTileSeg = 512;   // each wave's list segment (composites)
-constexpr int kTileKeep = 128;  // a list holding more than this after a batch is pruned to its k largest
+constexpr int kTileKeep = 256;  // a list holding more than this after a batch is pruned to its k largest
 constexpr int kTileSort = 256;  // rank-sort capacity (one composite per thread)
-static_assert(kTileKeep <= kTileSort && kTileKeep <= 2 * kWave, "a kept list must fit the sort and two per lane");
+static_assert(kTileKeep <= kTileSort && kTileKeep + 4 * kWave <= kTileSeg, "a kept list must fit the rank sort, and a "
+              "wave's share of it a step of re-pushes");
 static_assert(kTileSort == kThreads, "the rank sort and the merge heads use one composite per thread");
 
 typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
@@ -487,6 +489,7 @@ struct TileSmem {
   uint32_t red[2][kWaves];
   int cnt[kWaves];
   u64 pick;
+  int last;
 };
 
 // Order-preserving 32-bit key of fp32 bits u (the upper half of a composite).
@@ -541,7 +544,7 @@ struct BlockRed {
 // the keys' range (a block count per candidate bit), then, among the composites with that key, for the lower word.
 // Every thread returns it.
 template <int N, typename F>
-__device__ u64 block_kth(const F& slot, int k, BlockRed& red) {
+__device__ __forceinline__ u64 block_kth(const F& slot, int k, BlockRed& red) {
   uint32_t kmx = 0, kmn = 0xffffffffu;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
@@ -621,7 +624,7 @@ struct TileList {
   }
 
   // Keeps exactly the k largest of the list (which holds more, none dropped); returns the k-th.
-  __device__ u64 prune(BlockRed& red, int k) {
+  __device__ __forceinline__ u64 prune(BlockRed& red, int k) {
     constexpr int PER = kTileSeg / kWave;
     const int lane = lane_id();
     const int n = cnt;
@@ -645,11 +648,17 @@ struct TileList {
   // largest. If a segment overflowed, the batch is dropped and pushed again in `steps` steps from `floor` (a lower
   // bound of the k-th): step(s, floor, check) pushes step s's composites >= floor, calling check() after each group of
   // at most 256 per wave, and check() prunes whenever the list passes kTileKeep, raising floor to the k-th. Returns
-  // the new k-th, or 0.
+  // the new k-th, or 0, and sets `total` to the list's length when it is at most kTileKeep without a prune (else 0).
   template <typename S>
-  __device__ u64 settle(BlockRed& red, int k, int cnt0, int steps, u64 floor, const S& step) {
+  __device__ __forceinline__ u64 settle(BlockRed& red, int k, int cnt0, int steps, u64 floor, const S& step,
+                                        int& total) {
     const uint32_t v = red.sum((uint32_t)cnt + (cnt > kTileSeg ? (1u << 24) : 0u));
-    if (!(v >> 24)) return (int)(v & 0xffffffu) > kTileKeep ? prune(red, k) : 0ull;
+    total = 0;
+    if (!(v >> 24)) {
+      if ((int)(v & 0xffffffu) > kTileKeep) return prune(red, k);
+      total = (int)(v & 0xffffffu);
+      return 0ull;
+    }
     cnt = cnt0;
     u64 kth = 0;
     auto check = [&] {
@@ -677,11 +686,37 @@ __device__ __forceinline__ int rank_in(const u64* list, int n16, u64 c) {
   return r;
 }
 
+// Keeps exactly the k largest of the block's list of n composites (k < n <= kTileSort) by ranking every entry against
+// all of them (one per thread; cheaper than a bitwise search for short lists) and returns the k-th.
+__device__ __forceinline__ u64 prune_ranked(TileSmem& s, TileList& L, int k) {
+  const int wave = wave_id(), lane = lane_id(), t = threadIdx.x;
+  if (lane == 0) s.cnt[wave] = L.cnt;
+  __syncthreads();
+  int pre = 0, n = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int c = s.cnt[w];
+    pre += w < wave ? c : 0;
+    n += c;
+  }
+  for (int i = lane; i < L.cnt; i += kWave) s.sorted[pre + i] = L.seg[i];
+  const int n16 = (n + 15) & ~15;
+  if (t >= n && t < n16) s.sorted[t] = 0ull;
+  __syncthreads();
+  const u64 mine = t < n ? s.sorted[t] : 0ull;
+  const int rank = t < n ? rank_in(s.sorted, n16, mine) : kTileSort;
+  if (rank == k - 1) s.pick = mine;
+  L.cnt = 0;
+  L.push(mine, rank < k);
+  __syncthreads();
+  return s.pick;
+}
+
 // Ranks the block's list (at most kTileSort composites) and writes its k largest, in order, as the output row (a
-// list holding at least k) or to the chunk list wr (0 past the end of a shorter list).
+// list holding at least k) or to the chunk list wr with device-coherent stores (0 past the end of a shorter list).
 template <typename T>
-__device__ void finish_list(TileSmem& s, const TileList& L, void* values, long long* indices, u64* wr,
-                            long long row, int k, bool to_output) {
+__device__ __forceinline__ void finish_list(TileSmem& s, const TileList& L, void* values, long long* indices, u64* wr,
+                                            long long row, int k, bool to_output) {
   const int wave = wave_id(), lane = lane_id(), t = threadIdx.x;
   if (lane == 0) s.cnt[wave] = L.cnt;
   __syncthreads();
@@ -705,16 +740,17 @@ __device__ void finish_list(TileSmem& s, const TileList& L, void* values, long l
         else static_cast<uint16_t*>(values)[row * k + rank] = (uint16_t)(composite_bits(mine) >> 16);
         indices[row * k + rank] = composite_index(mine);
       } else {
-        wr[rank] = mine;
+        __hip_atomic_store(wr + rank, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
   if (!to_output)
-    for (int j = n + t; j < k; j += kThreads) wr[j] = 0ull;
+    for (int j = n + t; j < k; j += kThreads) __hip_atomic_store(wr + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// A register tile: thread t holds vectors v * 256 + t (v < NV) of elements [b0, b1) of a row, W each. fp32 registers
-// are turned into keys in place (prepare); bf16 keys are formed from the packed halves when used.
+// A register tile: thread t holds vectors v * 256 + t (v < NV) of elements [b0, b1) of a row, W each (an empty tile,
+// b0 >= b1, loads in-bounds duplicates and holds no element). load() only issues the loads; prepare() turns fp32
+// registers into keys in place once they are needed; bf16 keys are formed from the packed halves when used.
 template <typename T, bool VEC>
 struct Tile {
   static constexpr int W = Fmt<T>::W;
@@ -737,13 +773,15 @@ struct Tile {
     return ((u64)key(v, j) << 32) | (u64)(~(uint32_t)(first(v) + j));
   }
 
-  __device__ __forceinline__ void load(const T* row) {
+  __device__ __forceinline__ void load(const T* row, int t0, int end) {
+    b0 = t0;
+    b1 = end - t0 > kThreads * kTileE ? t0 + kThreads * kTileE : end;
     lane0 = b0 + (int)threadIdx.x * W;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int e0 = first(v);
       if constexpr (VEC) {
-        r[v] = load16<true>(row + (e0 < b1 ? e0 : b1 - W), 0);  // an in-range duplicate past the end, never used
+        r[v] = load16<true>(row + (e0 < b1 ? e0 : end - W), 0);  // an in-range duplicate past the end, never used
       } else {
         uint32_t u[W];
 #pragma unroll
@@ -756,6 +794,11 @@ struct Tile {
         else r[v] = (u32x4){u[0] | (u[1] << 16), u[2] | (u[3] << 16), u[4] | (u[5] << 16), u[6] | (u[7] << 16)};
       }
     }
+    asm volatile("" ::: "memory");  // issue the loads here: the scheduler must not sink them past later work
+  }
+
+  // Once the loads are needed: fp32 registers become keys in place.
+  __device__ __forceinline__ void prepare() {
     if constexpr (sizeof(T) == 4) {
 #pragma unroll
       for (int v = 0; v < NV; ++v)
@@ -793,34 +836,93 @@ struct Tile {
   }
 };
 
+// k <= 64 merge of a split row (the row's last workgroup). Every chunk list holds its chunk's k largest, descending,
+// so the first h = ceil(k / nchunks) entries of the lists give nchunks * h >= k distinct composites: the k-th largest
+// of these heads bounds the row's k-th from below and, the row's top k being spread over the chunks, admits little
+// beyond the answer. The lists (read with device-coherent loads: other workgroups wrote them) are then streamed
+// through the list from that floor, settled as in a tile, rank-sorted and written out.
+template <typename T>
+__device__ __forceinline__ void merge_lists(TileSmem& s, BlockRed& red, TileList& L, void* values,
+                                            long long* indices, const u64* wr, long long row, int nchunks, int k) {
+  const int t = threadIdx.x;
+  const int h = (k + nchunks - 1) / nchunks;
+  const int nh = h * nchunks;
+  constexpr int PER = 8;
+  const int total = nchunks * k;
+  auto ld = [&](int at) { return __hip_atomic_load(wr + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  u64 c[PER];
+  auto load = [&](int base) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int at = base + i * kThreads + t;
+      c[i] = at < total ? ld(at) : 0ull;
+    }
+  };
+  load(0);  // in flight together with the heads
+  u64 floor = 1;
+  if (nh <= kTileSort) {
+    const u64 hv = t < nh ? ld((t / h) * k + t % h) : 0ull;
+    s.sorted[t] = hv;  // zero past nh: the padding rank_in reads
+    const int real = (int)red.sum((uint32_t)__popcll(__ballot(hv != 0)));
+    if (real >= k) {
+      if (hv != 0 && rank_in(s.sorted, (nh + 15) & ~15, hv) == k - 1) s.pick = hv;
+      __syncthreads();
+      floor = s.pick;
+    }
+  }
+  for (int base = 0; base < total; base += kThreads * PER) {
+    if (base > 0) load(base);
+    const int cnt0 = L.cnt;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) L.push(c[i], c[i] >= floor);
+    int listed = 0;
+    const u64 kth = L.settle(
+        red, k, cnt0, PER, floor,
+        [&](int, const u64& f, const auto& check) {
+          L.push(c[0], c[0] >= f);
+          check();
+#pragma unroll
+          for (int i = 0; i + 1 < PER; ++i) c[i] = c[i + 1];
+        },
+        listed);
+    floor = kth > floor ? kth : floor;
+  }
+  finish_list<T>(s, L, values, indices, nullptr, row, k, true);
+}
+
 // k <= 64: one 256-thread workgroup per (chunk, row). The chunk is taken in register tiles of 16384 elements, all of a
 // tile's loads in flight at once. Per tile: each wave takes the ceil(k / 4)-th largest of its 64 lane maxima, which
 // has that many distinct elements at or above it, and the smallest of the four waves' keys has at least k; with the
 // k-th of the earlier tiles it is the admission key. Admitted elements (about k * 1.5 per tile on continuous data)
 // are appended to the waves' LDS segments; a list beyond kTileKeep is pruned to k, and an overflowing tile (ties, or
-// adversarial orders) is pushed again in index order with a prune whenever the list passes kTileKeep. The list is then rank-sorted:
-// written out for an unsplit row, or as the chunk's k largest, descending, for the merge.
+// adversarial orders) is pushed again in index order with a prune whenever the list passes kTileKeep. The list is
+// then rank-sorted and written out for an unsplit row. A split row's chunk writes its k largest, descending, to the
+// workspace with device-coherent stores, waits for them to complete and counts its arrival on the row's counter; the
+// row's last arrival merges the lists (merge_lists) and zeroes the counter for the next launch -- no L2 write-back
+// or invalidate, and no second kernel.
 template <typename T, bool VEC>
 __global__ void __launch_bounds__(kThreads)
     topk_tile(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
-              u64* __restrict__ work, long long cols, long long chunk, int nchunks, int k) {
+              u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
+              int k) {
   __shared__ TileSmem s;
   const long long row = blockIdx.y;
   const int part = blockIdx.x;
   const int begin = (int)((long long)part * chunk);
   const int end = (int)(begin + chunk < cols ? begin + chunk : cols);
   const T* xr = x + row * cols;
-  BlockRed red{s.red, 0};
-  TileList L{s.seg[wave_id()], 0};
+  BlockRed red;  // fields assigned at run time (an aggregate initializer of LDS addresses does not compile)
+  red.slot = s.red;
+  red.phase = 0;
+  TileList L;
+  L.seg = s.seg[wave_id()];
+  L.cnt = 0;
   uint32_t thr = 0;
   const int kw = (k + kWaves - 1) / kWaves;
   using TL = Tile<T, VEC>;
   constexpr int TE = kThreads * kTileE;
-  for (int t0 = begin; t0 < end; t0 += TE) {
-    TL tile;
-    tile.b0 = t0;
-    tile.b1 = end - t0 > TE ? t0 + TE : end;
-    tile.load(xr);
+  auto process = [&](TL& tile, bool more) __attribute__((always_inline)) {
+    tile.prepare();
     uint32_t m = 0;
     bool has = false;
 #pragma unroll
@@ -849,66 +951,42 @@ __global__ void __launch_bounds__(kThreads)
           for (int j = g; j < g + 4; ++j) L.push(tile.comp(v, j), tile.valid(v, j) && tile.key(v, j) >= thr);
         }
       }
-    const u64 kth = L.settle(red, k, cnt0, TL::NV, (u64)thr << 32,
-                             [&](int v, const u64& floor, const auto& check) { tile.push_first(L, v, floor, check); });
+    int total = 0;
+    u64 kth = L.settle(
+        red, k, cnt0, TL::NV, (u64)thr << 32,
+        [&](int v, const u64& floor, const auto& check) { tile.push_first(L, v, floor, check); }, total);
+    // before another tile, keep the list near k so that it admits less: the list's k-th raises the admission key
+    if (more && total > 2 * k) kth = prune_ranked(s, L, k);
     const uint32_t kk = (uint32_t)(kth >> 32);
     thr = kk > thr ? kk : thr;
-  }
-  finish_list<T>(s, L, values, indices, work + (row * nchunks + part) * (long long)k, row, k, nchunks == 1);
-}
-
-// k <= 64 merge, one 256-thread workgroup per split row. Every chunk list holds its chunk's k largest, descending, so
-// the first h = ceil(k / nchunks) entries of the lists give nchunks * h >= k distinct composites: the k-th largest of
-// these heads bounds the row's k-th from below and, the row's top k being spread over the chunks, admits little
-// beyond the answer. The lists are then streamed through the list from that floor, settled as in topk_tile.
-template <typename T>
-__global__ void __launch_bounds__(kThreads)
-    topk_tile_merge(void* __restrict__ values, long long* __restrict__ indices, const u64* __restrict__ work,
-                    int nchunks, int k) {
-  __shared__ TileSmem s;
-  const long long row = blockIdx.x;
-  const u64* wr = work + row * (long long)nchunks * k;
-  const int t = threadIdx.x;
-  BlockRed red{s.red, 0};
-  TileList L{s.seg[wave_id()], 0};
-  const int h = (k + nchunks - 1) / nchunks;
-  const int nh = h * nchunks;
-  constexpr int PER = 8;
-  const int total = nchunks * k;
-  u64 c[PER];
-  auto load = [&](int base) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int at = base + i * kThreads + t;
-      c[i] = at < total ? wr[at] : 0ull;
-    }
   };
-  load(0);  // in flight together with the heads
-  u64 floor = 1;
-  if (nh <= kTileSort) {
-    const u64 hv = t < nh ? wr[(long long)(t / h) * k + t % h] : 0ull;
-    s.sorted[t] = hv;  // zero past nh: the padding rank_in reads
-    const int real = (int)red.sum((uint32_t)__popcll(__ballot(hv != 0)));
-    if (real >= k) {
-      if (hv != 0 && rank_in(s.sorted, (nh + 15) & ~15, hv) == k - 1) s.pick = hv;
-      __syncthreads();
-      floor = s.pick;
-    }
+  // One register tile at a time, all of its loads in flight at once (the workgroups resident on a CU keep the memory
+  // busy while one of them computes; a second register tile per workgroup halves the resident workgroups and was
+  // slower).
+  for (int t0 = begin; t0 < end; t0 += TE) {
+    TL tile;
+    tile.load(xr, t0, end);
+    process(tile, end - t0 > TE);
   }
-  for (int base = 0; base < total; base += kThreads * PER) {
-    if (base > 0) load(base);
-    const int cnt0 = L.cnt;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) L.push(c[i], c[i] >= floor);
-    const u64 kth = L.settle(red, k, cnt0, PER, floor, [&](int, const u64& f, const auto& check) {
-      L.push(c[0], c[0] >= f);
-      check();
-#pragma unroll
-      for (int i = 0; i + 1 < PER; ++i) c[i] = c[i + 1];
-    });
-    floor = kth > floor ? kth : floor;
+  if (nchunks == 1) {
+    finish_list<T>(s, L, values, indices, nullptr, row, k, true);
+    return;
   }
-  finish_list<T>(s, L, values, indices, nullptr, row, k, true);
+  u64* wr = work + row * (long long)nchunks * k;
+  finish_list<T>(s, L, values, indices, wr + (long long)part * k, row, k, false);
+  // hand-off: the chunk list is device-visible before its arrival is counted; the row's last arrival merges the lists
+  // and zeroes the row's counter for the next launch
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old = __hip_atomic_fetch_add(counters + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s.last = old == (unsigned)nchunks - 1;
+  }
+  __syncthreads();
+  if (!s.last) return;
+  L.cnt = 0;
+  merge_lists<T>(s, red, L, values, indices, wr, row, nchunks, k);
+  if (threadIdx.x == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- merge kernel ----------------------------------------------------------------------------------------------------
@@ -969,14 +1047,16 @@ int lane_elems() {
 }
 
 template <typename T, bool VEC>
-int launch_chunks(const void* x, void* values, void* indices, void* work, long long rows, long long cols,
-                  long long chunk, int nchunks, int k, hipStream_t stream) {
+int launch_chunks(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
+                  long long cols, long long chunk, int nchunks, int k, hipStream_t stream) {
   const dim3 grid((unsigned)nchunks, (unsigned)rows);
   const int e = VEC ? lane_elems() : 16;
-  if (k <= kSeedMaxK)
+  if (k <= kSeedMaxK) {
     hipLaunchKernelGGL((topk_tile<T, VEC>), grid, dim3(kThreads), 0, stream, (const T*)x, values, (long long*)indices,
-                       (u64*)work, cols, chunk, nchunks, k);
-  else if (e == 16)
+                       (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k);
+    return (int)hipGetLastError();
+  }
+  if (e == 16)
     hipLaunchKernelGGL((topk_chunks<T, VEC, 16>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
                        (long long*)indices, (u64*)work, cols, chunk, nchunks, k);
   else if (e == 64)
@@ -985,14 +1065,9 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, long l
   else
     hipLaunchKernelGGL((topk_chunks<T, VEC, 32>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
                        (long long*)indices, (u64*)work, cols, chunk, nchunks, k);
-  if (nchunks > 1) {
-    if (k <= kSeedMaxK)
-      hipLaunchKernelGGL((topk_tile_merge<T>), dim3((unsigned)rows), dim3(kThreads), 0, stream, values,
-                         (long long*)indices, (const u64*)work, nchunks, k);
-    else
-      hipLaunchKernelGGL((topk_merge<T>), dim3((unsigned)rows), dim3(kThreads), 0, stream, values,
-                         (long long*)indices, (const u64*)work, nchunks, k);
-  }
+  if (nchunks > 1)
+    hipLaunchKernelGGL((topk_merge<T>), dim3((unsigned)rows), dim3(kThreads), 0, stream, values, (long long*)indices,
+                       (const u64*)work, nchunks, k);
   return (int)hipGetLastError();
 }
 
@@ -1034,13 +1109,13 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
 
 // topk/kernel.cu:549 `launch`: values [rows, k] in x's dtype and int64 indices [rows, k], sorted descending with ties
 // by the lowest index. work: u64 [rows * nchunks * k] with nchunks = ceil(cols / chunk), used when nchunks > 1;
-// counters: u32 [>= rows], zero on entry and left zero (the two-kernel hand-off does not touch them). Checks as the
+// counters: u32 [>= rows], zero on entry and zero again when the launch completes (the k <= 64 kernel counts each
+// split row's chunk arrivals there, as the reference's). Checks as the
 // reference's, except that k may be up to 1024 (the reference stops at 512): rows <= 0 or k <= 0 is a no-op; -1 for
 // k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0, a split row with chunk % 4 or
 // nchunks * k > INT_MAX / 2, threads not 128, 256 or 512, depth not 2, 4 or 8, or a dtype other than 0 and 1.
 extern "C" int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
                       long long cols, int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream) {
-  (void)counters;
   if (rows <= 0 || k <= 0) return rw_host::kOk;
   if (k > cols || k > kMaxK || cols > INT_MAX / 2 || rows > 65535 || chunk <= 0) return rw_host::kInvalid;
   const long long nchunks = (cols + chunk - 1) / chunk;
@@ -1049,19 +1124,19 @@ extern "C" int launch(const void* x, void* values, void* indices, void* work, vo
     return rw_host::kInvalid;
   if (dtype == 0) {
     if (cols % 4 == 0 && rw_host::aligned16(x))
-      return launch_chunks<float, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
-    return launch_chunks<float, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
+      return launch_chunks<float, true>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
+    return launch_chunks<float, false>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
   }
   if (dtype == 1) {
     if (cols % 8 == 0 && (chunk % 8 == 0 || nchunks == 1) && rw_host::aligned16(x))
-      return launch_chunks<uint16_t, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
-    return launch_chunks<uint16_t, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
+      return launch_chunks<uint16_t, true>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
+    return launch_chunks<uint16_t, false>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
   }
   return rw_host::kInvalid;
 }
 
 // No counterpart in the reference (whose counters self-reset only when a launch completes): zeroes counters[0, rows)
-// on `stream`. This build leaves the counters untouched, so the call only restores a caller's invariant.
+// on `stream`, for a caller recovering from a launch that did not complete.
 extern "C" int topk_reset(void* counters, long long rows, hipStream_t stream) {
   if (rows <= 0) return rw_host::kOk;
   if (!counters) return rw_host::kInvalid;

@@ -65,7 +65,7 @@ def _plan(x, rows, cols, dtype, k=K):
         return _last
     _last = None
     # larger k: larger chunks (fewer lists of k to merge per row)
-    chunk = _lib.plan(rows, cols, dtype, _THREADS, _DEPTH, max(_MIN_CHUNK, 16 * k) if k > 64 else _MIN_CHUNK)
+    chunk = _lib.plan(rows, cols, dtype, _THREADS, _DEPTH, max(_MIN_CHUNK, 32 * k) if k > 64 else _MIN_CHUNK)
     nchunks = -(-cols // chunk)
     work = torch.empty(rows * nchunks * k if nchunks > 1 else 1, dtype=torch.int64, device=x.device)
     counters = _row_counters(x.device, rows)

@@ -17,8 +17,9 @@ extern "C" {
 long long plan(long long rows, long long cols, int dtype, int threads, int depth, int min_chunk);
 
 /* topk/kernel.cu:549: values [rows, k] in x's dtype, indices [rows, k] int64; work: u64 [rows * nchunks * k]
- * (nchunks = ceil(cols / chunk), only used when nchunks > 1); counters: u32 [>= rows], zero on entry, left zero (the
- * chunk lists are merged by a second kernel in stream order, so this build does not touch them).
+ * (nchunks = ceil(cols / chunk), only used when nchunks > 1); counters: u32 [>= rows], zero on entry and zero again
+ * when the launch completes (for k <= 64 a split row's chunks count their arrivals there and the last one merges, as
+ * in the reference).
  * Returns 0 (rows <= 0 or k <= 0 is a no-op), -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0,
  * a split row with chunk % 4 != 0 or nchunks * k > INT_MAX / 2, threads not 128/256/512, depth not 2/4/8 or an unknown
  * dtype, otherwise the hipError_t of the launch. Launches sharing work/counters must be ordered (one stream). */
