@@ -44,7 +44,7 @@ TRAFFIC_PATH = os.path.join(ROOT, "profiles", "traffic.json")
 # it are summed (the whole launch for the two-kernel paths)
 KERNELS = {"rmsnorm_16384x4096": "rmsnorm_rows", "softmax_4096x4096": "softmax_rows",
            "softmax_64x262144": "softmax_split", "rope_4x4096_32q_8kv_128": "rope_vec",
-           "topk_128x128256_k50": "topk_tile"}
+           "topk_128x128256_k50": "topk_tile", "rmsnorm_add_16384x4096": "rmsnorm_rows"}
 
 
 def parse():
@@ -86,6 +86,20 @@ class Case:
                 y = torch.empty_like(x)
                 return lambda: lib.launch(x.data_ptr(), y.data_ptr(), rows, cols, 0, 256, 1024, stream())
             footprint = 2 * inp["x"].numel() * 4
+        elif name.startswith("rmsnorm_add"):
+            lib = pkg.candidate("rmsnorm")._lib
+            rows, cols = inp["x"].shape
+            eps = inp["eps"]
+            wt = inp["weight"].to(dev)
+            self.dtype = "bf16"
+
+            def make():
+                # in place, as a decoder layer does: the residual stream is overwritten with x + residual
+                x, r = inp["x"].to(dev), inp["residual"].to(dev)
+                y = torch.empty_like(x)
+                return lambda: lib.rmsnorm_add_launch(x.data_ptr(), r.data_ptr(), wt.data_ptr(), y.data_ptr(),
+                                                      r.data_ptr(), rows, cols, 1, eps, 256, stream())
+            footprint = 3 * inp["x"].numel() * 2
         elif name.startswith("rmsnorm"):
             lib = pkg.candidate("rmsnorm")._lib
             rows, cols = inp["x"].shape

@@ -53,6 +53,16 @@ def rmsnorm(x, weight=None, eps=1e-6):
     return candidate("rmsnorm").run(inputs)["y"]
 
 
+def rmsnorm_add(x, residual, weight=None, eps=1e-6, inplace=False):
+    """Fused residual add + RMSNorm: returns (y, h) with h = x + residual (written over residual when inplace) and
+    y = rmsnorm(h), times weight when given."""
+    inputs = {"x": x, "residual": residual, "eps": eps, "inplace": inplace}
+    if weight is not None:
+        inputs["weight"] = weight
+    out = candidate("rmsnorm").run(inputs)
+    return out["y"], out["residual"]
+
+
 def rope(q, k, position_ids, cos=None, sin=None, inv_freq=None, inplace=False):
     """RoPE of q [B, S, Hq, D] and k [B, S, Hk, D]: from a cos/sin cache, or on the fly from inv_freq."""
     inputs = {"q": q, "k": k, "position_ids": position_ids, "inplace": inplace}

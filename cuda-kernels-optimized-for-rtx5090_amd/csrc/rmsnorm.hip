@@ -6,6 +6,8 @@
 //   inv  = T(rsqrt(float(sum) / cols + eps))            (fp32 mean and eps, rsqrt rounded to x's dtype)
 //   y    = T(x * inv)                                   (one round to nearest even; the product is exact in fp32)
 //   y    = T(w * y)                                     (weighted entry only: torch's `w * y` on dtype tensors)
+// The fused residual entry (`rmsnorm_add_launch`) first forms h = T(x + residual), writes it to residual_out and
+// normalizes h as above: torch's `h = x + residual; y = rmsnorm(h)` on dtype tensors, one pass over memory.
 // The squares are summed in fp64, which makes the sum exact to far below fp32 resolution, so float(sum) is the
 // correctly rounded fp32 sum and does not depend on the summation order; rsqrt is evaluated in fp64 and rounded to
 // fp32 (the correctly rounded fp32 rsqrt). The reference's fp32 sum and rsqrtf are within an fp32 ulp or two of these
@@ -89,12 +91,33 @@ __device__ __forceinline__ void norm_row(const Regs<NV>& r, const Regs<NV>& w, v
   }
 }
 
+// Fused residual: r becomes h = T(x + residual), which is written to res_out (the lane's own vectors: res_out may be
+// residual, and y may be x).
+template <typename T, int G, int NV, bool FULL, bool NTS>
+__device__ __forceinline__ void add_residual(Regs<NV>& r, const Regs<NV>& res, void* res_out, long long row,
+                                             long long nvec, int t, bool active) {
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float a[T::V], b[T::V];
+    unpack<T>(r.v[k], a);
+    unpack<T>(res.v[k], b);
+#pragma unroll
+    for (int e = 0; e < T::V; ++e) a[e] = a[e] + b[e];
+    r.v[k] = pack<T>(a);
+    const long long i = (long long)k * G + t;
+    if (active && (FULL || i < nvec)) store16<NTS>(res_out, row * nvec + i, r.v[k]);
+  }
+}
+
 // Row kernel. A block is max(WAVES, 4) waves; GROUPS = block waves / WAVES groups walk their own rows with a uniform
 // trip count (a group past the last row loads an in-bounds row and stores nothing). Two LDS slot arrays alternate
 // between consecutive rows, so a slot is never rewritten before the barrier of the next reduction.
-template <typename T, int WAVES, int NV, bool FULL, bool HAS_W, bool NTL, bool NTS>
+// With RES the group also loads the residual rows, forms h = T(x + residual) and writes it to res_out before the
+// normalisation (x and y, and residual and res_out, may be the same buffers: a lane reads its vectors before it
+// writes them).
+template <typename T, int WAVES, int NV, bool FULL, bool HAS_W, bool RES, bool NTL, bool NTS>
 __global__ void __launch_bounds__((WAVES < 4 ? 4 : WAVES) * 64)
-    rmsnorm_rows(const void* __restrict__ x, const void* __restrict__ w, void* __restrict__ y, long long rows,
+    rmsnorm_rows(const void* x, const void* res, const void* __restrict__ w, void* y, void* res_out, long long rows,
                  long long nvec, int cols, float eps) {
   constexpr int BW = WAVES < 4 ? 4 : WAVES;
   constexpr int GROUPS = BW / WAVES;
@@ -111,16 +134,26 @@ __global__ void __launch_bounds__((WAVES < 4 ? 4 : WAVES) * 64)
   if constexpr (HAS_W) load_vectors<G, NV, FULL, false>(wr, w, 0, nvec, t);
   long long ra = base + wave / WAVES;
   Regs<NV> a, b;
+  Regs<RES ? NV : 1> ea, eb;  // residual rows
   load_vectors<G, NV, FULL, NTL>(a, x, (ra < rows ? ra : last) * nvec, nvec, t);
+  if constexpr (RES) load_vectors<G, NV, FULL, NTL>(ea, res, (ra < rows ? ra : last) * nvec, nvec, t);
   while (true) {
     const long long rb = ra + step;
     load_vectors<G, NV, FULL, NTL>(b, x, (rb < rows ? rb : last) * nvec, nvec, t);
+    if constexpr (RES) {
+      load_vectors<G, NV, FULL, NTL>(eb, res, (rb < rows ? rb : last) * nvec, nvec, t);
+      add_residual<T, G, NV, FULL, NTS>(a, ea, res_out, ra, nvec, t, ra < rows);
+    }
     norm_row<T, WAVES, NV, FULL, HAS_W, NTS>(a, wr, y, ra, nvec, cols, eps, t, ra < rows, slots[0], wave, first);
     base += step;
     if (base >= rows) break;
     ra = rb;
     const long long rc = ra + step;
     load_vectors<G, NV, FULL, NTL>(a, x, (rc < rows ? rc : last) * nvec, nvec, t);
+    if constexpr (RES) {
+      load_vectors<G, NV, FULL, NTL>(ea, res, (rc < rows ? rc : last) * nvec, nvec, t);
+      add_residual<T, G, NV, FULL, NTS>(b, eb, res_out, ra, nvec, t, ra < rows);
+    }
     norm_row<T, WAVES, NV, FULL, HAS_W, NTS>(b, wr, y, ra, nvec, cols, eps, t, ra < rows, slots[1], wave, first);
     base += step;
     if (base >= rows) break;
@@ -129,24 +162,30 @@ __global__ void __launch_bounds__((WAVES < 4 ? 4 : WAVES) * 64)
 }
 
 // Generic kernel: any row length and alignment, one 256-thread block per row (grid-strided), two scalar passes.
-template <typename T, bool HAS_W>
+// With RES, pass 1 writes h = T(x + residual) to res_out and pass 2 reads h back (the thread's own elements).
+template <typename T, bool HAS_W, bool RES>
 __global__ void __launch_bounds__(256)
-    rmsnorm_generic(const void* __restrict__ x, const void* __restrict__ w, void* __restrict__ y, long long rows,
-                    int cols, float eps) {
+    rmsnorm_generic(const void* x, const void* res, const void* __restrict__ w, void* y, void* res_out,
+                    long long rows, int cols, float eps) {
   __shared__ double slots[2][4];
   const int wave = wave_id();
   int parity = 0;
+  const void* src = RES ? (const void*)res_out : x;
   for (long long row = blockIdx.x; row < rows; row += gridDim.x, parity ^= 1) {
     const long long o = row * (long long)cols;
     double acc = 0.0;
     for (int j = threadIdx.x; j < cols; j += 256) {
-      const float f = load_elem<T>(x, o + j);
+      float f = load_elem<T>(x, o + j);
+      if constexpr (RES) {
+        f = round_to<T>(f + load_elem<T>(res, o + j));
+        store_elem<T>(res_out, o + j, f);
+      }
       acc += (double)(f * f);
     }
     acc = group_reduce<4>(acc, OpSum{}, slots[parity], wave, 0);
     const float inv = row_inv<T>(acc, cols, eps);
     for (int j = threadIdx.x; j < cols; j += 256) {
-      float v = load_elem<T>(x, o + j) * inv;
+      float v = load_elem<T>(src, o + j) * inv;
       if constexpr (HAS_W) v = load_elem<T>(w, j) * round_to<T>(v);
       store_elem<T>(y, o + j, v);
     }
@@ -179,6 +218,8 @@ struct Args {
   const void* x;
   const void* w;
   void* y;
+  const void* res;
+  void* res_out;
   long long rows;
   long long nvec;
   int cols;
@@ -186,11 +227,11 @@ struct Args {
   hipStream_t stream;
 };
 
-template <typename T, int WAVES, int NV, bool FULL, bool HAS_W, bool NTL>
+template <typename T, int WAVES, int NV, bool FULL, bool HAS_W, bool RES, bool NTL>
 int launch_k(const Args& a) {
   constexpr int BW = WAVES < 4 ? 4 : WAVES;
   constexpr int GROUPS = BW / WAVES;
-  auto kern = rmsnorm_rows<T, WAVES, NV, FULL, HAS_W, NTL, true>;
+  auto kern = rmsnorm_rows<T, WAVES, NV, FULL, HAS_W, RES, NTL, true>;
   static int occ = 0;
   if (occ <= 0) occ = blocks_per_cu(kern, BW * kWave);
   // about 8 resident waves per CU by default (more waves only contend for the memory queues; measured on MI355X)
@@ -200,44 +241,45 @@ int launch_k(const Args& a) {
   const long long need = (a.rows + GROUPS - 1) / GROUPS;
   long long grid = (long long)rw_host::device_cus() * per_cu;
   if (grid > need) grid = need;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(BW * kWave), 0, a.stream, a.x, a.w, a.y, a.rows, a.nvec, a.cols,
-                     a.eps);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(BW * kWave), 0, a.stream, a.x, a.res, a.w, a.y, a.res_out, a.rows,
+                     a.nvec, a.cols, a.eps);
   return (int)hipGetLastError();
 }
 
-template <typename T, int WAVES, int NV, bool HAS_W, bool NTL>
+template <typename T, int WAVES, int NV, bool HAS_W, bool RES, bool NTL>
 int launch_nv(const Args& a) {
-  if (a.nvec == (long long)WAVES * kWave * NV) return launch_k<T, WAVES, NV, true, HAS_W, NTL>(a);
-  return launch_k<T, WAVES, NV, false, HAS_W, NTL>(a);
+  if (a.nvec == (long long)WAVES * kWave * NV) return launch_k<T, WAVES, NV, true, HAS_W, RES, NTL>(a);
+  return launch_k<T, WAVES, NV, false, HAS_W, RES, NTL>(a);
 }
 
-template <typename T, int WAVES, bool HAS_W, bool NTL>
+template <typename T, int WAVES, bool HAS_W, bool RES, bool NTL>
 int launch_w(int nv, const Args& a) {
   switch (nv) {
-    case 1: return launch_nv<T, WAVES, 1, HAS_W, NTL>(a);
-    case 2: return launch_nv<T, WAVES, 2, HAS_W, NTL>(a);
-    case 4: return launch_nv<T, WAVES, 4, HAS_W, NTL>(a);
-    case 8: return launch_nv<T, WAVES, 8, HAS_W, NTL>(a);
+    case 1: return launch_nv<T, WAVES, 1, HAS_W, RES, NTL>(a);
+    case 2: return launch_nv<T, WAVES, 2, HAS_W, RES, NTL>(a);
+    case 4: return launch_nv<T, WAVES, 4, HAS_W, RES, NTL>(a);
+    case 8: return launch_nv<T, WAVES, 8, HAS_W, RES, NTL>(a);
     default: return rw_host::kInvalid;
   }
 }
 
-template <typename T, bool HAS_W, bool NTL>
+template <typename T, bool HAS_W, bool RES, bool NTL>
 int launch_rows(int waves, int nv, const Args& a) {
   switch (waves) {
-    case 1: return launch_w<T, 1, HAS_W, NTL>(nv, a);
-    case 2: return launch_w<T, 2, HAS_W, NTL>(nv, a);
-    case 4: return launch_w<T, 4, HAS_W, NTL>(nv, a);
-    case 8: return launch_w<T, 8, HAS_W, NTL>(nv, a);
-    case 16: return launch_w<T, 16, HAS_W, NTL>(nv, a);
+    case 1: return launch_w<T, 1, HAS_W, RES, NTL>(nv, a);
+    case 2: return launch_w<T, 2, HAS_W, RES, NTL>(nv, a);
+    case 4: return launch_w<T, 4, HAS_W, RES, NTL>(nv, a);
+    case 8: return launch_w<T, 8, HAS_W, RES, NTL>(nv, a);
+    case 16: return launch_w<T, 16, HAS_W, RES, NTL>(nv, a);
     default: return rw_host::kInvalid;
   }
 }
 
-template <typename T, bool HAS_W>
-int launch_typed(const void* x, const void* w, void* y, long long rows, int cols, float eps, hipStream_t stream) {
+template <typename T, bool HAS_W, bool RES = false>
+int launch_typed(const void* x, const void* w, void* y, long long rows, int cols, float eps, hipStream_t stream,
+                 const void* res = nullptr, void* res_out = nullptr) {
   const bool vec = cols % T::V == 0 && rw_host::aligned16(x) && rw_host::aligned16(y) &&
-                   (!HAS_W || rw_host::aligned16(w));
+                   (!HAS_W || rw_host::aligned16(w)) && (!RES || (rw_host::aligned16(res) && rw_host::aligned16(res_out)));
   const long long nvec = cols / T::V;
   if (vec && rw_host::tune_get(kTuneGeneric) != 1 && nvec <= (long long)kMaxWaves * kWave * kMaxNv) {
     int waves = rw_host::tune_get(kTuneWaves), nv = rw_host::tune_get(kTuneNv);
@@ -249,16 +291,16 @@ int launch_typed(const void* x, const void* w, void* y, long long rows, int cols
     }
     if (nv <= 0) nv = pow2_at_least((nvec + (long long)waves * kWave - 1) / ((long long)waves * kWave));
     if ((long long)waves * kWave * nv >= nvec) {
-      const Args a{x, w, y, rows, nvec, cols, eps, stream};
+      const Args a{x, w, y, res, res_out, rows, nvec, cols, eps, stream};
       // non-temporal loads unless switched off (2): x is read once
-      return rw_host::tune_get(kTuneNtLoads) != 2 ? launch_rows<T, HAS_W, true>(waves, nv, a)
-                                                  : launch_rows<T, HAS_W, false>(waves, nv, a);
+      return rw_host::tune_get(kTuneNtLoads) != 2 ? launch_rows<T, HAS_W, RES, true>(waves, nv, a)
+                                                  : launch_rows<T, HAS_W, RES, false>(waves, nv, a);
     }
   }
   long long grid = (long long)rw_host::device_cus() * 8;
   if (grid > rows) grid = rows;
-  hipLaunchKernelGGL((rmsnorm_generic<T, HAS_W>), dim3((unsigned)grid), dim3(256), 0, stream, x, w, y, rows, cols,
-                     eps);
+  hipLaunchKernelGGL((rmsnorm_generic<T, HAS_W, RES>), dim3((unsigned)grid), dim3(256), 0, stream, x, res, w, y,
+                     res_out, rows, cols, eps);
   return (int)hipGetLastError();
 }
 
@@ -290,6 +332,23 @@ extern "C" int rmsnorm_launch_weighted(const void* x, const void* weight, void* 
   if (validate(rows, cols, threads)) return rw_host::kInvalid;
   if (dtype == 1) return launch_typed<BF16, true>(x, weight, y, rows, cols, eps, stream);
   if (dtype == 2) return launch_typed<F16, true>(x, weight, y, rows, cols, eps, stream);
+  return rw_host::kInvalid;
+}
+
+// Fused residual add + RMSNorm (no counterpart in the reference; the step before an inference layer's norm):
+// h = T(x + residual) is written to residual_out, then y = RMSNorm(h) (times weight when weight != nullptr), in one
+// pass: x and residual read once, residual_out and y written once. residual_out may be residual and y may be x (in
+// place). Same argument checks and return codes as `launch`; residual and residual_out must not be null.
+extern "C" int rmsnorm_add_launch(const void* x, const void* residual, const void* weight, void* y, void* residual_out,
+                                  long long rows, int cols, int dtype, float eps, int threads, hipStream_t stream) {
+  if (rows <= 0) return rw_host::kOk;
+  if (validate(rows, cols, threads) || !residual || !residual_out) return rw_host::kInvalid;
+  if (dtype == 1)
+    return weight ? launch_typed<BF16, true, true>(x, weight, y, rows, cols, eps, stream, residual, residual_out)
+                  : launch_typed<BF16, false, true>(x, nullptr, y, rows, cols, eps, stream, residual, residual_out);
+  if (dtype == 2)
+    return weight ? launch_typed<F16, true, true>(x, weight, y, rows, cols, eps, stream, residual, residual_out)
+                  : launch_typed<F16, false, true>(x, nullptr, y, rows, cols, eps, stream, residual, residual_out);
   return rw_host::kInvalid;
 }
 

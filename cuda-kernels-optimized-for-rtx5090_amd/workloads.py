@@ -25,6 +25,16 @@ def rmsnorm_16384x4096():
     return {"x": x, "weight": w, "eps": EPS}
 
 
+def rmsnorm_add_16384x4096():
+    """Fused residual add + RMSNorm bf16 (the step before a decoder layer's norm): x, residual [16384, 4096] ~ N(0, 1),
+    weight[4096] ~ U(0.5, 1.5), eps 1e-6, seed 2."""
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(16384, 4096, generator=g).bfloat16()
+    r = torch.randn(16384, 4096, generator=g).bfloat16()
+    w = (torch.rand(4096, generator=g) + 0.5).bfloat16()
+    return {"x": x, "residual": r, "weight": w, "eps": EPS}
+
+
 def rope_inv_freq(head_dim=128, theta=THETA):
     """HF/Llama inverse frequencies 1 / theta ** (arange(0, D, 2) / D), fp32."""
     return 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
@@ -63,6 +73,8 @@ def algorithmic_bytes(name, k=50):
         return 2 * 64 * 262144 * 4
     if name == "rmsnorm_16384x4096":
         return 2 * 16384 * 4096 * 2 + 4096 * 2
+    if name == "rmsnorm_add_16384x4096":
+        return 4 * 16384 * 4096 * 2 + 4096 * 2
     if name == "rope_4x4096_32q_8kv_128":
         return 2 * (4 * 4096 * 32 * 128 + 4 * 4096 * 8 * 128) * 2 + 4 * 4096 * 8
     if name == "topk_128x128256":
@@ -76,4 +88,5 @@ WORKLOADS = {
     "rope_4x4096_32q_8kv_128": rope_4x4096_32q_8kv_128,
     "softmax_64x262144": softmax_64x262144,
     "topk_128x128256": topk_128x128256,
+    "rmsnorm_add_16384x4096": rmsnorm_add_16384x4096,
 }

@@ -18,6 +18,13 @@ int launch(const void* x, void* y, long long rows, int cols, int dtype, float ep
 int rmsnorm_launch_weighted(const void* x, const void* weight, void* y, long long rows, int cols, int dtype,
                             float eps, int threads, hipStream_t stream);
 
+/* No counterpart in the reference (the step before an inference layer's norm, SURVEY "next"): fused residual add.
+ * h = T(x + residual) is written to residual_out, then y = RMSNorm(h), times weight when weight != NULL, in one pass
+ * (x and residual read once, residual_out and y written once). residual_out may equal residual and y may equal x.
+ * Same checks and codes as launch(); residual or residual_out NULL is -1. */
+int rmsnorm_add_launch(const void* x, const void* residual, const void* weight, void* y, void* residual_out,
+                       long long rows, int cols, int dtype, float eps, int threads, hipStream_t stream);
+
 /* No counterpart in the reference: tuning override for parameter sweeps. Slots: 0 waves per row, 1 vectors per lane,
  * 2 resident blocks per CU, 3 forced generic kernel (1), 4 non-temporal loads (default on; 2 off). Returns 0 or -1. */
 int rmsnorm_tune(int slot, int value);

@@ -37,6 +37,7 @@ def lib():
         vp, ll, i, f = ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_float
         L.oracle_softmax.argtypes = [vp, vp, ll, ll, i]
         L.oracle_rmsnorm.argtypes = [vp, vp, vp, ll, ll, i, f, vp]
+        L.oracle_rmsnorm_add.argtypes = [vp, vp, vp, vp, vp, ll, ll, i, f]
         L.oracle_rope_cache.argtypes = [vp, vp, vp, vp, vp, vp, vp, ll, i, i, i, i, i]
         L.oracle_rope_freq.argtypes = [vp, vp, vp, vp, vp, vp, ll, i, i, i, i]
         L.oracle_rope_table.argtypes = [vp, ll, i, vp, vp]
@@ -88,6 +89,17 @@ def rmsnorm(x, weight=None, eps=1e-6, dtype="bf16", return_inv=False):
     inv = np.empty(rows, dtype=np.float32)
     lib().oracle_rmsnorm(_ptr(x), _ptr(w), _ptr(y), rows, cols, NORM_DTYPES[dtype], ctypes.c_float(eps), _ptr(inv))
     return (y, inv) if return_inv else y
+
+
+def rmsnorm_add(x, residual, weight=None, eps=1e-6, dtype="bf16"):
+    """Fused residual add + RMSNorm on uint16 bits: returns (y, h) with h = T(x + residual) and y = rmsnorm(h)."""
+    x, r = _c(x, np.uint16), _c(residual, np.uint16)
+    w = _c(weight, np.uint16) if weight is not None else None
+    y, h = np.empty_like(x), np.empty_like(x)
+    rows, cols = x.shape
+    lib().oracle_rmsnorm_add(_ptr(x), _ptr(r), _ptr(w), _ptr(y), _ptr(h), rows, cols, NORM_DTYPES[dtype],
+                             ctypes.c_float(eps))
+    return y, h
 
 
 def rope_cache(q, k, cos, sin, ids, dtype="bf16", cache_dtype="fp32"):

@@ -140,6 +140,16 @@ void oracle_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, long long
   }
 }
 
+/* Fused residual add + RMSNorm (no counterpart in the reference; its torch statement on dtype tensors is
+ * `h = x + residual; y = w * T(h * inv(h))`): h = T(fp32(x) + fp32(residual)) is written to h_out, then y is
+ * oracle_rmsnorm of h. x, residual, h_out and y are [rows, cols] bits of the dtype. */
+void oracle_rmsnorm_add(const uint16_t* x, const uint16_t* res, const uint16_t* w, uint16_t* y, uint16_t* h_out,
+                        long long rows, long long cols, int dtype, float eps) {
+  const int fmt = dtype == 2 ? 2 : 1;
+  for (long long i = 0; i < rows * cols; ++i) store_fmt(h_out, i, load_fmt(x, i, fmt) + load_fmt(res, i, fmt), fmt);
+  oracle_rmsnorm(h_out, w, y, rows, cols, dtype, eps, 0);
+}
+
 /* ---- RoPE (rope/kernel.cu:1-11, :73-79, :119-126; rope/candidate.py:3-5) ---------------------------------------------
  * For each token, head and i < h = D/2, with a = x[i], b = x[i + h] of the head:
  *   out[i]     = T(fp32(fp32(a * c1) - fp32(b * s1)))

@@ -24,6 +24,12 @@ def rmsnorm(x, weight=None, eps=1e-6):
     return y if weight is None else weight * y
 
 
+def rmsnorm_add(x, residual, weight=None, eps=1e-6):
+    """Fused residual add + RMSNorm as torch eager evaluates it on dtype tensors: h = x + residual, y = rmsnorm(h)."""
+    h = x + residual
+    return rmsnorm(h, weight, eps), h
+
+
 def inv_freq(head_dim, theta=10000.0):
     """The HF/Llama inverse frequencies: 1 / theta ** (arange(0, D, 2) / D) in fp32."""
     return 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))

@@ -103,3 +103,46 @@ def test_tuning_overrides_keep_results(pkg, oracle, dev):
     finally:
         for slot in range(5):
             lib.rmsnorm_tune(slot, 0)
+
+
+def check_add(pkg, oracle, dev, x, r, w, eps=1e-6, what="", inplace=False):
+    print(f"[rmsnorm_add] {what} {tuple(x.shape)} {x.dtype} weight={w is not None} inplace={inplace}", flush=True)
+    rd = r.to(dev)
+    y, h = pkg.rmsnorm_add(x.to(dev), rd, None if w is None else w.to(dev), eps, inplace=inplace)
+    ry, rh = oracle.rmsnorm_add(bits16(x), bits16(r), None if w is None else bits16(w), eps, DT[x.dtype])
+    assert np.array_equal(bits16(h), rh), f"{what}: h differs"
+    assert same_bits16(bits16(y), ry, x.dtype == torch.float16), f"{what}: y differs (max {ulp16(bits16(y), ry).max()})"
+    if inplace:
+        assert h.data_ptr() == rd.data_ptr() and np.array_equal(bits16(rd), rh)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,cols", [(1, 8), (5, 1000), (17, 4096), (4, 4104), (2, 32768), (3, 1001), (1000, 2048)])
+def test_fused_residual_shapes(pkg, oracle, dev, dtype, rows, cols):
+    g = torch.Generator().manual_seed(rows * 7919 + cols)
+    x = torch.randn(rows, cols, generator=g).to(dtype)
+    r = (torch.randn(rows, cols, generator=g) * 2).to(dtype)
+    w = (torch.rand(cols, generator=g) + 0.5).to(dtype)
+    check_add(pkg, oracle, dev, x, r, None, what=f"{rows}x{cols}")
+    check_add(pkg, oracle, dev, x, r, w, what=f"{rows}x{cols} weighted", inplace=True)
+
+
+def test_fused_residual_generic_and_special(pkg, oracle, dev):
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(6, 4096, generator=g).bfloat16()
+    r = torch.randn(6, 4096, generator=g).bfloat16()
+    r[1, 3] = float("nan")
+    r[2, :] = -x[2, :]  # h = 0: inv = rsqrt(eps), y = 0
+    check_add(pkg, oracle, dev, x, r, None, what="special")
+    lib = pkg.candidate("rmsnorm")._lib
+    try:
+        lib.rmsnorm_tune(3, 1)  # the generic two-pass kernel, in place
+        check_add(pkg, oracle, dev, x, r, None, what="generic", inplace=True)
+    finally:
+        lib.rmsnorm_tune(3, 0)
+
+
+def test_config_rmsnorm_add_16384x4096(pkg, oracle, dev):
+    inp = pkg.workloads.rmsnorm_add_16384x4096()
+    check_add(pkg, oracle, dev, inp["x"], inp["residual"], inp["weight"], inp["eps"], "rmsnorm_add_16384x4096",
+              inplace=True)

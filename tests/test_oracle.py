@@ -133,6 +133,27 @@ def test_rmsnorm_closed_forms(oracle):
     assert (from_bits16(oracle.rmsnorm(bits16(big)), torch.bfloat16) == 0).all()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rmsnorm_add_matches_torch_path(oracle, dtype):
+    """Fused residual add: h is torch's dtype sum bit for bit; y is RMSNorm of h under the same rule as above."""
+    from oracle import torch_paths
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(300, 512, generator=g).to(dtype)
+    r = (torch.randn(300, 512, generator=g) * 4).to(dtype)
+    w = (torch.rand(512, generator=g) + 0.5).to(dtype)
+    name = "bf16" if dtype == torch.bfloat16 else "fp16"
+    for weight in (None, w):
+        y, h = oracle.rmsnorm_add(bits16(x), bits16(r), None if weight is None else bits16(weight), 1e-6, name)
+        ty, th = torch_paths.rmsnorm_add(x, r, weight)
+        assert np.array_equal(h, bits16(th))
+        assert np.array_equal(y, _check_rms_against_torch(oracle, th, weight, name))
+    # a zero residual is plain RMSNorm; x + (-x) is a zero row (inv = rsqrt(eps), y = 0)
+    y, h = oracle.rmsnorm_add(bits16(x), bits16(torch.zeros_like(x)), bits16(w), 1e-6, name)
+    assert np.array_equal(y, oracle.rmsnorm(bits16(x), bits16(w), 1e-6, name)) and np.array_equal(h, bits16(x))
+    y, h = oracle.rmsnorm_add(bits16(x), bits16(-x), None, 1e-6, name)
+    assert not from_bits16(h, dtype).float().abs().any() and not from_bits16(y, dtype).float().abs().any()
+
+
 def test_rmsnorm_golden(oracle):
     f = golden("rmsnorm")
     y = oracle.rmsnorm(f["x"], f["w"], 1e-6, "bf16")
