@@ -44,7 +44,8 @@ TRAFFIC_PATH = os.path.join(ROOT, "profiles", "traffic.json")
 # it are summed (the whole launch for the two-kernel paths)
 KERNELS = {"rmsnorm_16384x4096": "rmsnorm_rows", "softmax_4096x4096": "softmax_rows",
            "softmax_64x262144": "softmax_split", "rope_4x4096_32q_8kv_128": "rope_vec",
-           "topk_128x128256_k50": "topk_tile", "rmsnorm_add_16384x4096": "rmsnorm_rows"}
+           "topk_128x128256_k50": "topk_tile", "rmsnorm_add_16384x4096": "rmsnorm_rows",
+           "rope_kv_4x4096_32q_8kv_128": "rope_vec"}
 
 
 def parse():
@@ -113,6 +114,22 @@ class Case:
                 return lambda: lib.rmsnorm_launch_weighted(x.data_ptr(), wt.data_ptr(), y.data_ptr(), rows, cols, 1,
                                                            eps, 256, stream())
             footprint = 2 * inp["x"].numel() * 2
+        elif name.startswith("rope_kv"):
+            lib = pkg.candidate("rope")._lib
+            B, S, Hq, D = inp["q"].shape
+            Hk = inp["k"].shape[2]
+            pos, inv = inp["position_ids"].to(dev), inp["inv_freq"].to(dev)
+            slots = inp["slot_mapping"].to(dev)
+            self.dtype = "bf16"
+
+            def make():
+                # q rotated in place; k, v read; the cache rows written
+                q, kk, v = inp["q"].to(dev), inp["k"].to(dev), inp["v"].to(dev)
+                kc, vc = inp["k_cache"].to(dev), inp["v_cache"].to(dev)
+                return lambda: lib.rope_kv_launch(q.data_ptr(), kk.data_ptr(), v.data_ptr(), pos.data_ptr(),
+                                                  inv.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                                  slots.data_ptr(), B * S, Hq, Hk, D, 1, stream())
+            footprint = (inp["q"].numel() + 4 * inp["k"].numel()) * 2
         elif name.startswith("rope"):
             lib = pkg.candidate("rope")._lib
             B, S, Hq, D = inp["q"].shape

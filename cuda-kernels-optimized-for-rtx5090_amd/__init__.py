@@ -74,6 +74,15 @@ def rope(q, k, position_ids, cos=None, sin=None, inv_freq=None, inplace=False):
     return out["q_out"], out["k_out"]
 
 
+def rope_kv(q, k, v, position_ids, inv_freq, k_cache, v_cache, slot_mapping, inplace=False):
+    """RoPE fused with the KV-cache write: returns q_out; the rotated k and v land in the cache rows slot_mapping
+    picks ([slots, Hk, D] caches, updated in place; a negative slot writes nothing)."""
+    out = candidate("rope").run({"q": q, "k": k, "v": v, "position_ids": position_ids, "inv_freq": inv_freq,
+                                 "k_cache": k_cache, "v_cache": v_cache, "slot_mapping": slot_mapping,
+                                 "inplace": inplace})
+    return out["q_out"]
+
+
 def topk(x, k=50):
     """The k largest entries of each row of a 2-D fp32/bf16 x, sorted descending, ties by lowest index."""
     out = candidate("topk").run({"x": x, "k": k})

@@ -6,7 +6,9 @@ bf16 (1) or fp16 (2), position_ids int64 [B, S], cos/sin [P, D] in fp32 (0), bf1
 reference ABI's `launch`. Two extensions:
   - inputs["inv_freq"] (fp32 [D/2]) in place of cos/sin: cos/sin are computed on the fly from the positions
     (`rope_launch_freq`), equal to a cache built from inv_freq with fp32 angles;
-  - inputs["inplace"] = True: q and k are rotated in place and returned as q_out and k_out.
+  - inputs["inplace"] = True: q and k are rotated in place and returned as q_out and k_out;
+  - inputs "v", "k_cache", "v_cache", "slot_mapping" (with inv_freq): RoPE fused with the KV-cache write
+    (`rope_kv_launch`): q rotated, the rotated k and v written to the cache rows [slots, Hk, D] the slots pick.
 Tensors are passed contiguous (an in-place call needs q and k contiguous already). params.json (optional) may set
 "rows" and "splits", the reference ABI's block-shape hints, validated as the reference does. The library is
 $CKOPT_BUILD_DIR/libkernel.so when CKOPT_BUILD_DIR is set, else this package's build/rope/libkernel.so.
@@ -38,6 +40,8 @@ _lib.launch.argtypes = [ctypes.c_void_p] * 7 + [ctypes.c_longlong] + [ctypes.c_i
 _lib.launch.restype = ctypes.c_int
 _lib.rope_launch_freq.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_longlong] + [ctypes.c_int] * 4 + [ctypes.c_void_p]
 _lib.rope_launch_freq.restype = ctypes.c_int
+_lib.rope_kv_launch.argtypes = [ctypes.c_void_p] * 9 + [ctypes.c_longlong] + [ctypes.c_int] * 4 + [ctypes.c_void_p]
+_lib.rope_kv_launch.restype = ctypes.c_int
 
 
 def _problem(q, k, cos, sin, ids, inv_freq, inplace):
@@ -63,7 +67,38 @@ def _problem(q, k, cos, sin, ids, inv_freq, inplace):
     return None
 
 
+def _run_kv(inputs):
+    """RoPE fused with the KV-cache write: q rotated (in place with inputs["inplace"]), rotated k and v written to the
+    k_cache / v_cache rows [slots, Hk, D] that slot_mapping (int64 [B, S], -1 = no write) picks."""
+    q, k, v, ids = inputs["q"], inputs["k"], inputs["v"], inputs["position_ids"]
+    kc, vc, slots, inv_freq = inputs["k_cache"], inputs["v_cache"], inputs["slot_mapping"], inputs.get("inv_freq")
+    inplace = bool(inputs.get("inplace", False))
+    problem = _problem(q, k, None, None, ids, inv_freq, inplace) if inv_freq is not None else "inv_freq missing"
+    if problem is None:
+        Hk, D = k.shape[2], k.shape[3]
+        if v.dtype != q.dtype or tuple(v.shape) != tuple(k.shape):
+            problem = f"v {v.dtype} {tuple(v.shape)}"
+        elif any(c.dtype != q.dtype or c.dim() != 3 or tuple(c.shape[1:]) != (Hk, D) or not c.is_contiguous()
+                 or c.device != q.device for c in (kc, vc)) or kc.shape != vc.shape:
+            problem = f"caches {tuple(kc.shape)} {tuple(vc.shape)} (contiguous [slots, {Hk}, {D}] of q's dtype)"
+        elif slots.dtype != torch.int64 or tuple(slots.shape) != tuple(ids.shape) or slots.device != q.device:
+            problem = f"slot_mapping {slots.dtype} {tuple(slots.shape)}"
+    if problem:
+        raise ValueError(f"rope candidate: {problem}")
+    q, k, v, ids, slots = q.contiguous(), k.contiguous(), v.contiguous(), ids.contiguous(), slots.contiguous()
+    q_out = q if inplace else torch.empty_like(q)
+    batch, seq, q_heads, head_dim = q.shape
+    err = _lib.rope_kv_launch(q.data_ptr(), k.data_ptr(), v.data_ptr(), ids.data_ptr(), inv_freq.contiguous().data_ptr(),
+                              q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), batch * seq, q_heads,
+                              k.shape[2], head_dim, _QK[q.dtype], torch.cuda.current_stream(q.device).cuda_stream)
+    if err:
+        raise RuntimeError(f"kernel launch failed: HIP error {err}")
+    return {"q_out": q_out, "k_cache": kc, "v_cache": vc}
+
+
 def run(inputs):
+    if "k_cache" in inputs:
+        return _run_kv(inputs)
     q, k, ids = inputs["q"], inputs["k"], inputs["position_ids"]
     cos, sin, inv_freq = inputs.get("cos"), inputs.get("sin"), inputs.get("inv_freq")
     inplace = bool(inputs.get("inplace", False))

@@ -50,6 +50,19 @@ def rope_4x4096_32q_8kv_128():
     return {"q": q, "k": k, "position_ids": pos, "inv_freq": rope_inv_freq(128)}
 
 
+def rope_kv_4x4096_32q_8kv_128():
+    """RoPE fused with the KV-cache write, bf16: the rope_4x4096_32q_8kv_128 inputs plus v[4, 4096, 8, 128] and a
+    16384-slot cache [16384, 8, 128] for k and v; the tokens' slots are a seeded permutation (a paged cache's blocks
+    in any order), seed 3."""
+    inp = rope_4x4096_32q_8kv_128()
+    g = torch.Generator().manual_seed(3)
+    inp["v"] = torch.randn(4, 4096, 8, 128, generator=g).bfloat16()
+    inp["slot_mapping"] = torch.randperm(16384, generator=g).view(4, 4096)
+    inp["k_cache"] = torch.zeros(16384, 8, 128, dtype=torch.bfloat16)
+    inp["v_cache"] = torch.zeros(16384, 8, 128, dtype=torch.bfloat16)
+    return inp
+
+
 def softmax_64x262144():
     """Long-row softmax fp32: x[64, 262144] ~ N(0, 5^2) with exactly 1% of the entries set to +20, seed 1."""
     g = torch.Generator().manual_seed(1)
@@ -75,6 +88,9 @@ def algorithmic_bytes(name, k=50):
         return 2 * 16384 * 4096 * 2 + 4096 * 2
     if name == "rmsnorm_add_16384x4096":
         return 4 * 16384 * 4096 * 2 + 4096 * 2
+    if name == "rope_kv_4x4096_32q_8kv_128":
+        # q read and written; k and v read, their cache rows written; int64 positions and slots read
+        return 2 * (4 * 4096 * 32 * 128 + 2 * 4 * 4096 * 8 * 128) * 2 + 2 * 4 * 4096 * 8
     if name == "rope_4x4096_32q_8kv_128":
         return 2 * (4 * 4096 * 32 * 128 + 4 * 4096 * 8 * 128) * 2 + 4 * 4096 * 8
     if name == "topk_128x128256":
@@ -89,4 +105,5 @@ WORKLOADS = {
     "softmax_64x262144": softmax_64x262144,
     "topk_128x128256": topk_128x128256,
     "rmsnorm_add_16384x4096": rmsnorm_add_16384x4096,
+    "rope_kv_4x4096_32q_8kv_128": rope_kv_4x4096_32q_8kv_128,
 }

@@ -125,6 +125,19 @@ def rope_freq(q, k, ids, inv_freq, dtype="bf16"):
     return qo, ko
 
 
+def rope_kv(q, k, v, ids, inv_freq, slots, k_cache, v_cache, dtype="bf16"):
+    """RoPE fused with the KV-cache write (flash layout [slots, kv_heads, D]): returns (q_out, k_cache', v_cache')
+    with q_out = rope_freq(q), and for every token t with slots[t] >= 0, k_cache'[slots[t]] = rope_freq(k)[t] and
+    v_cache'[slots[t]] = v[t]; other cache rows keep their contents. All tensors as uint16 bits."""
+    qo, ko = rope_freq(q, k, ids, inv_freq, dtype)
+    kc, vc = np.array(k_cache, dtype=np.uint16, copy=True), np.array(v_cache, dtype=np.uint16, copy=True)
+    for t, slot in enumerate(np.asarray(slots, dtype=np.int64)):
+        if slot >= 0:
+            kc[slot] = ko[t]
+            vc[slot] = np.asarray(v, dtype=np.uint16)[t]
+    return qo, kc, vc
+
+
 def rope_table(inv_freq, positions, head_dim):
     """The fp32 cos/sin cache [positions, head_dim] that the on-the-fly form evaluates."""
     inv_freq = _c(inv_freq, np.float32)

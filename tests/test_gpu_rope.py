@@ -126,3 +126,51 @@ def test_config_rope_4x4096_32q_8kv_128(pkg, oracle, dev):
     qo, ko = pkg.rope(q.to(dev), k.to(dev), pos.to(dev), cos=torch.from_numpy(ct).to(dev),
                       sin=torch.from_numpy(st).to(dev))
     assert np.array_equal(flat(qo), rq) and np.array_equal(flat(ko), rk)
+
+
+def kv_case(B, S, Hq, Hk, D, dtype, seed, slots_total=None, drop=0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, S, Hq, D, generator=g).to(dtype)
+    k = torch.randn(B, S, Hk, D, generator=g).to(dtype)
+    v = torch.randn(B, S, Hk, D, generator=g).to(dtype)
+    pos = torch.randint(0, 8192, (B, S), generator=g)
+    n = slots_total or 2 * B * S
+    slots = torch.randperm(n, generator=g)[: B * S].view(B, S).clone()
+    if drop:
+        slots.view(-1)[torch.randperm(B * S, generator=g)[:drop]] = -1  # padding tokens: no cache write
+    kc = torch.randn(n, Hk, D, generator=g).to(dtype)
+    vc = torch.randn(n, Hk, D, generator=g).to(dtype)
+    return q, k, v, pos, slots, kc, vc
+
+
+def check_kv(pkg, oracle, dev, case, inv_freq, inplace, what):
+    q, k, v, pos, slots, kc, vc = case
+    print(f"[rope kv] {what} q={tuple(q.shape)} k={tuple(k.shape)} {q.dtype} slots={kc.shape[0]} inplace={inplace}",
+          flush=True)
+    qd, kcd, vcd = q.to(dev), kc.to(dev), vc.to(dev)
+    kd = k.to(dev)
+    qo = pkg.rope_kv(qd, kd, v.to(dev), pos.to(dev), inv_freq.to(dev), kcd, vcd, slots.to(dev), inplace=inplace)
+    rq, rkc, rvc = oracle.rope_kv(flat(q), flat(k), flat(v), pos.view(-1).numpy(), inv_freq.numpy(),
+                                  slots.view(-1).numpy(), bits16(kc), bits16(vc), DT[q.dtype])
+    assert np.array_equal(flat(qo), rq), f"{what}: q differs"
+    assert np.array_equal(bits16(kcd), rkc), f"{what}: k cache differs"
+    assert np.array_equal(bits16(vcd), rvc), f"{what}: v cache differs"
+    assert np.array_equal(bits16(kd), bits16(k)), f"{what}: k was modified"
+    if inplace:
+        assert qo.data_ptr() == qd.data_ptr()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(1, 5, 4, 2, 64), (2, 33, 32, 8, 128), (1, 9, 2, 2, 40), (1, 4, 1, 1, 256)])
+def test_rope_kv_cache_write(pkg, oracle, dev, dtype, shape):
+    B, S, Hq, Hk, D = shape
+    inv_freq = pkg.workloads.rope_inv_freq(D)
+    case = kv_case(B, S, Hq, Hk, D, dtype, 11 * sum(shape), drop=min(3, B * S - 1))
+    check_kv(pkg, oracle, dev, case, inv_freq, True, f"{shape}")
+    check_kv(pkg, oracle, dev, kv_case(B, S, Hq, Hk, D, dtype, 13 * sum(shape)), inv_freq, False, f"{shape} out")
+
+
+def test_config_rope_kv_4x4096_32q_8kv_128(pkg, oracle, dev):
+    inp = pkg.workloads.rope_kv_4x4096_32q_8kv_128()
+    case = (inp["q"], inp["k"], inp["v"], inp["position_ids"], inp["slot_mapping"], inp["k_cache"], inp["v_cache"])
+    check_kv(pkg, oracle, dev, case, inp["inv_freq"], True, "rope_kv_4x4096_32q_8kv_128")

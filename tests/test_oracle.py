@@ -248,6 +248,29 @@ def test_rope_freq_vs_torch_cache(oracle):
     assert ((of - tf).abs() <= tf.abs() * 2 ** -7 + pair * 2 ** -22).all()
 
 
+def test_rope_kv_scatter_semantics(oracle):
+    """The fused cache write: q and the scattered k rows are the frequency form's rotation, v rows are copied, a
+    negative slot writes nothing and untouched rows keep their contents (checked element by element)."""
+    g = torch.Generator().manual_seed(34)
+    T_, H, Hk, D, S = 9, 4, 2, 64, 16
+    q, k, v = (torch.randn(T_, H, D, generator=g).bfloat16(), torch.randn(T_, Hk, D, generator=g).bfloat16(),
+               torch.randn(T_, Hk, D, generator=g).bfloat16())
+    ids = torch.randint(0, 100, (T_,), generator=g)
+    slots = torch.tensor([3, 0, -1, 15, 7, -1, 8, 1, 12])
+    inv = torch.rand(D // 2, generator=g)
+    kc0 = bits16(torch.randn(S, Hk, D, generator=g).bfloat16())
+    vc0 = bits16(torch.randn(S, Hk, D, generator=g).bfloat16())
+    qo, kc, vc = oracle.rope_kv(bits16(q), bits16(k), bits16(v), ids.numpy(), inv.numpy(), slots.numpy(), kc0, vc0)
+    rq, rk = oracle.rope_freq(bits16(q), bits16(k), ids.numpy(), inv.numpy())
+    assert np.array_equal(qo, rq)
+    written = {int(s_): t for t, s_ in enumerate(slots.tolist()) if s_ >= 0}
+    for slot in range(S):
+        if slot in written:
+            assert np.array_equal(kc[slot], rk[written[slot]]) and np.array_equal(vc[slot], bits16(v)[written[slot]])
+        else:
+            assert np.array_equal(kc[slot], kc0[slot]) and np.array_equal(vc[slot], vc0[slot])
+
+
 def test_rope_golden(oracle):
     f = golden("rope")
     oq, ok = oracle.rope_cache(f["q"], f["k"], f["cos"], f["sin"], f["ids"])
