@@ -143,6 +143,33 @@ class Case:
                 return lambda: lib.rope_launch_freq(q.data_ptr(), kk.data_ptr(), pos.data_ptr(), inv.data_ptr(),
                                                     q.data_ptr(), kk.data_ptr(), B * S, Hq, Hk, D, 1, stream())
             footprint = 2 * (inp["q"].numel() + inp["k"].numel()) * 2
+        elif name.startswith("topk_sample"):
+            cand = pkg.candidate("topk")
+            lib = cand._lib
+            rows, cols = inp["x"].shape
+            k, temp, top_p = inp["k"], inp["temperature"], inp["top_p"]
+            chunk = cand._plan(inp["x"].to(dev), rows, cols, 0, k)[1]
+            nchunks = -(-cols // chunk)
+            uni = inp["uniforms"].to(dev)
+            self.dtype = "fp32"
+
+            def make():
+                x = inp["x"].to(dev)
+                vals = torch.empty(rows, k, device=dev)
+                idx = torch.empty(rows, k, dtype=torch.int64, device=dev)
+                drawn = torch.empty(rows, dtype=torch.int64, device=dev)
+                work = torch.empty(max(1, rows * nchunks * k), dtype=torch.int64, device=dev)
+                counters = torch.zeros(rows, dtype=torch.int32, device=dev)
+                keep = (x, vals, idx, drawn, work, counters)
+
+                def run():
+                    err = lib.launch(keep[0].data_ptr(), vals.data_ptr(), idx.data_ptr(), work.data_ptr(),
+                                     counters.data_ptr(), rows, cols, k, 0, cand._THREADS, cand._DEPTH, chunk,
+                                     stream())
+                    return err or lib.topk_sample_launch(vals.data_ptr(), idx.data_ptr(), uni.data_ptr(),
+                                                         drawn.data_ptr(), rows, k, 0, temp, top_p, stream())
+                return run
+            footprint = inp["x"].numel() * 4
         elif name.startswith("topk"):
             cand = pkg.candidate("topk")
             lib = cand._lib
@@ -358,7 +385,7 @@ def main():
     names = [args.workload] if args.workload else list(pkg.workloads.WORKLOADS)
     cases = []
     for name in names:
-        if name.startswith("topk"):
+        if name.startswith("topk") and not name.startswith("topk_sample"):
             cases += [(name, k) for k in ([args.k] if args.k else (1, 50, 1024))]
         else:
             cases.append((name, None))

@@ -87,3 +87,8 @@ def topk(x, k=50):
     """The k largest entries of each row of a 2-D fp32/bf16 x, sorted descending, ties by lowest index."""
     out = candidate("topk").run({"x": x, "k": k})
     return out["values"], out["indices"]
+
+
+def topk_sample(values, indices, uniforms, temperature=1.0, top_p=1.0):
+    """Draws one index per row from a top-k list with temperature, nucleus cut and the caller's uniforms."""
+    return candidate("topk").sample(values, indices, uniforms, temperature, top_p)

@@ -1034,6 +1034,98 @@ __global__ void __launch_bounds__(kThreads)
   write_outputs<T>(values, indices, row, k, s.buf, n);
 }
 
+// ---- sampling from the top k ----------------------------------------------------------------------------------------
+
+constexpr int kSamplePer = kMaxK / kWave;  // list entries per lane (k <= 1024)
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), lane));
+}
+
+// Inclusive prefix sum over the wave's lanes (lane order).
+__device__ __forceinline__ float wave_prefix(float v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const float o = __shfl_up(v, d, kWave);
+    v += lane >= d ? o : 0.0f;
+  }
+  return v;
+}
+
+// One wave per row of a top-k list (values [rows, k] in T, int64 indices, as topk writes them): temperature, top-p
+// and a draw with the caller's uniform u[row] in [0, 1). With x = value / temperature, e_i = exp(x_i - max x) and
+// S_i = e_0 + ... + e_i (list order), the draw keeps the entries i with S_(i-1) < top_p * S_(k-1) (always the
+// first; every entry when top_p >= 1), and picks the first kept i with S_i > u * S_last_kept (the last kept if
+// rounding leaves none). temperature
+// <= 0 is greedy: position 0, the list's largest value (lowest index among ties). Values must be finite when
+// temperature > 0. Lane l holds positions [l E, l E + E), E = ceil(k / 64).
+template <typename T>
+__global__ void __launch_bounds__(kWave)
+    topk_sample(const void* __restrict__ values, const long long* __restrict__ indices, const float* __restrict__ u,
+                long long* __restrict__ out, int k, float temperature, float top_p) {
+  const long long row = blockIdx.x;
+  const int lane = lane_id();
+  const int per = (k + kWave - 1) / kWave;
+  const int base = lane * per;
+  float x[kSamplePer];
+#pragma unroll
+  for (int e = 0; e < kSamplePer; ++e) {
+    const int i = base + e;
+    float v = -INFINITY;
+    if (e < per && i < k) {
+      if constexpr (sizeof(T) == 4) v = static_cast<const float*>(values)[row * k + i];
+      else v = __uint_as_float((uint32_t) static_cast<const uint16_t*>(values)[row * k + i] << 16);
+    }
+    x[e] = v;
+  }
+  int chosen;
+  if (temperature <= 0.0f) {
+    chosen = 0;  // greedy: the list's first entry, its largest value (lowest position among ties)
+  } else {
+    float m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < kSamplePer; ++e) {
+      x[e] = x[e] / temperature;
+      m = fmaxf(m, x[e]);
+    }
+    m = wave_max(m);
+    float run = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kSamplePer; ++e) {
+      const float ex = (e < per && base + e < k) ? expf(x[e] - m) : 0.0f;
+      run += ex;
+      x[e] = run;  // lane-local inclusive sums
+    }
+    const float lane_excl = wave_prefix(run) - run;
+    const float total = readlane_f(wave_prefix(run), kWave - 1);
+    const float cut = top_p * total;
+    // kept: positions whose exclusive sum is below the cut (a prefix of the list; at least position 0)
+    int keep = 0;
+#pragma unroll
+    for (int e = 0; e < kSamplePer; ++e) {
+      const float excl = lane_excl + (e ? x[e - 1] : 0.0f);
+      keep += (e < per && base + e < k && (base + e == 0 || top_p >= 1.0f || excl < cut)) ? 1 : 0;
+    }
+    const int kept = (int)wave_sum((float)keep);
+    // the kept mass is the inclusive sum at position kept - 1
+    float mass = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kSamplePer; ++e)
+      if (e < per && base + e == kept - 1) mass = lane_excl + x[e];
+    mass = wave_max(mass);
+    const float target = u[row] * mass;
+    int first = kept - 1;
+#pragma unroll
+    for (int e = 0; e < kSamplePer; ++e) {
+      const int i = base + e;
+      if (e < per && i < kept && lane_excl + x[e] > target && i < first) first = i;
+    }
+    chosen = (int)wave_ext64<false>((u64)(uint32_t)first);
+  }
+  if (lane == 0) out[row] = indices[row * k + chosen];
+}
+
 // ---- host side -------------------------------------------------------------------------------------------------------
 
 // Tuning slots (0 = automatic): 0 resident workgroups per CU assumed by plan(), 1 elements per lane of a register
@@ -1141,6 +1233,28 @@ extern "C" int topk_reset(void* counters, long long rows, hipStream_t stream) {
   if (rows <= 0) return rw_host::kOk;
   if (!counters) return rw_host::kInvalid;
   return (int)hipMemsetAsync(counters, 0, (size_t)rows * sizeof(unsigned), stream);
+}
+
+// Sampling from a top-k list (no counterpart in the reference: the step after top-k in a decoder's sampler; see
+// topk_sample): out[row] = the int64 index drawn for each row from values/indices [rows, k] (k <= 1024, values in
+// fp32 (dtype 0) or bf16 (1)), with the caller's uniforms u[rows] in [0, 1), temperature (<= 0: greedy) and top_p
+// (>= 1: no nucleus cut). Returns 0 (rows <= 0 is a no-op), -1 for k outside [1, 1024], rows > 2^31 - 1, a null
+// pointer or an unknown dtype, otherwise the hipError_t of the launch.
+extern "C" int topk_sample_launch(const void* values, const void* indices, const float* uniforms, void* out,
+                                  long long rows, int k, int dtype, float temperature, float top_p,
+                                  hipStream_t stream) {
+  if (rows <= 0) return rw_host::kOk;
+  if (k < 1 || k > kMaxK || rows > 2147483647LL || !values || !indices || !uniforms || !out)
+    return rw_host::kInvalid;
+  if (dtype == 0)
+    hipLaunchKernelGGL((topk_sample<float>), dim3((unsigned)rows), dim3(kWave), 0, stream, values,
+                       (const long long*)indices, uniforms, (long long*)out, k, temperature, top_p);
+  else if (dtype == 1)
+    hipLaunchKernelGGL((topk_sample<uint16_t>), dim3((unsigned)rows), dim3(kWave), 0, stream, values,
+                       (const long long*)indices, uniforms, (long long*)out, k, temperature, top_p);
+  else
+    return rw_host::kInvalid;
+  return (int)hipGetLastError();
 }
 
 extern "C" int topk_tune(int slot, int value) { return rw_host::tune_set(slot, value); }

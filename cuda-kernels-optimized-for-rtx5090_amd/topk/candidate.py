@@ -43,6 +43,9 @@ _lib.launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctype
 _lib.launch.restype = ctypes.c_int
 _lib.topk_reset.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
 _lib.topk_reset.restype = ctypes.c_int
+_lib.topk_sample_launch.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
+                                                             ctypes.c_float, ctypes.c_float, ctypes.c_void_p]
+_lib.topk_sample_launch.restype = ctypes.c_int
 
 _counters = {}
 _last = None  # (key, chunk, work pointer, counters pointer, work, counters) of the last shape
@@ -90,3 +93,25 @@ def run(inputs):
     if err:
         raise RuntimeError(f"kernel launch failed: HIP error {err}")
     return {"values": values, "indices": indices}
+
+
+def sample(values, indices, uniforms, temperature=1.0, top_p=1.0):
+    """One index per row drawn from a top-k list (run()'s values and indices): softmax(values / temperature), the
+    nucleus cut top_p, and the caller's uniforms [rows] (fp32 in [0, 1)) as the draw; temperature <= 0 is greedy.
+    No counterpart in the reference (the step after top-k in a decoder's sampler). Returns int64 [rows]."""
+    dtype = _DTYPES.get(values.dtype)
+    if dtype is None or values.dim() != 2 or indices.shape != values.shape or indices.dtype != torch.int64 \
+            or uniforms.dtype != torch.float32 or tuple(uniforms.shape) != (values.shape[0],) \
+            or not 1 <= values.shape[1] <= K_MAX or values.device.type != "cuda" \
+            or indices.device != values.device or uniforms.device != values.device:
+        raise ValueError(f"topk sample takes values [rows, k] (fp32/bf16, k <= {K_MAX}), int64 indices of that shape "
+                         f"and fp32 uniforms [rows] on one GPU, got {values.dtype} {tuple(values.shape)}, "
+                         f"{indices.dtype} {tuple(indices.shape)}, {uniforms.dtype} {tuple(uniforms.shape)}")
+    values, indices, uniforms = values.contiguous(), indices.contiguous(), uniforms.contiguous()
+    out = torch.empty(values.shape[0], dtype=torch.int64, device=values.device)
+    err = _lib.topk_sample_launch(values.data_ptr(), indices.data_ptr(), uniforms.data_ptr(), out.data_ptr(),
+                                  values.shape[0], values.shape[1], dtype, float(temperature), float(top_p),
+                                  torch.cuda.current_stream(values.device).cuda_stream)
+    if err:
+        raise RuntimeError(f"kernel launch failed: HIP error {err}")
+    return out

@@ -79,6 +79,15 @@ def topk_128x128256():
     return {"x": torch.randn(128, 128256, generator=g) * 2}
 
 
+def topk_sample_128x128256():
+    """Top-k (k = 50) and a draw from it per row (temperature 0.8, top_p 0.9) over the top-k workload's logits, with
+    seeded uniforms, seed 4."""
+    inp = topk_128x128256()
+    g = torch.Generator().manual_seed(4)
+    inp.update({"k": 50, "temperature": 0.8, "top_p": 0.9, "uniforms": torch.rand(128, generator=g)})
+    return inp
+
+
 def algorithmic_bytes(name, k=50):
     if name == "softmax_4096x4096":
         return 2 * 4096 * 4096 * 4
@@ -93,6 +102,10 @@ def algorithmic_bytes(name, k=50):
         return 2 * (4 * 4096 * 32 * 128 + 2 * 4 * 4096 * 8 * 128) * 2 + 2 * 4 * 4096 * 8
     if name == "rope_4x4096_32q_8kv_128":
         return 2 * (4 * 4096 * 32 * 128 + 4 * 4096 * 8 * 128) * 2 + 4 * 4096 * 8
+    if name == "topk_sample_128x128256":
+        # the logits read once, the uniforms read, the drawn int64 indices written (the top-k list stays on chip
+        # between the two kernels' L2 and is not counted)
+        return 128 * 128256 * 4 + 128 * 4 + 128 * 8
     if name == "topk_128x128256":
         return 128 * 128256 * 4 + 128 * k * (4 + 8)
     raise KeyError(name)
@@ -106,4 +119,5 @@ WORKLOADS = {
     "topk_128x128256": topk_128x128256,
     "rmsnorm_add_16384x4096": rmsnorm_add_16384x4096,
     "rope_kv_4x4096_32q_8kv_128": rope_kv_4x4096_32q_8kv_128,
+    "topk_sample_128x128256": topk_sample_128x128256,
 }

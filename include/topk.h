@@ -31,6 +31,16 @@ int launch(const void* x, void* values, void* indices, void* work, void* counter
  * hipError_t of the memset. */
 int topk_reset(void* counters, long long rows, hipStream_t stream);
 
+/* No counterpart in the reference (the step after top-k in a decoder's sampler, SURVEY "next"): one index per row drawn
+ * from a top-k list -- values [rows, k] in fp32 (dtype 0) or bf16 (1) and int64 indices [rows, k], as launch() writes
+ * them -- with the caller's uniforms[rows] (fp32 in [0, 1)). x = value / temperature, e_i = exp(x_i - max x),
+ * S_i = e_0 + ... + e_i; the positions i with i == 0 or S_(i-1) < top_p * S_(k-1) are kept, and the first kept i with
+ * S_i > u * S_(last kept) is drawn. temperature <= 0 is greedy (position 0); top_p >= 1 keeps every position. Values
+ * must be finite when temperature > 0. out: int64 [rows]. Returns 0 (rows <= 0 is a no-op), -1 for k outside
+ * [1, 1024], rows > 2^31 - 1, a null pointer or an unknown dtype, otherwise the hipError_t of the launch. */
+int topk_sample_launch(const void* values, const void* indices, const float* uniforms, void* out, long long rows, int k,
+                       int dtype, float temperature, float top_p, hipStream_t stream);
+
 /* No counterpart in the reference: tuning override for parameter sweeps. Slot 0: resident workgroups per CU assumed by
  * plan(); slot 1: elements per lane of the k > 64 kernel's register block (16, 32 or 64). Returns 0 or -1. */
 int topk_tune(int slot, int value);

@@ -38,6 +38,7 @@ def lib():
         L.oracle_softmax.argtypes = [vp, vp, ll, ll, i]
         L.oracle_rmsnorm.argtypes = [vp, vp, vp, ll, ll, i, f, vp]
         L.oracle_rmsnorm_add.argtypes = [vp, vp, vp, vp, vp, ll, ll, i, f]
+        L.oracle_topk_sample.argtypes = [vp, vp, vp, vp, ll, i, i, f, f, vp]
         L.oracle_rope_cache.argtypes = [vp, vp, vp, vp, vp, vp, vp, ll, i, i, i, i, i]
         L.oracle_rope_freq.argtypes = [vp, vp, vp, vp, vp, vp, ll, i, i, i, i]
         L.oracle_rope_table.argtypes = [vp, ll, i, vp, vp]
@@ -169,3 +170,16 @@ def f32_to_bf16_bits(a):
 
 def bf16_bits_to_f32(b):
     return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def topk_sample(values, indices, u, temperature=1.0, top_p=1.0, dtype="fp32"):
+    """Draws one index per row of a top-k list (values fp32 or bf16 bits [rows, k], int64 indices) with uniforms u.
+    Returns (drawn int64 [rows], ambiguous bool [rows]: the draw or the cut lies within fp32 rounding of a boundary)."""
+    vals = _c(values, np.float32 if dtype == "fp32" else np.uint16)
+    idx, uu = _c(indices, np.int64), _c(u, np.float32)
+    rows, k = idx.shape
+    out = np.empty(rows, dtype=np.int64)
+    amb = np.empty(rows, dtype=np.int32)
+    lib().oracle_topk_sample(_ptr(vals), _ptr(idx), _ptr(uu), _ptr(out), rows, k, 0 if dtype == "fp32" else 1,
+                             ctypes.c_float(temperature), ctypes.c_float(top_p), _ptr(amb))
+    return out, amb.astype(bool)

@@ -285,3 +285,46 @@ void oracle_topk(const void* x, void* values, int64_t* indices, long long rows, 
   }
   free(heap);
 }
+
+/* ---- sampling from a top-k list (no counterpart in the reference; the step after top-k in a decoder's sampler) ------
+ * The rule of the HIP kernel, restated in fp64 for each row of values/indices [rows, k] (the order top-k writes):
+ * x_i = v_i / temperature, e_i = exp(x_i - max x), S_i = e_0 + ... + e_i; keep the positions i with i == 0 or
+ * S_(i-1) < top_p * S_(k-1) (every position when top_p >= 1); draw the first kept i with S_i > u * S_(last kept), else
+ * the last kept. temperature <= 0 takes position 0. ambiguous[row] = 1 when the draw's target lies within
+ * 2e-5 * S_(k-1) of an interval edge (where the kernel's fp32 sums may decide it either way). */
+void oracle_topk_sample(const void* values, const int64_t* indices, const float* u, int64_t* out, long long rows,
+                        int k, int dtype, float temperature, float top_p, int* ambiguous) {
+  double* S = (double*)malloc(sizeof(double) * (size_t)k);
+  for (long long r = 0; r < rows; ++r) {
+    ambiguous[r] = 0;
+    if (temperature <= 0.0f) {
+      out[r] = indices[r * k];
+      continue;
+    }
+    double m = -INFINITY;
+    for (int i = 0; i < k; ++i) {
+      const double x = (double)load_fmt(values, r * k + i, dtype == 1 ? 1 : 0) / (double)temperature;
+      if (x > m) m = x;
+    }
+    double run = 0.0;
+    for (int i = 0; i < k; ++i) {
+      const double x = (double)load_fmt(values, r * k + i, dtype == 1 ? 1 : 0) / (double)temperature;
+      run += exp(x - m);
+      S[i] = run;
+    }
+    /* a cut that rounding moves changes the kept mass by less than tol, which moves the target by less than tol:
+     * the draw's tolerance band (2 tol) covers it */
+    const double total = S[k - 1], tol = 1e-5 * total, cut = (double)top_p * total;
+    int kept = top_p >= 1.0f ? k : 1;
+    for (int i = 1; i < k && top_p < 1.0f; ++i)
+      if (S[i - 1] < cut) kept = i + 1;
+    const double target = (double)u[r] * S[kept - 1];
+    int chosen = kept - 1;
+    for (int i = 0; i < kept; ++i) {
+      if (fabs(S[i] - target) < 2.0 * tol) ambiguous[r] = 1;
+      if (S[i] > target && i < chosen) chosen = i;
+    }
+    out[r] = indices[r * k + chosen];
+  }
+  free(S);
+}

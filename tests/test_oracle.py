@@ -367,3 +367,57 @@ def test_planted_mistakes_are_caught(oracle):
     si = torch.sort(t, dim=-1, descending=True, stable=True)[1][:, :20].numpy()
     assert np.array_equal(i, si) and not np.array_equal(i + 1, si)
     assert not np.array_equal(i, torch.sort(t.flip(-1), dim=-1, descending=True, stable=True)[1][:, :20].numpy())
+
+
+# ---- sampling from a top-k list --------------------------------------------------------------------------------------
+
+
+def _sorted_list(rows, k, seed, scale=2.0):
+    g = torch.Generator().manual_seed(seed)
+    v, i = torch.sort(torch.randn(rows, 4 * k, generator=g) * scale, dim=-1, descending=True, stable=True)
+    return v[:, :k].contiguous().numpy(), i[:, :k].contiguous().numpy()
+
+
+def test_topk_sample_inverse_cdf(oracle):
+    """temperature and no nucleus cut: the draw is the inverse CDF of softmax(v / T) at u, computed independently."""
+    v, i = _sorted_list(200, 50, 41)
+    u = np.random.default_rng(1).random(200, dtype=np.float32)
+    for T in (0.5, 1.0, 2.0):
+        got, amb = oracle.topk_sample(v, i, u, T, 1.0)
+        p = np.exp((v.astype(np.float64) - v[:, :1]) / T)
+        c = np.cumsum(p, axis=1)
+        pos = np.array([np.searchsorted(c[r], u[r] * c[r, -1], side="right") for r in range(200)])
+        expect = i[np.arange(200), np.minimum(pos, 49)]
+        # ambiguous: u lands within fp32 rounding of an interval edge (common only among a peaked list's tail entries,
+        # whose intervals are narrower than that)
+        assert np.array_equal(got[~amb], expect[~amb]) and amb.mean() < 0.1
+
+
+def test_topk_sample_nucleus_and_greedy(oracle):
+    v, i = _sorted_list(100, 64, 42)
+    p = np.exp(v.astype(np.float64) - v[:, :1])
+    c = np.cumsum(p, axis=1)
+    for top_p in (0.2, 0.6, 0.95):
+        kept = 1 + np.sum(c[:, :-1] < top_p * c[:, -1:], axis=1)
+        # u just below 1 draws the last kept position; u = 0 draws the first
+        hi, amb = oracle.topk_sample(v, i, np.full(100, 1 - 2 ** -24, np.float32), 1.0, top_p)
+        ok = ~amb
+        assert np.array_equal(hi[ok], i[np.arange(100), kept - 1][ok])
+        lo, _ = oracle.topk_sample(v, i, np.zeros(100, np.float32), 1.0, top_p)
+        assert np.array_equal(lo, i[:, 0])
+    g0, _ = oracle.topk_sample(v, i, np.full(100, 0.7, np.float32), 0.0, 0.5)
+    assert np.array_equal(g0, i[:, 0])
+
+
+def test_topk_sample_frequencies(oracle):
+    """A regular grid of u draws each kept position in proportion to its renormalised probability."""
+    v, i = _sorted_list(1, 8, 43)
+    n = 4096
+    u = ((np.arange(n) + 0.5) / n).astype(np.float32)
+    got, _ = oracle.topk_sample(np.repeat(v, n, 0), np.repeat(i, n, 0), u, 0.8, 0.9)
+    p = np.exp((v[0].astype(np.float64) - v[0, 0]) / 0.8)
+    c = np.cumsum(p)
+    kept = 1 + int(np.sum(c[:-1] < 0.9 * c[-1]))
+    q = p[:kept] / c[kept - 1]
+    freq = np.array([(got == i[0, j]).mean() for j in range(kept)])
+    assert np.abs(freq - q).max() < 2.0 / n and set(got) <= set(i[0, :kept])
