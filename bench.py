@@ -43,7 +43,7 @@ TRAFFIC_PATH = os.path.join(ROOT, "profiles", "traffic.json")
 # the kernels whose counters give each workload's traffic: a name fragment; the dispatches of one launch that contain
 # it are summed (the whole launch for the two-kernel paths)
 KERNELS = {"rmsnorm_16384x4096": "rmsnorm_rows", "softmax_4096x4096": "softmax_rows",
-           "softmax_64x262144": "softmax_split", "rope_4x4096_32q_8kv_128": "rope_vec",
+           "softmax_64x262144": "softmax_coop", "rope_4x4096_32q_8kv_128": "rope_vec",
            "topk_128x128256_k50": "topk_tile", "rmsnorm_add_16384x4096": "rmsnorm_rows",
            "rope_kv_4x4096_32q_8kv_128": "rope_vec"}
 
