@@ -43,9 +43,19 @@ inline int device_cus() {
 // ends. Returns nullptr with *err set on failure.
 // `purpose` keeps separate buffers for users that must not share one (a buffer whose contents carry over between
 // launches); with `zeroed` a new buffer is cleared on `stream` before first use.
+// The workspace table: (device, purpose, stream) -> (buffer, bytes).
+struct WorkspaceTable {
+  std::mutex mu;
+  std::map<std::pair<std::pair<int, int>, hipStream_t>, std::pair<void*, size_t>> buffers;
+};
+inline WorkspaceTable& workspaces() {
+  static WorkspaceTable table;
+  return table;
+}
+
 inline void* stream_workspace(hipStream_t stream, size_t bytes, int* err, int purpose = 0, bool zeroed = false) {
-  static std::mutex mu;
-  static std::map<std::pair<std::pair<int, int>, hipStream_t>, std::pair<void*, size_t>> buffers;
+  std::mutex& mu = workspaces().mu;
+  auto& buffers = workspaces().buffers;
   *err = kOk;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -81,6 +91,18 @@ inline void* stream_workspace(hipStream_t stream, size_t bytes, int* err, int pu
   }
   slot = {p, want};
   return p;
+}
+
+// Zeroes the current device's workspace for (purpose, stream), if one was allocated, on `stream`. Returns 0 or the
+// hipError_t.
+inline int clear_stream_workspace(hipStream_t stream, int purpose) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  std::lock_guard<std::mutex> lock(workspaces().mu);
+  auto it = workspaces().buffers.find(std::make_pair(std::make_pair(dev, purpose), stream));
+  if (it == workspaces().buffers.end() || !it->second.first) return kOk;
+  return (int)hipMemsetAsync(it->second.first, 0, it->second.second, stream);
 }
 
 // Tuning overrides: slot i holds 0 (automatic choice) or a value the launcher uses instead of its own choice. They are

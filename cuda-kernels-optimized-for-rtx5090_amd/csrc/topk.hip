@@ -7,7 +7,7 @@
 // for bit, so x is read once.
 //
 // k <= 64: topk_tile, one kernel (see its comment); the row's last workgroup merges the chunk lists, handed over
-// through device-coherent stores and loads and the caller's per-row counter, as the reference's last-block merge.
+// through device-coherent stores and loads and a per-row arrival counter, as the reference's last-block merge.
 //
 // k > 64: two kernels on the caller's stream (the stream order publishes the first kernel's workspace to the second):
 //  - topk_chunks, one 256-thread workgroup per (chunk, row): the workgroup loads a block of its chunk (E elements per
@@ -483,6 +483,10 @@ static_assert(kTileSort == kThreads, "the rank sort and the merge heads use one 
 
 typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
 
+// A row's arrival counter sits alone in its 256 bytes: the device-scope atomics of the rows' last workgroups, which
+// come close together, are not serialized on a shared line (the caller's counters are 4 bytes apart).
+constexpr int kArrivalStride = 64;
+
 struct TileSmem {
   u64 seg[kWaves][kTileSeg];
   alignas(16) u64 sorted[kTileSort];
@@ -494,19 +498,39 @@ struct TileSmem {
 
 // Order-preserving 32-bit key of fp32 bits u (the upper half of a composite).
 __device__ __forceinline__ uint32_t key_of(uint32_t u) { return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u); }
+// Its inverse: the fp32 bits of key K.
+__device__ __forceinline__ uint32_t bits_of(uint32_t K) { return (K & 0x80000000u) ? (K & 0x7fffffffu) : ~K; }
 
-// The k-th largest (1 <= k <= the number of lanes with ok) of the wave's 32-bit values v (one per lane): a bitwise
-// search from the highest bit where the valid minimum and maximum differ, keeping the largest prefix with at least k
-// values at or above it (counted with ballots). Wave-uniform.
+// Wave-wide maximum (MAX) or minimum of a u32; every lane returns it.
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_ext32(uint32_t v) {
+  auto pick = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+  v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor1, 0xF, 0xF, false));
+  v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor2, 0xF, 0xF, false));
+  v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppHalfMirror, 0xF, 0xF, false));
+  v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppMirror, 0xF, 0xF, false));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return pick(pick(a, b), pick(c, d));
+}
+
+constexpr int kThrBits = 12;  // bits resolved by the threshold search below the highest differing one
+
+// A lower bound of the k-th largest (1 <= k <= the number of lanes with ok) of the wave's 32-bit values v (one per
+// lane) with at least k of them at or above it: a bitwise search from the highest bit where the valid minimum and
+// maximum differ, keeping the largest prefix with at least k values at or above it (counted with ballots), stopped
+// after kThrBits bits (the bound is then within 2^(top - kThrBits) of the k-th). Wave-uniform.
 __device__ __forceinline__ uint32_t wave_kth32(uint32_t v, bool ok, int k) {
-  const uint32_t mx = (uint32_t)wave_ext64<true>(ok ? v : 0u);
-  const uint32_t mn = (uint32_t)wave_ext64<false>(ok ? v : 0xffffffffu);
+  v = ok ? v : 0u;
+  const uint32_t mx = wave_ext32<true>(v);
+  if (k == 1) return mx;
+  const uint32_t mn = wave_ext32<false>(ok ? v : 0xffffffffu);
   if (mx == mn) return mx;
   const int top = 31 - __builtin_clz(mx ^ mn);
   uint32_t p = mx & ~((2u << top) - 1u);
-  for (int b = top; b >= 0; --b) {
-    const uint32_t cand = p | (1u << b);
-    if (__popcll(__ballot(ok && v >= cand)) >= k) p = cand;
+  for (int b = top; b >= 0 && b > top - kThrBits; --b) {
+    const uint32_t cand = p | (1u << b);  // >= 1: the lanes without ok (0) never count
+    if (__popcll(__ballot(v >= cand)) >= k) p = cand;
   }
   return p;
 }
@@ -554,8 +578,8 @@ __device__ __forceinline__ u64 block_kth(const F& slot, int k, BlockRed& red) {
       kmn = kk < kmn ? kk : kmn;
     }
   }
-  kmx = red.max((uint32_t)wave_ext64<true>(kmx));
-  kmn = red.min((uint32_t)wave_ext64<false>(kmn));
+  kmx = red.max(wave_ext32<true>(kmx));
+  kmn = red.min(wave_ext32<false>(kmn));
   uint32_t K = kmx;
   if (kmx != kmn) {
     const int top = 31 - __builtin_clz(kmx ^ kmn);
@@ -586,8 +610,8 @@ __device__ __forceinline__ u64 block_kth(const F& slot, int k, BlockRed& red) {
   }
   gt = (int)red.sum((uint32_t)gt);
   eq = (int)red.sum((uint32_t)eq);
-  lmx = red.max((uint32_t)wave_ext64<true>(lmx));
-  lmn = red.min((uint32_t)wave_ext64<false>(lmn));
+  lmx = red.max(wave_ext32<true>(lmx));
+  lmn = red.min(wave_ext32<false>(lmn));
   const int r = k - gt;  // 1 <= r <= eq
   uint32_t L = lmn;
   if (r < eq) {
@@ -620,6 +644,21 @@ struct TileList {
       const int pos = cnt + lanes_below(m);
       if (keep && pos < kTileSeg) seg[pos] = c;
       cnt += __popcll(m);
+    }
+  }
+
+  // push() for a batch whose ballot m is already known: keep is this lane's bit of m, comp() its composite. A batch
+  // that would pass the segment's end is counted and not stored (the list then overflows, see settle()).
+  template <typename C>
+  __device__ __forceinline__ void push_mask(u64 m, bool keep, const C& comp) {
+    if (m) {
+      const int n = __popcll(m);
+      if (cnt + n <= kTileSeg && keep) {
+        const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)cnt));
+        seg[pos] = comp();
+      }
+      cnt += n;
     }
   }
 
@@ -748,29 +787,41 @@ __device__ __forceinline__ void finish_list(TileSmem& s, const TileList& L, void
     for (int j = n + t; j < k; j += kThreads) __hip_atomic_store(wr + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// A register tile: thread t holds vectors v * 256 + t (v < NV) of elements [b0, b1) of a row, W each (an empty tile,
-// b0 >= b1, loads in-bounds duplicates and holds no element). load() only issues the loads; prepare() turns fp32
-// registers into keys in place once they are needed; bf16 keys are formed from the packed halves when used.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+// What a vector load past a tile's end reads instead (all ones: the sentinel below).
+__device__ u32x4 g_sentinel_vec = {~0u, ~0u, ~0u, ~0u};
+
+// A register tile: thread t holds vectors v * 256 + t (v < NV) of elements [b0, b1) of a row, W each, as raw bits; an
+// element outside [b0, b1) holds the sentinel (all ones: the -NaN whose key is the smallest of its format), read from
+// g_sentinel_vec by a vector load past the end. load() only issues the loads.
+//
+// The raw bits are ordered without forming keys: over non-negative values key order is the signed order of the bits
+// (as int32, or int16 for a bf16 half), over negative values it is the reverse. So the largest element of a set, in
+// key order, is its signed maximum when that is non-negative and its signed minimum otherwise (the sentinel, -1 as an
+// integer, is the largest negative one: it never moves the minimum of a set holding a real element); and for a
+// threshold key K with bits t, key(u) >= K iff (int)u >= (int)t when K is a non-negative value, iff u <= t (unsigned)
+// when K is negative.
 template <typename T, bool VEC>
 struct Tile {
   static constexpr int W = Fmt<T>::W;
   static constexpr int NV = kTileE / W;
+  static constexpr uint32_t kSentinelKey = sizeof(T) == 4 ? 0u : 0xffffu;  // key of the sentinel
   u32x4 r[NV];
   int b0, b1;
   int lane0;  // b0 + threadIdx.x * W, the first element of vector 0 (kept opaque with the registers)
 
   __device__ __forceinline__ int first(int v) const { return lane0 + v * kThreads * W; }
-  __device__ __forceinline__ bool valid(int v, int j) const { return VEC ? first(v) < b1 : first(v) + j < b1; }
-  __device__ __forceinline__ uint32_t key(int v, int j) const {
+  __device__ __forceinline__ uint32_t bits(int v, int j) const {
     if constexpr (sizeof(T) == 4) {
       return r[v][j];
     } else {
       const uint32_t w = r[v][j >> 1];
-      return key_of((j & 1) ? (w & 0xffff0000u) : (w << 16));
+      return (j & 1) ? (w & 0xffff0000u) : (w << 16);
     }
   }
   __device__ __forceinline__ u64 comp(int v, int j) const {
-    return ((u64)key(v, j) << 32) | (u64)(~(uint32_t)(first(v) + j));
+    return ((u64)key_of(bits(v, j)) << 32) | (u64)(~(uint32_t)(first(v) + j));
   }
 
   __device__ __forceinline__ void load(const T* row, int t0, int end) {
@@ -781,14 +832,14 @@ struct Tile {
     for (int v = 0; v < NV; ++v) {
       const int e0 = first(v);
       if constexpr (VEC) {
-        r[v] = load16<true>(row + (e0 < b1 ? e0 : end - W), 0);  // an in-range duplicate past the end, never used
+        r[v] = load16<true>(e0 < b1 ? (const void*)(row + e0) : (const void*)&g_sentinel_vec, 0);
       } else {
         uint32_t u[W];
 #pragma unroll
         for (int j = 0; j < W; ++j) {
           const int e = e0 + j;
-          if constexpr (sizeof(T) == 4) u[j] = e < b1 ? reinterpret_cast<const uint32_t*>(row)[e] : 0u;
-          else u[j] = e < b1 ? (uint32_t)reinterpret_cast<const uint16_t*>(row)[e] : 0u;
+          if constexpr (sizeof(T) == 4) u[j] = e < b1 ? reinterpret_cast<const uint32_t*>(row)[e] : 0xffffffffu;
+          else u[j] = e < b1 ? (uint32_t)reinterpret_cast<const uint16_t*>(row)[e] : 0xffffu;
         }
         if constexpr (sizeof(T) == 4) r[v] = (u32x4){u[0], u[1], u[2], u[3]};
         else r[v] = (u32x4){u[0] | (u[1] << 16), u[2] | (u[3] << 16), u[4] | (u[5] << 16), u[6] | (u[7] << 16)};
@@ -797,15 +848,63 @@ struct Tile {
     asm volatile("" ::: "memory");  // issue the loads here: the scheduler must not sink them past later work
   }
 
-  // Once the loads are needed: fp32 registers become keys in place.
-  __device__ __forceinline__ void prepare() {
+  // The key of this lane's largest element (the sentinel's key for a lane holding none).
+  __device__ __forceinline__ uint32_t max_key() const {
     if constexpr (sizeof(T) == 4) {
+      int mx = INT_MIN, mn = INT_MAX;
 #pragma unroll
       for (int v = 0; v < NV; ++v)
 #pragma unroll
-        for (int j = 0; j < W; ++j) r[v][j] = key_of(r[v][j]);
+        for (int j = 0; j < W; ++j) {
+          const int x = (int)r[v][j];
+          mx = x > mx ? x : mx;
+          mn = x < mn ? x : mn;
+        }
+      return key_of((uint32_t)(mx >= 0 ? mx : mn));
+    } else {
+      s16x2 mx = {(short)-32768, (short)-32768}, mn = {(short)32767, (short)32767};
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const s16x2 x = __builtin_bit_cast(s16x2, r[v][j]);
+          mx = __builtin_elementwise_max(mx, x);
+          mn = __builtin_elementwise_min(mn, x);
+        }
+      const uint32_t lo = (uint32_t)(uint16_t)(mx.x >= 0 ? mx.x : mn.x) << 16;
+      const uint32_t hi = (uint32_t)(uint16_t)(mx.y >= 0 ? mx.y : mn.y) << 16;
+      const uint32_t kl = key_of(lo), kh = key_of(hi);
+      return kl > kh ? kl : kh;
     }
-    opaque();
+  }
+
+  // Pushes every element with key >= K (K above the sentinel's key; NEG: K is a negative value): one compare per
+  // element on the raw bits, the list's positions from the compare's ballot.
+  template <bool NEG, typename Lst>
+  __device__ __forceinline__ void filter(Lst& L, uint32_t K) {
+    const uint32_t t = bits_of(K);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      bool a[W];
+      u64 m[W];
+      u64 any = 0;
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        if constexpr (sizeof(T) == 4) {
+          a[j] = NEG ? r[v][j] <= t : (int)r[v][j] >= (int)t;
+        } else {
+          const uint32_t w = r[v][j >> 1];
+          if (j & 1) a[j] = NEG ? w <= (t | 0xffffu) : (int)w >= (int)t;  // the low half only breaks ties
+          else a[j] = NEG ? (uint16_t)w <= (uint16_t)(t >> 16) : (int16_t)(uint16_t)w >= (int16_t)(uint16_t)(t >> 16);
+        }
+        m[j] = __ballot(a[j]);
+        any |= m[j];
+      }
+      if (any) {
+#pragma unroll
+        for (int j = 0; j < W; ++j) L.push_mask(m[j], a[j], [&] { return comp(v, j); });
+      }
+    }
   }
 
   // Pushes the elements of vector v, held in r[0], with composites >= floor, calling check() after every 4 per lane;
@@ -818,7 +917,7 @@ struct Tile {
     for (int g = 0; g < W; g += 4) {
 #pragma unroll
       for (int j = g; j < g + 4; ++j) {
-        const u64 c = ((u64)key(0, j) << 32) | (u64)(~(uint32_t)(e0 + j));
+        const u64 c = ((u64)key_of(bits(0, j)) << 32) | (u64)(~(uint32_t)(e0 + j));
         L.push(c, (VEC ? e0 < b1 : e0 + j < b1) && c >= floor);
       }
       check();
@@ -891,19 +990,19 @@ __device__ __forceinline__ void merge_lists(TileSmem& s, BlockRed& red, TileList
 }
 
 // k <= 64: one 256-thread workgroup per (chunk, row). The chunk is taken in register tiles of 16384 elements, all of a
-// tile's loads in flight at once. Per tile: each wave takes the ceil(k / 4)-th largest of its 64 lane maxima, which
-// has that many distinct elements at or above it, and the smallest of the four waves' keys has at least k; with the
-// k-th of the earlier tiles it is the admission key. Admitted elements (about k * 1.5 per tile on continuous data)
-// are appended to the waves' LDS segments; a list beyond kTileKeep is pruned to k, and an overflowing tile (ties, or
-// adversarial orders) is pushed again in index order with a prune whenever the list passes kTileKeep. The list is
-// then rank-sorted and written out for an unsplit row. A split row's chunk writes its k largest, descending, to the
-// workspace with device-coherent stores, waits for them to complete and counts its arrival on the row's counter; the
-// row's last arrival merges the lists (merge_lists) and zeroes the counter for the next launch -- no L2 write-back
-// or invalidate, and no second kernel.
+// tile's loads in flight at once. Per tile: each wave takes (a lower bound of) the ceil(k / 4)-th largest of its 64
+// lane maxima, which has that many distinct elements at or above it, and the smallest of the four waves' keys has at
+// least k; with the k-th of the earlier tiles it is the admission key. Admitted elements (about k * 1.5 per tile on
+// continuous data) are appended to the waves' LDS segments; a list beyond kTileKeep is pruned to k, and an overflowing
+// tile (ties, or adversarial orders) is pushed again in index order with a prune whenever the list passes kTileKeep.
+// The list is then rank-sorted and written out for an unsplit row. A split row's chunk writes its k largest,
+// descending, to the workspace with device-coherent stores, waits for them to complete and counts its arrival on the
+// row's counter (arrivals[row * kArrivalStride]); the row's last arrival merges the lists (merge_lists) and zeroes the
+// counter for the next launch -- no L2 write-back or invalidate, and no second kernel.
 template <typename T, bool VEC>
 __global__ void __launch_bounds__(kThreads)
     topk_tile(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
-              u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
+              u64* __restrict__ work, unsigned* __restrict__ arrivals, long long cols, long long chunk, int nchunks,
               int k) {
   __shared__ TileSmem s;
   const long long row = blockIdx.y;
@@ -922,35 +1021,20 @@ __global__ void __launch_bounds__(kThreads)
   using TL = Tile<T, VEC>;
   constexpr int TE = kThreads * kTileE;
   auto process = [&](TL& tile, bool more) __attribute__((always_inline)) {
-    tile.prepare();
-    uint32_t m = 0;
-    bool has = false;
-#pragma unroll
-    for (int v = 0; v < TL::NV; ++v)
-#pragma unroll
-      for (int j = 0; j < TL::W; ++j)
-        if (tile.valid(v, j)) {
-          const uint32_t kk = tile.key(v, j);
-          m = kk > m ? kk : m;
-          has = true;
-        }
+    const bool has = tile.lane0 < tile.b1;
+    const uint32_t m = tile.max_key();  // vector by vector as the loads complete
     const uint32_t tw = __popcll(__ballot(has)) >= kw ? wave_kth32(m, has, kw) : 0u;
     const uint32_t tb = red.min(tw);
     thr = tb > thr ? tb : thr;
+    L.cnt = __builtin_amdgcn_readfirstlane(L.cnt);
     const int cnt0 = L.cnt;
     tile.opaque();
-#pragma unroll
-    for (int v = 0; v < TL::NV; ++v)
-#pragma unroll
-      for (int g = 0; g < TL::W; g += 4) {
-        bool any = false;
-#pragma unroll
-        for (int j = g; j < g + 4; ++j) any |= tile.valid(v, j) && tile.key(v, j) >= thr;
-        if (__ballot(any)) {
-#pragma unroll
-          for (int j = g; j < g + 4; ++j) L.push(tile.comp(v, j), tile.valid(v, j) && tile.key(v, j) >= thr);
-        }
-      }
+    if (thr > TL::kSentinelKey) {
+      if (thr & 0x80000000u) tile.template filter<false>(L, thr);
+      else tile.template filter<true>(L, thr);
+    } else {
+      L.cnt = kTileSeg + 1;  // no usable bound: every element may pass, so the tile takes the exact re-push path
+    }
     int total = 0;
     u64 kth = L.settle(
         red, k, cnt0, TL::NV, (u64)thr << 32,
@@ -979,14 +1063,16 @@ __global__ void __launch_bounds__(kThreads)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned old = __hip_atomic_fetch_add(counters + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned old =
+        __hip_atomic_fetch_add(arrivals + row * kArrivalStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s.last = old == (unsigned)nchunks - 1;
   }
   __syncthreads();
   if (!s.last) return;
   L.cnt = 0;
   merge_lists<T>(s, red, L, values, indices, wr, row, nchunks, k);
-  if (threadIdx.x == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(arrivals + row * kArrivalStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- merge kernel ----------------------------------------------------------------------------------------------------
@@ -1121,7 +1207,7 @@ __global__ void __launch_bounds__(kWave)
       const int i = base + e;
       if (e < per && i < kept && lane_excl + x[e] > target && i < first) first = i;
     }
-    chosen = (int)wave_ext64<false>((u64)(uint32_t)first);
+    chosen = (int)wave_ext32<false>((uint32_t)first);
   }
   if (lane == 0) out[row] = indices[row * k + chosen];
 }
@@ -1131,6 +1217,7 @@ __global__ void __launch_bounds__(kWave)
 // Tuning slots (0 = automatic): 0 resident workgroups per CU assumed by plan(), 1 elements per lane of a register
 // block (16, 32 or 64).
 enum { kTuneBlocksPerCu = 0, kTuneE = 1 };
+constexpr int kArrivalsPurpose = 2;  // stream_workspace key of the k <= 64 arrival counters
 constexpr int kDefaultE = 32;
 
 int lane_elems() {
@@ -1139,13 +1226,20 @@ int lane_elems() {
 }
 
 template <typename T, bool VEC>
-int launch_chunks(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
+int launch_chunks(const void* x, void* values, void* indices, void* work, long long rows,
                   long long cols, long long chunk, int nchunks, int k, hipStream_t stream) {
   const dim3 grid((unsigned)nchunks, (unsigned)rows);
   const int e = VEC ? lane_elems() : 16;
   if (k <= kSeedMaxK) {
+    unsigned* arrivals = nullptr;
+    if (nchunks > 1) {  // the arrival counters: zeros between launches, kept per (device, stream)
+      int err = rw_host::kOk;
+      arrivals = (unsigned*)rw_host::stream_workspace(stream, (size_t)rows * kArrivalStride * sizeof(unsigned), &err,
+                                                      kArrivalsPurpose, true);
+      if (!arrivals) return err;
+    }
     hipLaunchKernelGGL((topk_tile<T, VEC>), grid, dim3(kThreads), 0, stream, (const T*)x, values, (long long*)indices,
-                       (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k);
+                       (u64*)work, arrivals, cols, chunk, nchunks, k);
     return (int)hipGetLastError();
   }
   if (e == 16)
@@ -1201,10 +1295,10 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
 
 // topk/kernel.cu:549 `launch`: values [rows, k] in x's dtype and int64 indices [rows, k], sorted descending with ties
 // by the lowest index. work: u64 [rows * nchunks * k] with nchunks = ceil(cols / chunk), used when nchunks > 1;
-// counters: u32 [>= rows], zero on entry and zero again when the launch completes (the k <= 64 kernel counts each
-// split row's chunk arrivals there, as the reference's). Checks as the
-// reference's, except that k may be up to 1024 (the reference stops at 512): rows <= 0 or k <= 0 is a no-op; -1 for
-// k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0, a split row with chunk % 4 or
+// counters: u32 [>= rows], zero on entry and left zero (the k <= 64 kernel counts a split row's chunk arrivals in
+// counters of the library's own instead, one per 256 bytes, kept per device and stream and zero between launches).
+// Checks as the reference's, except that k may be up to 1024 (the reference stops at 512): rows <= 0 or k <= 0 is a
+// no-op; -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0, a split row with chunk % 4 or
 // nchunks * k > INT_MAX / 2, threads not 128, 256 or 512, depth not 2, 4 or 8, or a dtype other than 0 and 1.
 extern "C" int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
                       long long cols, int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream) {
@@ -1216,23 +1310,26 @@ extern "C" int launch(const void* x, void* values, void* indices, void* work, vo
     return rw_host::kInvalid;
   if (dtype == 0) {
     if (cols % 4 == 0 && rw_host::aligned16(x))
-      return launch_chunks<float, true>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
-    return launch_chunks<float, false>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
+      return launch_chunks<float, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
+    return launch_chunks<float, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
   }
   if (dtype == 1) {
     if (cols % 8 == 0 && (chunk % 8 == 0 || nchunks == 1) && rw_host::aligned16(x))
-      return launch_chunks<uint16_t, true>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
-    return launch_chunks<uint16_t, false>(x, values, indices, work, counters, rows, cols, chunk, (int)nchunks, k, stream);
+      return launch_chunks<uint16_t, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
+    return launch_chunks<uint16_t, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
   }
   return rw_host::kInvalid;
 }
 
 // No counterpart in the reference (whose counters self-reset only when a launch completes): zeroes counters[0, rows)
-// on `stream`, for a caller recovering from a launch that did not complete.
+// and the library's arrival counters for `stream` on `stream`, for a caller recovering from a launch that did not
+// complete.
 extern "C" int topk_reset(void* counters, long long rows, hipStream_t stream) {
   if (rows <= 0) return rw_host::kOk;
   if (!counters) return rw_host::kInvalid;
-  return (int)hipMemsetAsync(counters, 0, (size_t)rows * sizeof(unsigned), stream);
+  const int e = (int)hipMemsetAsync(counters, 0, (size_t)rows * sizeof(unsigned), stream);
+  if (e != rw_host::kOk) return e;
+  return rw_host::clear_stream_workspace(stream, kArrivalsPurpose);
 }
 
 // Sampling from a top-k list (no counterpart in the reference: the step after top-k in a decoder's sampler; see

@@ -26,6 +26,11 @@ HIPCC_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
+# Per-op additions. topk: no wave-level atomic optimizer, which turns the start-order count (an atomic by one lane,
+# issued first thing in the k <= 64 kernel) into a broadcast of its result that waits for the atomic before the tile's
+# loads are issued.
+OP_FLAGS = {"topk": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
+
 
 def hipcc():
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
@@ -43,7 +48,7 @@ def build_one(op):
     out = lib_path(op)
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", CSRC, src, "-o", tmp]
+    cmd = [hipcc(), *HIPCC_FLAGS, *OP_FLAGS.get(op, []), "-I", CSRC, src, "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     lines = [l for l in (proc.stdout + proc.stderr).splitlines() if "not a recognized feature" not in l]
     if proc.returncode != 0:

@@ -18,7 +18,7 @@ int launch(const void* x, void* y, long long rows, int cols, int dtype, float ep
 int rmsnorm_launch_weighted(const void* x, const void* weight, void* y, long long rows, int cols, int dtype,
                             float eps, int threads, hipStream_t stream);
 
-/* No counterpart in the reference (the step before an inference layer's norm, SURVEY "next"): fused residual add.
+/* No counterpart in the reference (the step before an inference layer's norm): fused residual add.
  * h = T(x + residual) is written to residual_out, then y = RMSNorm(h), times weight when weight != NULL, in one pass
  * (x and residual read once, residual_out and y written once). residual_out may equal residual and y may equal x.
  * Same checks and codes as launch(); residual or residual_out NULL is -1. */

@@ -1,8 +1,10 @@
 /* topk: the k largest entries of each row of x[rows, cols] in fp32 (dtype 0) or bf16 (dtype 1), sorted descending with
  * ties broken by the lowest index (+0 above -0, +NaN above +inf, -NaN at the bottom: the composite order of the
  * reference), 1 <= k <= 1024. Library: build/topk/libkernel.so. Replaces the reference's topk/kernel.cu:520-570 (ctypes
- * binding topk/candidate.py:31-36). Device pointers; asynchronous on `stream`; no allocation: the caller owns the
- * workspace and counters. */
+ * binding topk/candidate.py:31-36). Device pointers; asynchronous on `stream`. The caller owns the workspace and
+ * counters; for k <= 64 a split row's chunks count their arrivals in counters of the library's own instead (one per
+ * 256 bytes, so that the rows' counting atomics do not share a line), allocated on first use per (device, stream),
+ * grown when a launch needs more, and all zeros between launches. */
 #ifndef ROWKERN_TOPK_H
 #define ROWKERN_TOPK_H
 #include <hip/hip_runtime_api.h>
@@ -17,9 +19,8 @@ extern "C" {
 long long plan(long long rows, long long cols, int dtype, int threads, int depth, int min_chunk);
 
 /* topk/kernel.cu:549: values [rows, k] in x's dtype, indices [rows, k] int64; work: u64 [rows * nchunks * k]
- * (nchunks = ceil(cols / chunk), only used when nchunks > 1); counters: u32 [>= rows], zero on entry and zero again
- * when the launch completes (for k <= 64 a split row's chunks count their arrivals there and the last one merges, as
- * in the reference).
+ * (nchunks = ceil(cols / chunk), only used when nchunks > 1); counters: u32 [>= rows], zero on entry and left zero
+ * (for k <= 64 a split row's last chunk to arrive merges, as in the reference, counted in the library's counters).
  * Returns 0 (rows <= 0 or k <= 0 is a no-op), -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0,
  * a split row with chunk % 4 != 0 or nchunks * k > INT_MAX / 2, threads not 128/256/512, depth not 2/4/8 or an unknown
  * dtype, otherwise the hipError_t of the launch. Launches sharing work/counters must be ordered (one stream). */
@@ -27,11 +28,11 @@ int launch(const void* x, void* values, void* indices, void* work, void* counter
            int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream);
 
 /* No counterpart in the reference (whose counters self-reset only when a launch completes): zeroes counters[0, rows)
- * on `stream`, for a caller recovering from a launch that did not complete. Returns 0, -1 (NULL counters) or the
- * hipError_t of the memset. */
+ * and the library's arrival counters for `stream` on `stream`, for a caller recovering from a launch that did not
+ * complete. Returns 0, -1 (NULL counters) or the hipError_t of a memset. */
 int topk_reset(void* counters, long long rows, hipStream_t stream);
 
-/* No counterpart in the reference (the step after top-k in a decoder's sampler, SURVEY "next"): one index per row drawn
+/* No counterpart in the reference (the step after top-k in a decoder's sampler): one index per row drawn
  * from a top-k list -- values [rows, k] in fp32 (dtype 0) or bf16 (1) and int64 indices [rows, k], as launch() writes
  * them -- with the caller's uniforms[rows] (fp32 in [0, 1)). x = value / temperature, e_i = exp(x_i - max x),
  * S_i = e_0 + ... + e_i; the positions i with i == 0 or S_(i-1) < top_p * S_(k-1) are kept, and the first kept i with

@@ -1,9 +1,11 @@
 """GPU parity of top-k (build/topk/libkernel.so: `plan`, `launch`, `topk_reset`) against the oracle, bit for bit:
 values (the element bits) and int64 indices, sorted descending with ties by the lowest index.
 
-Covers single- and multi-chunk rows (the last-workgroup merge), every k class (1, the lane-maxima seed up to 64, the
-general path up to 1024), ties and special values, bf16, unaligned and ragged rows, workspace reuse and the counters'
-self-reset, adversarial orders that force many prunes, and the top-k workload at k = 1, 50 and 1024.
+Covers single- and multi-chunk rows (the merge by the row's last workgroup to arrive, counted in the library's
+arrival counters), every k class (1, the lane-maxima bound up to 64, the general path up to 1024), ties and special
+values, negative rows and the all-ones NaN (the value the k <= 64 kernel pads tiles with), bf16, unaligned and ragged
+rows, workspace reuse, the arrival counters' growth, reset and self-reset, adversarial orders that force many prunes,
+and the top-k workload at k = 1, 50 and 1024.
 """
 
 import numpy as np
@@ -107,6 +109,46 @@ def test_adversarial_orders(pkg, oracle, dev):
     c = torch.randn(2, 30000, generator=g)
     c[:, ::3] = 5.0 + torch.arange(10000).float() * 1e-7
     check(pkg, oracle, c, 1024, dev, what="cluster")
+
+
+def test_negative_rows_and_all_ones_nan(pkg, oracle, dev):
+    # log-probabilities: every value negative, so the bound and the admission compare work on reversed bit orders
+    g = torch.Generator().manual_seed(6)
+    lp = torch.log_softmax(torch.randn(4, 40000, generator=g) * 3, dim=-1)
+    for k in (1, 50):
+        check(pkg, oracle, lp, k, dev, what="log-probs")
+        check(pkg, oracle, lp, k, dev, chunk=8192, what="log-probs split")
+    # the all-ones NaN (bits 0xffffffff, the lowest key) among values, as the whole row but one, and as the k-th
+    x = torch.randn(3, 20000, generator=g)
+    xi = x.view(torch.int32)
+    xi[0, ::7] = -1
+    xi[1] = -1
+    x[1, 5] = 1.0
+    xi[2, :19990] = -1
+    for k in (1, 13, 50):
+        check(pkg, oracle, x, k, dev, what="all-ones nan")
+        check(pkg, oracle, x, k, dev, chunk=4096, what="all-ones nan split")
+    xb = torch.randn(3, 20000, generator=g).bfloat16()
+    xbi = xb.view(torch.int16)
+    xbi[0, ::7] = -1
+    xbi[1] = -1
+    xb[1, 5] = 1.0
+    xbi[2, :19990] = -1
+    for k in (1, 50):
+        check(pkg, oracle, xb, k, dev, what="bf16 all-ones nan")
+        check(pkg, oracle, xb, k, dev, chunk=4096, what="bf16 all-ones nan split")
+
+
+def test_handoff_workspace_across_shapes(pkg, oracle, dev):
+    # back-to-back split launches on one stream, growing (a reallocation of the arrival counters) and shrinking:
+    # every launch must leave the counters all zeros for the next; topk_reset clears them as well
+    g = torch.Generator().manual_seed(7)
+    for rows, cols, k, chunk in [(2, 9000, 7, 2048), (512, 32000, 64, 1024), (3, 20000, 64, 1024), (64, 40000, 50, 4096),
+                                 (2, 9000, 7, 2048)]:
+        check(pkg, oracle, torch.randn(rows, cols, generator=g), k, dev, chunk=chunk, what="hand-off reuse")
+    counters = torch.zeros(8, dtype=torch.int32, device=dev)
+    assert lib(pkg).topk_reset(counters.data_ptr(), 8, torch.cuda.current_stream().cuda_stream) == 0
+    check(pkg, oracle, torch.randn(5, 30000, generator=g), 50, dev, chunk=4096, what="after reset")
 
 
 def test_bf16_and_unaligned(pkg, oracle, dev):
