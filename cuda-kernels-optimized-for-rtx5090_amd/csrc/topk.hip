@@ -9,20 +9,9 @@
 // k <= 64: topk_tile, one kernel (see its comment); the row's last workgroup merges the chunk lists, handed over
 // through device-coherent stores and loads and a per-row arrival counter, as the reference's last-block merge.
 //
-// k > 64: two kernels on the caller's stream (the stream order publishes the first kernel's workspace to the second):
-//  - topk_chunks, one 256-thread workgroup per (chunk, row): the workgroup loads a block of its chunk (E elements per
-//    lane, 16-byte loads, all in flight at once) into registers and admits the block's top-k into an LDS buffer:
-//      seed   - for k <= 64 each wave ranks its 64 lane maxima (v_readlane broadcasts, no barrier) and takes the k-th;
-//               k distinct elements lie at or above it, and the block takes the largest such wave seed;
-//      admit  - if the composites >= the seed fit the buffer they are appended (one LDS atomic per wave: ballot,
-//               popcount, mbcnt), otherwise 256-bin histograms over the register values narrow the range [lo, hi]
-//               holding the k-th (bins (c - lo) >> s, adaptive to the data) until the rest fits;
-//    then prunes the buffer to exactly its k largest with the same histogram narrowing over LDS. A chunk longer than
-//    one register block repeats this per block, from the buffer's current k-th. With one chunk per row it sorts and
-//    writes the outputs; otherwise it writes its k composites (smallest first) to the workspace.
-//  - topk_merge, one workgroup per split row: streams the row's nchunks * k composites through the buffer from a floor
-//    equal to the largest chunk minimum (each full list holds k composites at or above its minimum), prunes to k,
-//    sorts (bitonic in LDS) and writes values and int64 indices.
+// 64 < k <= 1024: topk_wide, one kernel of the same shape (see its comment): a bound from group maxima admits about
+// 1.4k elements per tile, the row's last workgroup merges the chunks' candidate lists from a floor made of their
+// published bounds, and the output row is ordered by bucketing and ranking in LDS.
 #include <climits>
 #include <cstdint>
 #include <type_traits>
@@ -40,14 +29,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kBins = 256;
 constexpr int kMaxK = 1024;
-constexpr int kChunkBuf = 2048;   // chunk kernel buffer: k composites kept + a block's admissions
-constexpr int kMergeBuf = 4096;   // merge kernel buffer: k kept + one 2048-composite tile
-constexpr int kMergePer = 8;      // composites per lane per merge tile
-constexpr int kMergeTile = kThreads * kMergePer;
-constexpr int kSeedMaxK = 64;
-
-static_assert(2 * kMaxK <= kChunkBuf, "a block's top-k must fit beside the kept k");
-static_assert(kMaxK + kMergeTile <= kMergeBuf, "a merge tile must fit beside the kept k");
+constexpr int kSeedMaxK = 64;  // the largest k of the tile kernel
 
 template <int CAP>
 struct Smem {
@@ -59,6 +41,7 @@ struct Smem {
   int count;     // composites in buf
   int bin;       // narrowing: the bin holding the wanted rank
   int above;     // narrowing: composites in the bins above it
+  int last;      // the row's last arrival (split rows of the 64 < k kernel)
 };
 
 __device__ __forceinline__ u64 composite(uint32_t u, uint32_t index) {
@@ -260,216 +243,9 @@ __device__ void prune(S& s, int k) {
   __syncthreads();
 }
 
-// Sorts buf[0, n) descending (bitonic over the next power of two >= 64, padded with 0).
-template <typename S>
-__device__ void sort_desc(S& s, int n) {
-  int m = 64;
-  while (m < n) m <<= 1;
-  for (int i = n + (int)threadIdx.x; i < m; i += kThreads) s.buf[i] = 0ull;
-  __syncthreads();
-  for (int size = 2; size <= m; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < (m >> 1); i += kThreads) {
-        const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1)), hi = lo + stride;
-        const u64 a = s.buf[lo], b = s.buf[hi];
-        const bool desc = (lo & size) == 0;
-        if (desc ? a < b : a > b) {
-          s.buf[lo] = b;
-          s.buf[hi] = a;
-        }
-      }
-      __syncthreads();
-    }
-  }
-}
-
 template <typename T> struct Fmt;
 template <> struct Fmt<float> { static constexpr int W = 4; };      // elements per 16-byte vector
 template <> struct Fmt<uint16_t> { static constexpr int W = 8; };
-
-template <typename T>
-__device__ __forceinline__ void write_outputs(void* values, long long* indices, long long row, int k, const u64* buf,
-                                              int n) {
-  for (int j = threadIdx.x; j < k; j += kThreads) {
-    const u64 c = j < n ? buf[j] : 0ull;
-    if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + j] = composite_bits(c);
-    else static_cast<uint16_t*>(values)[row * k + j] = (uint16_t)(composite_bits(c) >> 16);
-    indices[row * k + j] = composite_index(c);
-  }
-}
-
-// ---- chunk kernel ----------------------------------------------------------------------------------------------------
-
-// A register block: lane t of LANES holds vectors v * LANES + t (v < NV) of elements [b0, b1) of a row, W elements
-// each.
-template <typename T, bool VEC, int E, int LANES = kThreads>
-struct Block {
-  static constexpr int W = Fmt<T>::W;
-  static constexpr int NV = E / W;
-  static_assert(NV * W == E, "E must be a multiple of the vector width");
-  u32x4 r[NV];
-  int b0, b1;  // element offsets within the row (cols <= INT_MAX / 2)
-
-  __device__ __forceinline__ void load(const T* row) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int e0 = b0 + (v * LANES + (int)threadIdx.x) * W;
-      if constexpr (VEC) {
-        const int e = e0 < b1 ? e0 : b1 - W;  // an in-range duplicate, skipped by each_vec()
-        r[v] = load16<true>(row + e, 0);
-      } else {
-        uint32_t u[W];
-#pragma unroll
-        for (int j = 0; j < W; ++j) {
-          const int e = e0 + j;
-          if constexpr (sizeof(T) == 4) u[j] = e < b1 ? reinterpret_cast<const uint32_t*>(row)[e] : 0u;
-          else u[j] = e < b1 ? (uint32_t)reinterpret_cast<const uint16_t*>(row)[e] : 0u;
-        }
-        if constexpr (sizeof(T) == 4) r[v] = (u32x4){u[0], u[1], u[2], u[3]};
-        else r[v] = (u32x4){u[0] | (u[1] << 16), u[2] | (u[3] << 16), u[4] | (u[5] << 16), u[6] | (u[7] << 16)};
-      }
-    }
-  }
-
-  // f(c, ok) for each vector of this lane: c[W] its composites, ok[W] whether each element lies in [b0, b1). Each call
-  // recomputes the composites from the raw registers: the empty asm makes them opaque, so the compiler does not keep
-  // E 64-bit composites alive across the selection passes.
-  template <typename F>
-  __device__ __forceinline__ void each_vec(F f) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) asm volatile("" : "+v"(r[v]));
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int e0 = b0 + (v * LANES + (int)threadIdx.x) * W;
-      const bool vin = e0 < b1;
-      const uint32_t i0 = (uint32_t)e0;
-      u64 c[W];
-      bool ok[W];
-#pragma unroll
-      for (int j = 0; j < W; ++j) {
-        uint32_t u;
-        if constexpr (sizeof(T) == 4) {
-          u = r[v][j];
-        } else {
-          const uint32_t w = r[v][j >> 1];
-          u = (j & 1) ? (w & 0xffff0000u) : (w << 16);
-        }
-        ok[j] = VEC ? vin : (e0 + j < b1);
-        c[j] = composite(u, i0 + (uint32_t)j);
-      }
-      f(c, ok);
-    }
-  }
-
-  // f(composite) for every element of this lane in [b0, b1).
-  template <typename F>
-  __device__ __forceinline__ void each(F f) {
-    each_vec([&](const u64 (&c)[W], const bool (&ok)[W]) {
-#pragma unroll
-      for (int j = 0; j < W; ++j)
-        if (ok[j]) f(c[j]);
-    });
-  }
-};
-
-// Admits the block's top-k composites (among those >= the buffer's threshold) into the buffer, which holds at most k
-// on entry: exactly the block's top-k, or a superset of them when it fits beside the kept k.
-template <typename S, typename B>
-__device__ void admit_block(S& s, B& blk, int k) {
-  // lane maximum; for k <= 64 the wave's seed is the k-th largest of its lane maxima (k distinct elements at or above)
-  u64 m = 0;
-  blk.each([&](u64 c) { m = c > m ? c : m; });
-  u64 seed = 1;
-  if (k == 1) {
-    seed = wave_ext64<true>(m);
-  } else if (k <= kSeedMaxK) {
-    int rank = 0;
-#pragma unroll 8
-    for (int j = 0; j < kWave; ++j) rank += readlane64(m, j) > m;
-    const u64 hit = __ballot(m != 0 && rank == k - 1);
-    if (hit) seed = readlane64(m, (int)__builtin_ctzll(hit));
-  }
-  const u64 hi = block_ext64<true>(m, s);
-  const u64 seed_blk = block_ext64<true>(seed, s);
-  u64 lo = seed_blk > s.thr ? seed_blk : s.thr;
-  if (hi < lo) return;  // nothing here reaches the buffer's k-th
-  int n = 0;
-  blk.each([&](u64 c) { n += c >= lo; });
-  n = block_count(n, s);
-  int r = k < n ? k : n, above = 0;
-  u64 h = hi;
-  // narrow until the composites >= lo fit beside the buffer; [lo, h] keeps the block's r-th largest of the range
-  while (s.count + n > kChunkBuf && lo < h) {
-    const int pop = narrow(s, [&](auto f) { blk.each(f); }, lo, h, r, above);
-    n = above + pop;
-  }
-  const u64 floor = lo;
-  blk.each_vec([&](const u64 (&c)[B::W], const bool (&ok)[B::W]) {
-    bool keep[B::W];
-    bool any = false;
-#pragma unroll
-    for (int j = 0; j < B::W; ++j) {
-      keep[j] = ok[j] && c[j] >= floor;
-      any |= keep[j];
-    }
-    if (__ballot(any)) append<B::W>(s, c, keep);
-  });
-  __syncthreads();
-}
-
-template <typename T, bool VEC, int E>
-__global__ void __launch_bounds__(kThreads)
-    topk_chunks(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
-                u64* __restrict__ work, long long cols, long long chunk, int nchunks, int k) {
-  __shared__ Smem<kChunkBuf> s;
-  const long long row = blockIdx.y;
-  const int part = blockIdx.x;
-  const int begin = (int)((long long)part * chunk);
-  const int end = (int)(begin + chunk < cols ? begin + chunk : cols);
-  const T* xr = x + row * cols;
-  if (threadIdx.x == 0) {
-    s.count = 0;
-    s.thr = 1;
-  }
-  __syncthreads();
-  constexpr int CH = kThreads * E;
-  for (int b0 = begin; b0 < end; b0 += CH) {
-    Block<T, VEC, E> blk;
-    blk.b0 = b0;
-    blk.b1 = end - b0 > CH ? b0 + CH : end;
-    blk.load(xr);
-    prune(s, k);  // at most k kept, threshold at the k-th
-    admit_block(s, blk, k);
-  }
-  prune(s, k);
-  const int n = s.count;
-  if (nchunks == 1) {
-    sort_desc(s, n);
-    write_outputs<T>(values, indices, row, k, s.buf, n);
-    return;
-  }
-  // the list with its smallest composite first (0 first when the chunk holds fewer than k elements)
-  u64 mn = ~0ull;
-  for (int j = threadIdx.x; j < k; j += kThreads) {
-    const u64 v = j < n ? s.buf[j] : 0ull;
-    mn = v < mn ? v : mn;
-  }
-  mn = block_ext64<false>(mn, s);
-  if (threadIdx.x == 0) s.bin = 0;
-  __syncthreads();
-  for (int j = threadIdx.x; j < n; j += kThreads)
-    if (s.buf[j] == mn) s.bin = j;
-  __syncthreads();
-  const int at = n < k ? n : s.bin;
-  u64* wr = work + (row * nchunks + part) * (long long)k;
-  for (int j = threadIdx.x; j < k; j += kThreads) {
-    u64 v;
-    if (j == 0) v = at < n ? s.buf[at] : 0ull;
-    else if (j == at) v = s.buf[0];
-    else v = j < n ? s.buf[j] : 0ull;
-    wr[j] = v;
-  }
-}
 
 // ---- tile kernels (k <= 64) ---------------------------------------------------------------------------------------
 
@@ -789,6 +565,8 @@ __device__ __forceinline__ void finish_list(TileSmem& s, const TileList& L, void
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 
+constexpr int kWideGroups = 8;  // groups per lane for the admission bound of the 64 < k <= 1024 kernel
+
 // What a vector load past a tile's end reads instead (all ones: the sentinel below).
 __device__ u32x4 g_sentinel_vec = {~0u, ~0u, ~0u, ~0u};
 
@@ -905,6 +683,112 @@ struct Tile {
         for (int j = 0; j < W; ++j) L.push_mask(m[j], a[j], [&] { return comp(v, j); });
       }
     }
+  }
+
+  // Keys of the lane's kWideGroups groups of 64 / kWideGroups elements (vectors g * VPG .. g * VPG + VPG - 1): each
+  // group's largest element in key order, 0 (counted nowhere) for a group past the tile's end.
+  __device__ __forceinline__ void group_keys(uint32_t (&g)[kWideGroups]) const {
+    constexpr int VPG = NV / kWideGroups;
+    static_assert(VPG * kWideGroups == NV, "groups must be whole vectors");
+#pragma unroll
+    for (int gi = 0; gi < kWideGroups; ++gi) {
+      uint32_t key;
+      if constexpr (sizeof(T) == 4) {
+        int mx = INT_MIN, mn = INT_MAX;
+#pragma unroll
+        for (int v = gi * VPG; v < gi * VPG + VPG; ++v)
+#pragma unroll
+          for (int j = 0; j < W; ++j) {
+            const int x = (int)r[v][j];
+            mx = x > mx ? x : mx;
+            mn = x < mn ? x : mn;
+          }
+        key = key_of((uint32_t)(mx >= 0 ? mx : mn));
+      } else {
+        s16x2 mx = {(short)-32768, (short)-32768}, mn = {(short)32767, (short)32767};
+#pragma unroll
+        for (int v = gi * VPG; v < gi * VPG + VPG; ++v)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const s16x2 x = __builtin_bit_cast(s16x2, r[v][j]);
+            mx = __builtin_elementwise_max(mx, x);
+            mn = __builtin_elementwise_min(mn, x);
+          }
+        const uint32_t kl = key_of((uint32_t)(uint16_t)(mx.x >= 0 ? mx.x : mn.x) << 16);
+        const uint32_t kh = key_of((uint32_t)(uint16_t)(mx.y >= 0 ? mx.y : mn.y) << 16);
+        key = kl > kh ? kl : kh;
+      }
+      g[gi] = first(gi * VPG) < b1 ? key : 0u;
+    }
+  }
+
+  // filter() into a shared buffer: appends every element with key >= K (K above the sentinel's key; NEG: K is a
+  // negative value) to s.buf, reserving each batch of 16 elements per lane with one LDS atomic per wave. Appends past
+  // the buffer's end are counted in s.count and not stored.
+  template <bool NEG, typename S>
+  __device__ __forceinline__ void filter_append(S& s, uint32_t K) {
+    constexpr int VB = 16 / W;  // vectors per batch
+    const uint32_t t = bits_of(K);
+#pragma unroll
+    for (int v0 = 0; v0 < NV; v0 += VB) {
+      bool a[VB][W];
+      u64 m[VB][W];
+      int tot = 0;
+#pragma unroll
+      for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+          const int v = v0 + vb;
+          if constexpr (sizeof(T) == 4) {
+            a[vb][j] = NEG ? r[v][j] <= t : (int)r[v][j] >= (int)t;
+          } else {
+            const uint32_t w = r[v][j >> 1];
+            if (j & 1) a[vb][j] = NEG ? w <= (t | 0xffffu) : (int)w >= (int)t;
+            else a[vb][j] = NEG ? (uint16_t)w <= (uint16_t)(t >> 16)
+                                : (int16_t)(uint16_t)w >= (int16_t)(uint16_t)(t >> 16);
+          }
+          m[vb][j] = __ballot(a[vb][j]);
+          tot += __popcll(m[vb][j]);
+        }
+      if (tot) {
+        int base = 0;
+        if (lane_id() == 0) base = atomicAdd(&s.count, tot);
+        base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+        for (int vb = 0; vb < VB; ++vb)
+#pragma unroll
+          for (int j = 0; j < W; ++j) {
+            const u64 mm = m[vb][j];
+            if (mm) {
+              if (a[vb][j]) {
+                const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)mm, (uint32_t)base));
+                if (pos < (int)(sizeof(s.buf) / sizeof(u64))) s.buf[pos] = comp(v0 + vb, j);
+              }
+              base += __popcll(mm);
+            }
+          }
+      }
+    }
+  }
+
+  // Appends the elements of vector v, held in r[0], with composites >= floor to s.buf (exact validity; the caller
+  // keeps room for them); then moves the later vectors down one place (as push_first).
+  template <typename S>
+  __device__ __forceinline__ void append_first(S& s, int v, u64 floor) {
+    const int e0 = first(v);
+    u64 c[W];
+    bool keep[W];
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      c[j] = ((u64)key_of(bits(0, j)) << 32) | (u64)(~(uint32_t)(e0 + j));
+      keep[j] = (VEC ? e0 < b1 : e0 + j < b1) && c[j] >= floor;
+      any |= keep[j];
+    }
+    if (__ballot(any)) append<W>(s, c, keep);
+#pragma unroll
+    for (int i = 0; i + 1 < NV; ++i) r[i] = r[i + 1];
   }
 
   // Pushes the elements of vector v, held in r[0], with composites >= floor, calling check() after every 4 per lane;
@@ -1075,49 +959,294 @@ __global__ void __launch_bounds__(kThreads)
     __hip_atomic_store(arrivals + row * kArrivalStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ---- merge kernel ----------------------------------------------------------------------------------------------------
+// ---- wide kernel (64 < k <= 1024) ----------------------------------------------------------------------------------
 
-template <typename T>
-__global__ void __launch_bounds__(kThreads)
-    topk_merge(void* __restrict__ values, long long* __restrict__ indices, const u64* __restrict__ work, int nchunks,
-               int k) {
-  __shared__ Smem<kMergeBuf> s;
-  const long long row = blockIdx.x;
-  const u64* wr = work + row * (long long)nchunks * k;
-  // floor: the largest chunk minimum (slot 0 of each list)
-  u64 fl = 0;
-  for (int c = threadIdx.x; c < nchunks; c += kThreads) {
-    const u64 v = wr[(long long)c * k];
-    fl = v > fl ? v : fl;
+// Orders one wave's LDS writes before its later LDS reads of other lanes' entries (a wave's LDS operations execute in
+// order; this keeps the compiler from moving them across).
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
+
+constexpr int kWideCap = 4096;    // the wide kernel's candidate buffer (composites)
+constexpr int kWideList = 2048;   // the most candidates a chunk publishes (it prunes to k beyond)
+constexpr int kWideHead = 4;      // a published list's header: count, k-bound, q-bound, unused
+constexpr int kWideSlot = kWideHead + kWideList;
+constexpr int kWideMaxChunks = 256;
+
+constexpr int kRankBuckets = 2048;  // buckets of write_ranked
+
+// Writes the k largest of the m candidates s.buf[0, m) (k <= m <= kWideList), in order, as the output row: the
+// candidates are bucketed by their distance below the largest, (max - c) >> sh with sh chosen so that the range fills
+// kRankBuckets buckets, with LDS counters; an exclusive scan of the counts gives each bucket's first output position;
+// the candidates are scattered by bucket into LDS, and each one's position is its bucket's first plus the number of
+// its bucket's members above it. Nearly linear on spread-out values; a bucket holding many candidates (values
+// clustered far below an outlier) costs its size per member. Every thread calls it.
+template <typename T, typename S>
+__device__ void write_ranked(S& s, int m, int k, void* values, long long* indices, long long row) {
+  constexpr int P = kWideList / kThreads;
+  constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan
+  static_assert(kWideList * 2 <= kWideCap && kRankBuckets * 2 * sizeof(unsigned) <= kWideList * sizeof(u64),
+                "the bucketed copy and the counters share the buffer");
+  const int t = (int)threadIdx.x;
+  u64 c[P];
+  u64 mx = 0, mn = ~0ull;
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    const int i = r * kThreads + t;
+    c[r] = i < m ? s.buf[i] : 0ull;
+    if (i < m) {
+      mx = c[r] > mx ? c[r] : mx;
+      mn = c[r] < mn ? c[r] : mn;
+    }
   }
-  fl = block_ext64<true>(fl, s);
-  if (threadIdx.x == 0) {
-    s.count = 0;
-    s.thr = fl > 1 ? fl : 1;
+  mx = block_ext64<true>(mx, s);  // also orders every read of s.buf above before the writes below
+  mn = block_ext64<false>(mn, s);
+  const u64 range = mx - mn;
+  const int bits = range ? 64 - __clzll(range) : 0;
+  const int sh = bits > 11 ? bits - 11 : 0;
+  u64* sorted = s.buf;
+  unsigned* cnt = reinterpret_cast<unsigned*>(s.buf + kWideList);
+  unsigned* first = cnt + kRankBuckets;
+  for (int b = t; b < kRankBuckets; b += kThreads) cnt[b] = 0;
+  __syncthreads();
+  int bk[P], slot[P];
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    bk[r] = (int)((mx - c[r]) >> sh);
+    slot[r] = r * kThreads + t < m ? (int)atomicAdd(&cnt[bk[r]], 1u) : 0;
   }
   __syncthreads();
-  const long long total = (long long)nchunks * k;
-  for (long long t0 = 0; t0 < total; t0 += kMergeTile) {
-    const u64 thr = s.thr;
-    u64 c[kMergePer];
-    bool keep[kMergePer];
+  // exclusive scan of the counts, bucket 0 (the largest candidates) first
+  unsigned own[BPT], sum = 0;
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    own[i] = cnt[t * BPT + i];
+    sum += own[i];
+  }
+  unsigned incl = sum;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const unsigned o = __shfl_up(incl, d, kWave);
+    if (lane_id() >= d) incl += o;
+  }
+  if (lane_id() == kWave - 1) s.wsum[wave_id()] = incl;
+  __syncthreads();
+  unsigned run = incl - sum;
+  for (int w = 0; w < wave_id(); ++w) run += s.wsum[w];
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    first[t * BPT + i] = run;
+    run += own[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < P; ++r)
+    if (r * kThreads + t < m) sorted[first[bk[r]] + slot[r]] = c[r];
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    if (r * kThreads + t >= m) continue;
+    const int f = (int)first[bk[r]], n = (int)cnt[bk[r]];
+    int pos = f;
+    for (int j = 0; j < n; ++j) pos += sorted[f + j] > c[r];
+    if (pos < k) {
+      if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + pos] = composite_bits(c[r]);
+      else static_cast<uint16_t*>(values)[row * k + pos] = (uint16_t)(composite_bits(c[r]) >> 16);
+      indices[row * k + pos] = composite_index(c[r]);
+    }
+  }
+}
+
+// A lower bound of the k-th largest of the wave's values v[i] (N per lane; 0 marks no value and is never counted) with
+// at least k values at or above it; 0 when the wave holds fewer than k values. The bitwise search of wave_kth32 over N
+// values per lane.
+template <int N>
+__device__ __forceinline__ uint32_t wave_kth_multi(const uint32_t (&v)[N], int k) {
+  uint32_t mx = 0, mn = 0xffffffffu;
+  int real = 0;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    mx = v[i] > mx ? v[i] : mx;
+    mn = v[i] != 0 && v[i] < mn ? v[i] : mn;
+    real += __popcll(__ballot(v[i] != 0));
+  }
+  if (real < k) return 0u;
+  mx = wave_ext32<true>(mx);
+  mn = wave_ext32<false>(mn);
+  if (mx == mn) return mx;
+  const int top = 31 - __builtin_clz(mx ^ mn);
+  uint32_t p = mx & ~((2u << top) - 1u);
+  for (int b = top; b >= 0 && b > top - kThrBits; --b) {
+    const uint32_t cand = p | (1u << b);
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) c += __popcll(__ballot(v[i] >= cand));
+    if (c >= k) p = cand;
+  }
+  return p;
+}
+
+// 64 < k <= 1024: one 256-thread workgroup per (chunk, row), the chunk in register tiles as topk_tile. Per tile: each
+// lane's 64 elements form kWideGroups groups; a group's largest element has the group behind it, so each wave's
+// ceil(k / 4)-th largest group maximum has that many distinct elements at or above it and the smallest of the four
+// waves' has at least k: with the k-th of the earlier tiles it is the admission key (about k * 1.4 admitted per tile
+// on continuous data). The same bound for q = ceil(k / nchunks) gives a q-bound. Admitted elements are appended to an
+// LDS buffer (one LDS atomic per wave and 16 elements per lane); a tile that overflows it (ties, adversarial orders)
+// is appended again vector by vector from the buffer's k-th, pruning to k (histogram narrowing) whenever a vector
+// might not fit. An unsplit row sorts its candidates (bitonic, registers and LDS) and writes the first k. A split
+// row's chunk publishes its candidates (at most kWideList: pruned to k beyond) with its k- and q-bounds to its list in
+// the library's workspace with device-coherent stores, waits for them and counts its arrival; the row's last arrival
+// merges: every chunk has k elements at or above its k-bound and q at or above its q-bound, so the largest k-bound
+// and, when every chunk has one, the smallest q-bound (nchunks * q >= k elements at or above it) bound the row's k-th
+// from below; the lists' candidates at or above that floor (about k * 1.4) are gathered, sorted and the first k
+// written out.
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+    topk_wide(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
+              u64* __restrict__ lists, unsigned* __restrict__ arrivals, long long cols, long long chunk, int nchunks,
+              int k) {
+  __shared__ Smem<kWideCap> s;
+  __shared__ uint32_t redslots[2][kWaves];
+  __shared__ int counts[kWideMaxChunks];
+  const long long row = blockIdx.y;
+  const int part = blockIdx.x;
+  const int begin = (int)((long long)part * chunk);
+  const int end = (int)(begin + chunk < cols ? begin + chunk : cols);
+  const T* xr = x + row * cols;
+  BlockRed red;
+  red.slot = redslots;
+  red.phase = 0;
+  if (threadIdx.x == 0) {
+    s.count = 0;
+    s.thr = 1;
+  }
+  __syncthreads();
+  uint32_t thr = 0, thq = 0;
+  const int q = (k + nchunks - 1) / nchunks;
+  const int kw = (k + kWaves - 1) / kWaves, kwq = (q + kWaves - 1) / kWaves;
+  using TL = Tile<T, VEC>;
+  constexpr int TE = kThreads * kTileE;
+  constexpr int kStep = kThreads * TL::W;  // what one vector of a tile may append
+  for (int t0 = begin; t0 < end; t0 += TE) {
+    TL tile;
+    tile.load(xr, t0, end);
+    const int cnt0 = s.count;  // block-uniform: the buffer is settled between tiles
+    uint32_t g[kWideGroups];
+    tile.group_keys(g);
+    const uint32_t tb = red.min(wave_kth_multi<kWideGroups>(g, kw));
+    thr = tb > thr ? tb : thr;
+    if (nchunks > 1) {
+      const uint32_t qb = red.min(wave_kth_multi<kWideGroups>(g, kwq));
+      thq = qb > thq ? qb : thq;
+    }
+    tile.opaque();
+    bool redo = true;
+    if (thr > TL::kSentinelKey) {
+      if (thr & 0x80000000u) tile.template filter_append<false>(s, thr);
+      else tile.template filter_append<true>(s, thr);
+      __syncthreads();
+      redo = s.count > kWideCap;
+    }
+    if (redo) {  // every element may pass, or the buffer overflowed: append again vector by vector, pruning to k
+      __syncthreads();
+      if (threadIdx.x == 0) s.count = cnt0;
+      __syncthreads();
+      const u64 bound = thr > TL::kSentinelKey ? (u64)thr << 32 : 0ull;
+      for (int v = 0; v < TL::NV; ++v) {
+        if (s.count > kWideCap - kStep) prune(s, k);
+        const u64 floor = s.thr > bound ? s.thr : bound;
+        tile.append_first(s, v, floor);
+        __syncthreads();
+      }
+    }
+    if (end - t0 > TE && s.count > kWideCap - kWideList) {  // before another tile: room for a tile's candidates
+      prune(s, k);
+      const uint32_t kk = (uint32_t)(s.thr >> 32);
+      thr = kk > thr ? kk : thr;
+    }
+  }
+  if (nchunks == 1) {
+    if (s.count > kWideList) prune(s, k);
+    write_ranked<T>(s, s.count, k, values, indices, row);
+    return;
+  }
+  if (s.count > kWideList) prune(s, k);
+  const int n = s.count;
+  // publish: header (count, k-bound, q-bound) and the candidates
+  u64* wr = lists + row * (long long)nchunks * kWideSlot;
+  u64* mine = wr + (long long)part * kWideSlot;
+  auto put = [&](int at, u64 v) { __hip_atomic_store(mine + at, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  for (int i = threadIdx.x; i < n; i += kThreads) put(kWideHead + i, s.buf[i]);
+  if (threadIdx.x == 0) {
+    const u64 kb = (u64)thr << 32;
+    put(0, (u64)n);
+    put(1, s.thr > kb ? s.thr : kb);
+    put(2, (u64)thq << 32);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old =
+        __hip_atomic_fetch_add(arrivals + row * kArrivalStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s.last = old == (unsigned)nchunks - 1;
+  }
+  __syncthreads();
+  if (!s.last) return;
+  // merge (the row's last arrival): the floor from the headers, then every list's candidates at or above it
+  auto ld = [&](long long at) { return __hip_atomic_load(wr + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  u64 kmax = 0, qmn = ~0ull;
+  for (int c = threadIdx.x; c < nchunks; c += kThreads) {
+    counts[c] = (int)ld((long long)c * kWideSlot);
+    const u64 kb = ld((long long)c * kWideSlot + 1), qb = ld((long long)c * kWideSlot + 2);
+    kmax = kb > kmax ? kb : kmax;
+    qmn = qb < qmn ? qb : qmn;
+  }
+  kmax = block_ext64<true>(kmax, s);
+  qmn = block_ext64<false>(qmn, s);  // 0 when a chunk has no q-bound
+  u64 floor = kmax > qmn ? kmax : qmn;
+  floor = floor > 1 ? floor : 1;
+  if (threadIdx.x == 0) {
+    s.count = 0;
+    s.thr = floor;
+  }
+  __syncthreads();
+  constexpr int PER = kWideList / kThreads;
+  u64 ca[PER], cb[PER];
+  auto load = [&](int c, u64 (&v)[PER]) {
+    const int cnt = counts[c];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int at = i * kThreads + (int)threadIdx.x;
+      v[i] = at < cnt ? ld((long long)c * kWideSlot + kWideHead + at) : 0ull;
+    }
+  };
+  auto take = [&](const u64 (&v)[PER]) {  // appends the entries at or above the floor (room for a list is kept)
+    if (s.count > kWideCap - kWideList) prune(s, k);
+    const u64 f = s.thr;
+    bool keep[PER];
     bool any = false;
 #pragma unroll
-    for (int j = 0; j < kMergePer; ++j) {
-      const long long i = t0 + (long long)j * kThreads + (int)threadIdx.x;
-      c[j] = i < total ? wr[i] : 0ull;
-      keep[j] = c[j] >= thr;
-      any |= keep[j];
+    for (int i = 0; i < PER; ++i) {
+      keep[i] = v[i] >= f;
+      any |= keep[i];
     }
-    int fill = 0;
-    if (__ballot(any)) fill = append<kMergePer>(s, c, keep);
-    // one block-wide decision per tile (every wave branches alike even if one has moved on to the next tile)
-    if (__syncthreads_or(fill > kMergeBuf - kMergeTile)) prune(s, k);
+    if (__ballot(any)) append<PER>(s, v, keep);
+    __syncthreads();
+  };
+  load(0, ca);
+  for (int c = 0; c < nchunks; c += 2) {  // the next list's loads are in flight while one is taken
+    if (c + 1 < nchunks) load(c + 1, cb);
+    take(ca);
+    if (c + 1 < nchunks) {
+      if (c + 2 < nchunks) load(c + 2, ca);
+      take(cb);
+    }
   }
-  prune(s, k);
-  const int n = s.count;
-  sort_desc(s, n);
-  write_outputs<T>(values, indices, row, k, s.buf, n);
+  if (s.count > kWideList) prune(s, k);
+  write_ranked<T>(s, s.count, k, values, indices, row);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(arrivals + row * kArrivalStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- sampling from the top k ----------------------------------------------------------------------------------------
@@ -1214,22 +1343,15 @@ __global__ void __launch_bounds__(kWave)
 
 // ---- host side -------------------------------------------------------------------------------------------------------
 
-// Tuning slots (0 = automatic): 0 resident workgroups per CU assumed by plan(), 1 elements per lane of a register
-// block (16, 32 or 64).
-enum { kTuneBlocksPerCu = 0, kTuneE = 1 };
-constexpr int kArrivalsPurpose = 2;  // stream_workspace key of the k <= 64 arrival counters
-constexpr int kDefaultE = 32;
-
-int lane_elems() {
-  const int e = rw_host::tune_get(kTuneE);
-  return (e == 16 || e == 32 || e == 64) ? e : kDefaultE;
-}
+// Tuning slot (0 = automatic): 0 resident workgroups per CU assumed by plan().
+enum { kTuneBlocksPerCu = 0 };
+constexpr int kArrivalsPurpose = 2;  // stream_workspace key of the arrival counters
+constexpr int kListsPurpose = 3;     // stream_workspace key of the 64 < k kernel's published lists
 
 template <typename T, bool VEC>
 int launch_chunks(const void* x, void* values, void* indices, void* work, long long rows,
                   long long cols, long long chunk, int nchunks, int k, hipStream_t stream) {
   const dim3 grid((unsigned)nchunks, (unsigned)rows);
-  const int e = VEC ? lane_elems() : 16;
   if (k <= kSeedMaxK) {
     unsigned* arrivals = nullptr;
     if (nchunks > 1) {  // the arrival counters: zeros between launches, kept per (device, stream)
@@ -1242,18 +1364,28 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, long l
                        (u64*)work, arrivals, cols, chunk, nchunks, k);
     return (int)hipGetLastError();
   }
-  if (e == 16)
-    hipLaunchKernelGGL((topk_chunks<T, VEC, 16>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
-                       (long long*)indices, (u64*)work, cols, chunk, nchunks, k);
-  else if (e == 64)
-    hipLaunchKernelGGL((topk_chunks<T, VEC, 64>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
-                       (long long*)indices, (u64*)work, cols, chunk, nchunks, k);
-  else
-    hipLaunchKernelGGL((topk_chunks<T, VEC, 32>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
-                       (long long*)indices, (u64*)work, cols, chunk, nchunks, k);
-  if (nchunks > 1)
-    hipLaunchKernelGGL((topk_merge<T>), dim3((unsigned)rows), dim3(kThreads), 0, stream, values, (long long*)indices,
-                       (const u64*)work, nchunks, k);
+  // The result does not depend on the chunking, so the chunks are made long enough for a useful bound (16k elements:
+  // a tile holds the 4 * ceil(k / 4) group maxima the bound needs) and few enough for the merge (kWideMaxChunks).
+  long long want = 16LL * k;
+  if (want < (cols + kWideMaxChunks - 1) / kWideMaxChunks) want = (cols + kWideMaxChunks - 1) / kWideMaxChunks;
+  if (chunk < want && nchunks > 1) {
+    chunk = want < cols ? (want + 7) / 8 * 8 : cols;
+    nchunks = (int)((cols + chunk - 1) / chunk);
+  }
+  unsigned* arrivals = nullptr;
+  u64* lists = nullptr;
+  if (nchunks > 1) {
+    int err = rw_host::kOk;
+    arrivals = (unsigned*)rw_host::stream_workspace(stream, (size_t)rows * kArrivalStride * sizeof(unsigned), &err,
+                                                    kArrivalsPurpose, true);
+    if (!arrivals) return err;
+    lists = (u64*)rw_host::stream_workspace(stream, (size_t)rows * nchunks * kWideSlot * sizeof(u64), &err,
+                                            kListsPurpose);
+    if (!lists) return err;
+  }
+  const dim3 wgrid((unsigned)nchunks, (unsigned)rows);
+  hipLaunchKernelGGL((topk_wide<T, VEC>), wgrid, dim3(kThreads), 0, stream, (const T*)x, values, (long long*)indices,
+                     lists, arrivals, cols, chunk, nchunks, k);
   return (int)hipGetLastError();
 }
 
@@ -1294,12 +1426,12 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
 }
 
 // topk/kernel.cu:549 `launch`: values [rows, k] in x's dtype and int64 indices [rows, k], sorted descending with ties
-// by the lowest index. work: u64 [rows * nchunks * k] with nchunks = ceil(cols / chunk), used when nchunks > 1;
-// counters: u32 [>= rows], zero on entry and left zero (the k <= 64 kernel counts a split row's chunk arrivals in
-// counters of the library's own instead, one per 256 bytes, kept per device and stream and zero between launches).
-// Checks as the reference's, except that k may be up to 1024 (the reference stops at 512): rows <= 0 or k <= 0 is a
-// no-op; -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0, a split row with chunk % 4 or
-// nchunks * k > INT_MAX / 2, threads not 128, 256 or 512, depth not 2, 4 or 8, or a dtype other than 0 and 1.
+// by the lowest index. work: u64 [rows * nchunks * k] with nchunks = ceil(cols / chunk), validated as the
+// reference's and not used (the hand-off goes through the library's workspaces, kept per device and stream);
+// counters: u32 [>= rows], zero on entry and left zero. Checks as the reference's, except that k may be up to 1024
+// (the reference stops at 512): rows <= 0 or k <= 0 is a no-op; -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows
+// > 65535, chunk <= 0, a split row with chunk % 4 or nchunks * k > INT_MAX / 2, threads not 128, 256 or 512, depth
+// not 2, 4 or 8, or a dtype other than 0 and 1.
 extern "C" int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
                       long long cols, int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream) {
   if (rows <= 0 || k <= 0) return rw_host::kOk;

@@ -4,8 +4,8 @@ values, indices = the k largest entries of each row of x[m, n] in descending ord
 the lowest index (the reference's topk/candidate.py:1-10 with K = 50). k is inputs["k"] when given (1..1024; the
 reference fixes 50). The one `launch` entry of libkernel.so serves both dtypes: fp32 (0) and bf16 (1), row-major x;
 values keep x's dtype and indices are int64. `plan` picks the columns per workgroup so the grid is one resident wave;
-rows split into several chunks merge through an int64 workspace and a per-row int32 counter (zeroed once, reset by the
-kernel). The plan and workspace of the last shape are cached, so a repeated call allocates only its outputs.
+rows split into several chunks merge in the kernel (the library keeps its hand-off workspaces; the reference's int64
+workspace and per-row int32 counters are still allocated and passed, zeroed once). The plan and workspace of the last shape are cached, so a repeated call allocates only its outputs.
 params.json (optional) may set "log2_threads" (7..9), "log2_depth" (1..3) -- the reference's knobs, validated and not
 needed by this build -- and "min_chunk". The library is $CKOPT_BUILD_DIR/libkernel.so when CKOPT_BUILD_DIR is set,
 else this package's build/topk/libkernel.so.
@@ -68,7 +68,7 @@ def _plan(x, rows, cols, dtype, k=K):
         return _last
     _last = None
     # larger k: larger chunks (fewer lists of k to merge per row)
-    chunk = _lib.plan(rows, cols, dtype, _THREADS, _DEPTH, max(_MIN_CHUNK, 32 * k) if k > 64 else _MIN_CHUNK)
+    chunk = _lib.plan(rows, cols, dtype, _THREADS, _DEPTH, max(_MIN_CHUNK, 16 * k) if k > 64 else _MIN_CHUNK)
     nchunks = -(-cols // chunk)
     work = torch.empty(rows * nchunks * k if nchunks > 1 else 1, dtype=torch.int64, device=x.device)
     counters = _row_counters(x.device, rows)

@@ -2,9 +2,10 @@
  * ties broken by the lowest index (+0 above -0, +NaN above +inf, -NaN at the bottom: the composite order of the
  * reference), 1 <= k <= 1024. Library: build/topk/libkernel.so. Replaces the reference's topk/kernel.cu:520-570 (ctypes
  * binding topk/candidate.py:31-36). Device pointers; asynchronous on `stream`. The caller owns the workspace and
- * counters; for k <= 64 a split row's chunks count their arrivals in counters of the library's own instead (one per
- * 256 bytes, so that the rows' counting atomics do not share a line), allocated on first use per (device, stream),
- * grown when a launch needs more, and all zeros between launches. */
+ * counters; a split row's chunks count their arrivals in counters of the library's own instead (one per 256 bytes,
+ * so that the rows' counting atomics do not share a line, all zeros between launches), and for k > 64 hand their
+ * candidate lists over in a workspace of the library's (up to 2052 u64 per chunk); both are allocated on first use
+ * per (device, stream) and grown when a launch needs more. */
 #ifndef ROWKERN_TOPK_H
 #define ROWKERN_TOPK_H
 #include <hip/hip_runtime_api.h>
@@ -19,8 +20,10 @@ extern "C" {
 long long plan(long long rows, long long cols, int dtype, int threads, int depth, int min_chunk);
 
 /* topk/kernel.cu:549: values [rows, k] in x's dtype, indices [rows, k] int64; work: u64 [rows * nchunks * k]
- * (nchunks = ceil(cols / chunk), only used when nchunks > 1); counters: u32 [>= rows], zero on entry and left zero
- * (for k <= 64 a split row's last chunk to arrive merges, as in the reference, counted in the library's counters).
+ * (nchunks = ceil(cols / chunk); validated as the reference's, not used); counters: u32 [>= rows], zero on entry and
+ * left zero (a split row's last chunk to arrive merges, as in the reference, counted in the library's counters; for
+ * k > 64 a row is split into at most 256 chunks, longer than `chunk` when needed, as the result does not depend on
+ * the chunking).
  * Returns 0 (rows <= 0 or k <= 0 is a no-op), -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0,
  * a split row with chunk % 4 != 0 or nchunks * k > INT_MAX / 2, threads not 128/256/512, depth not 2/4/8 or an unknown
  * dtype, otherwise the hipError_t of the launch. Launches sharing work/counters must be ordered (one stream). */
@@ -43,7 +46,7 @@ int topk_sample_launch(const void* values, const void* indices, const float* uni
                        int dtype, float temperature, float top_p, hipStream_t stream);
 
 /* No counterpart in the reference: tuning override for parameter sweeps. Slot 0: resident workgroups per CU assumed by
- * plan(); slot 1: elements per lane of the k > 64 kernel's register block (16, 32 or 64). Returns 0 or -1. */
+ * plan(). Returns 0 or -1. */
 int topk_tune(int slot, int value);
 
 #ifdef __cplusplus
