@@ -1426,9 +1426,9 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
 }
 
 // topk/kernel.cu:549 `launch`: values [rows, k] in x's dtype and int64 indices [rows, k], sorted descending with ties
-// by the lowest index. work: u64 [rows * nchunks * k] with nchunks = ceil(cols / chunk), validated as the
-// reference's and not used (the hand-off goes through the library's workspaces, kept per device and stream);
-// counters: u32 [>= rows], zero on entry and left zero. Checks as the reference's, except that k may be up to 1024
+// by the lowest index. work: u64 [rows * nchunks * k] with nchunks = ceil(cols / chunk), the chunk lists of split rows
+// for k <= 64 (for k > 64 they go through a workspace of the library's); counters: u32 [>= rows], zero on entry and
+// left zero (the arrivals are counted in the library's counters, kept per device and stream). Checks as the reference's, except that k may be up to 1024
 // (the reference stops at 512): rows <= 0 or k <= 0 is a no-op; -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows
 // > 65535, chunk <= 0, a split row with chunk % 4 or nchunks * k > INT_MAX / 2, threads not 128, 256 or 512, depth
 // not 2, 4 or 8, or a dtype other than 0 and 1.

@@ -20,8 +20,8 @@ extern "C" {
 long long plan(long long rows, long long cols, int dtype, int threads, int depth, int min_chunk);
 
 /* topk/kernel.cu:549: values [rows, k] in x's dtype, indices [rows, k] int64; work: u64 [rows * nchunks * k]
- * (nchunks = ceil(cols / chunk); validated as the reference's, not used); counters: u32 [>= rows], zero on entry and
- * left zero (a split row's last chunk to arrive merges, as in the reference, counted in the library's counters; for
+ * (nchunks = ceil(cols / chunk); the chunk lists of split rows for k <= 64); counters: u32 [>= rows], zero on entry
+ * and left zero (a split row's last chunk to arrive merges, as in the reference, counted in the library's counters; for
  * k > 64 a row is split into at most 256 chunks, longer than `chunk` when needed, as the result does not depend on
  * the chunking).
  * Returns 0 (rows <= 0 or k <= 0 is a no-op), -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0,
