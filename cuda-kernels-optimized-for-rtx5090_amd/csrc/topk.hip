@@ -645,7 +645,8 @@ struct Tile {
       for (int v = 0; v < NV; ++v)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const s16x2 x = __builtin_bit_cast(s16x2, r[v][j]);
+          const uint32_t w = r[v][j];  // (bit-casting the element expression itself reads element 0)
+          const s16x2 x = __builtin_bit_cast(s16x2, w);
           mx = __builtin_elementwise_max(mx, x);
           mn = __builtin_elementwise_min(mn, x);
         }
@@ -710,7 +711,8 @@ struct Tile {
         for (int v = gi * VPG; v < gi * VPG + VPG; ++v)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const s16x2 x = __builtin_bit_cast(s16x2, r[v][j]);
+            const uint32_t w = r[v][j];  // (bit-casting the element expression itself reads element 0)
+            const s16x2 x = __builtin_bit_cast(s16x2, w);
             mx = __builtin_elementwise_max(mx, x);
             mn = __builtin_elementwise_min(mn, x);
           }
