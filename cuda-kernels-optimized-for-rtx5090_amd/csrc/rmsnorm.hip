@@ -192,7 +192,7 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// ---- host side -------------------------------------------------------------------------------------------------------
+// ---- host side ------------------------------------------------------------------------------------------------------
 
 // Tuning slots (0 = automatic): waves per row, vectors per lane, resident blocks per CU, forced generic kernel (1),
 // non-temporal loads (1 on, 2 off).
@@ -279,7 +279,8 @@ template <typename T, bool HAS_W, bool RES = false>
 int launch_typed(const void* x, const void* w, void* y, long long rows, int cols, float eps, hipStream_t stream,
                  const void* res = nullptr, void* res_out = nullptr) {
   const bool vec = cols % T::V == 0 && rw_host::aligned16(x) && rw_host::aligned16(y) &&
-                   (!HAS_W || rw_host::aligned16(w)) && (!RES || (rw_host::aligned16(res) && rw_host::aligned16(res_out)));
+                   (!HAS_W || rw_host::aligned16(w)) &&
+                   (!RES || (rw_host::aligned16(res) && rw_host::aligned16(res_out)));
   const long long nvec = cols / T::V;
   if (vec && rw_host::tune_get(kTuneGeneric) != 1 && nvec <= (long long)kMaxWaves * kWave * kMaxNv) {
     int waves = rw_host::tune_get(kTuneWaves), nv = rw_host::tune_get(kTuneNv);

@@ -286,7 +286,7 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// ---- host side -------------------------------------------------------------------------------------------------------
+// ---- host side ------------------------------------------------------------------------------------------------------
 
 // Tuning slots (0 = automatic): threads per block, resident blocks per CU, forced scalar kernel (1).
 enum { kTuneThreads = 0, kTuneBlocksPerCu = 1, kTuneScalar = 2 };
@@ -387,7 +387,8 @@ extern "C" int launch(const void* q, const void* k, const void* cos_rows, const 
                       int qk_dtype, int cache_dtype, int rows, int splits, hipStream_t stream) {
   if (tokens <= 0) return rw_host::kOk;
   if (validate(tokens, q_heads, kv_heads, head_dim, rows, splits)) return rw_host::kInvalid;
-  const Ptrs p{q, k, cos_rows, sin_rows, nullptr, (const long long*)ids, q_out, k_out, Cache{nullptr, nullptr, nullptr}};
+  const Ptrs p{q,     k,     cos_rows, sin_rows, nullptr, (const long long*)ids,
+               q_out, k_out, Cache{nullptr, nullptr, nullptr}};
   const Shape s{tokens, q_heads, kv_heads, head_dim, 0};
   if (qk_dtype == 1) return launch_cache<BF16>(cache_dtype, p, s, stream);
   if (qk_dtype == 2) return launch_cache<F16>(cache_dtype, p, s, stream);

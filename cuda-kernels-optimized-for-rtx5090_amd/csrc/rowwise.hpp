@@ -134,7 +134,7 @@ __device__ __forceinline__ void store16(void* p, long long v, const u32x4& r) {
   else *q = r;
 }
 
-// ---- wave64 reductions -----------------------------------------------------------------------------------------------
+// ---- wave64 reductions ----------------------------------------------------------------------------------------------
 
 // DPP controls: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror. Applied in this order with a
 // commutative operator they leave each 16-lane row holding its row's reduction.

@@ -365,7 +365,7 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// ---- host side -------------------------------------------------------------------------------------------------------
+// ---- host side ------------------------------------------------------------------------------------------------------
 
 // Tuning slots (0 = automatic): row-tier waves per row, row-tier vectors per lane, row-tier resident blocks per CU,
 // split-tier waves, split-tier vectors per lane, forced tier (1 row, 2 split, 3 generic, 4 co-resident), non-temporal
@@ -530,7 +530,8 @@ int launch_typed(const void* x, void* y, long long rows, long long cols, hipStre
     if (tier == 1) return rw_host::kInvalid;
   }
   if (tier == 0 || tier == 4) {
-    const int rc = ntl ? launch_coop<T, true>(x, y, rows, nvec, stream) : launch_coop<T, false>(x, y, rows, nvec, stream);
+    const int rc =
+        ntl ? launch_coop<T, true>(x, y, rows, nvec, stream) : launch_coop<T, false>(x, y, rows, nvec, stream);
     if (rc != 1) return rc;
     if (tier == 4) return rw_host::kInvalid;
   }

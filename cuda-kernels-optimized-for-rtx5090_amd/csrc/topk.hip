@@ -76,7 +76,8 @@ __device__ __forceinline__ u64 wave_ext64(u64 v) {
   v = pick64<MAX>(v, dpp64<kDppXor2>(v));
   v = pick64<MAX>(v, dpp64<kDppHalfMirror>(v));
   v = pick64<MAX>(v, dpp64<kDppMirror>(v));
-  return pick64<MAX>(pick64<MAX>(readlane64(v, 0), readlane64(v, 16)), pick64<MAX>(readlane64(v, 32), readlane64(v, 48)));
+  return pick64<MAX>(pick64<MAX>(readlane64(v, 0), readlane64(v, 16)),
+                     pick64<MAX>(readlane64(v, 32), readlane64(v, 48)));
 }
 
 // Block-wide max (MAX) or min of v; every thread returns it. Synchronizes the block.
@@ -285,8 +286,10 @@ __device__ __forceinline__ uint32_t wave_ext32(uint32_t v) {
   v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor2, 0xF, 0xF, false));
   v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppHalfMirror, 0xF, 0xF, false));
   v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppMirror, 0xF, 0xF, false));
-  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
   return pick(pick(a, b), pick(c, d));
 }
 
@@ -560,7 +563,8 @@ __device__ __forceinline__ void finish_list(TileSmem& s, const TileList& L, void
     }
   }
   if (!to_output)
-    for (int j = n + t; j < k; j += kThreads) __hip_atomic_store(wr + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int j = n + t; j < k; j += kThreads)
+      __hip_atomic_store(wr + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
@@ -1090,19 +1094,18 @@ __device__ __forceinline__ uint32_t wave_kth_multi(const uint32_t (&v)[N], int k
 }
 
 // 64 < k <= 1024: one 256-thread workgroup per (chunk, row), the chunk in register tiles as topk_tile. Per tile: each
-// lane's 64 elements form kWideGroups groups; a group's largest element has the group behind it, so each wave's
-// ceil(k / 4)-th largest group maximum has that many distinct elements at or above it and the smallest of the four
-// waves' has at least k: with the k-th of the earlier tiles it is the admission key (about k * 1.4 admitted per tile
-// on continuous data). The same bound for q = ceil(k / nchunks) gives a q-bound. Admitted elements are appended to an
-// LDS buffer (one LDS atomic per wave and 16 elements per lane); a tile that overflows it (ties, adversarial orders)
-// is appended again vector by vector from the buffer's k-th, pruning to k (histogram narrowing) whenever a vector
-// might not fit. An unsplit row sorts its candidates (bitonic, registers and LDS) and writes the first k. A split
-// row's chunk publishes its candidates (at most kWideList: pruned to k beyond) with its k- and q-bounds to its list in
-// the library's workspace with device-coherent stores, waits for them and counts its arrival; the row's last arrival
-// merges: every chunk has k elements at or above its k-bound and q at or above its q-bound, so the largest k-bound
-// and, when every chunk has one, the smallest q-bound (nchunks * q >= k elements at or above it) bound the row's k-th
-// from below; the lists' candidates at or above that floor (about k * 1.4) are gathered, sorted and the first k
-// written out.
+// lane's 64 elements form kWideGroups groups; a group's largest element has the group behind it, so each wave's ceil(k
+// / 4)-th largest group maximum has that many distinct elements at or above it and the smallest of the four waves' has
+// at least k: with the k-th of the earlier tiles it is the admission key (about k * 1.4 admitted per tile on continuous
+// data). The same bound for q = ceil(k / nchunks) gives a q-bound. Admitted elements are appended to an LDS buffer (one
+// LDS atomic per wave and 16 elements per lane); a tile that overflows it (ties, adversarial orders) is appended again
+// vector by vector from the buffer's k-th, pruning to k (histogram narrowing) whenever a vector might not fit. An
+// unsplit row ranks its candidates (write_ranked) and writes the first k. A split row's chunk publishes its candidates
+// (at most kWideList: pruned to k beyond) with its k- and q-bounds to its list in the library's workspace with
+// device-coherent stores, waits for them and counts its arrival; the row's last arrival merges: every chunk has k
+// elements at or above its k-bound and q at or above its q-bound, so the largest k-bound and, when every chunk has one,
+// the smallest q-bound (nchunks * q >= k elements at or above it) bound the row's k-th from below; the lists'
+// candidates at or above that floor (about k * 1.4) are gathered, ranked and the first k written out.
 template <typename T, bool VEC>
 __global__ void __launch_bounds__(kThreads)
     topk_wide(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
@@ -1343,7 +1346,7 @@ __global__ void __launch_bounds__(kWave)
   if (lane == 0) out[row] = indices[row * k + chosen];
 }
 
-// ---- host side -------------------------------------------------------------------------------------------------------
+// ---- host side ------------------------------------------------------------------------------------------------------
 
 // Tuning slot (0 = automatic): 0 resident workgroups per CU assumed by plan().
 enum { kTuneBlocksPerCu = 0 };
@@ -1396,8 +1399,8 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, long l
 // topk/kernel.cu:520 `plan`: the chunk length (columns per workgroup) for a rows x cols launch. The grid of chunks
 // fills the GPU's resident workgroup slots (CUs x resident workgroups of the k <= 64 kernel per CU) about once; a chunk
 // longer than one register tile (16384 elements) is rounded up to whole tiles; never shorter than min_chunk, which
-// carries the caller's k dependence (longer chunks for larger k: fewer lists of k to merge); a multiple of 8 when a
-// row is split. `threads` and `depth` are the reference's CUDA tuning knobs, accepted and not used.
+// carries the caller's k dependence; a multiple of 8 when a row is split. (launch lengthens the chunks of k > 64 to at
+// least 16k elements.) `threads` and `depth` are the reference's CUDA tuning knobs, accepted and not used.
 extern "C" long long plan(long long rows, long long cols, int dtype, int threads, int depth, int min_chunk) {
   (void)threads;
   (void)depth;
@@ -1430,10 +1433,10 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
 // topk/kernel.cu:549 `launch`: values [rows, k] in x's dtype and int64 indices [rows, k], sorted descending with ties
 // by the lowest index. work: u64 [rows * nchunks * k] with nchunks = ceil(cols / chunk), the chunk lists of split rows
 // for k <= 64 (for k > 64 they go through a workspace of the library's); counters: u32 [>= rows], zero on entry and
-// left zero (the arrivals are counted in the library's counters, kept per device and stream). Checks as the reference's, except that k may be up to 1024
-// (the reference stops at 512): rows <= 0 or k <= 0 is a no-op; -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows
-// > 65535, chunk <= 0, a split row with chunk % 4 or nchunks * k > INT_MAX / 2, threads not 128, 256 or 512, depth
-// not 2, 4 or 8, or a dtype other than 0 and 1.
+// left zero (the arrivals are counted in the library's counters, kept per device and stream). Checks as the
+// reference's, except that k may be up to 1024 (the reference stops at 512): rows <= 0 or k <= 0 is a no-op; -1 for k
+// > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0, a split row with chunk % 4 or nchunks * k > INT_MAX
+// / 2, threads not 128, 256 or 512, depth not 2, 4 or 8, or a dtype other than 0 and 1.
 extern "C" int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
                       long long cols, int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream) {
   if (rows <= 0 || k <= 0) return rw_host::kOk;

@@ -89,7 +89,7 @@ def topk_workloads(quick):
             yield f"s{rows}x{cols}_{dt}", dt, (rows, cols)
 
 
-# ---- per-op cases: inputs, candidate, baseline, seed, check ------------------------------------------------------------
+# ---- per-op cases: inputs, candidate, baseline, seed, check ----------------------------------------------------------
 
 
 class Case:

@@ -88,7 +88,8 @@ def _run_kv(inputs):
     q, k, v, ids, slots = q.contiguous(), k.contiguous(), v.contiguous(), ids.contiguous(), slots.contiguous()
     q_out = q if inplace else torch.empty_like(q)
     batch, seq, q_heads, head_dim = q.shape
-    err = _lib.rope_kv_launch(q.data_ptr(), k.data_ptr(), v.data_ptr(), ids.data_ptr(), inv_freq.contiguous().data_ptr(),
+    inv_freq = inv_freq.contiguous()
+    err = _lib.rope_kv_launch(q.data_ptr(), k.data_ptr(), v.data_ptr(), ids.data_ptr(), inv_freq.data_ptr(),
                               q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), slots.data_ptr(), batch * seq, q_heads,
                               k.shape[2], head_dim, _QK[q.dtype], torch.cuda.current_stream(q.device).cuda_stream)
     if err:

@@ -5,7 +5,8 @@ the lowest index (the reference's topk/candidate.py:1-10 with K = 50). k is inpu
 reference fixes 50). The one `launch` entry of libkernel.so serves both dtypes: fp32 (0) and bf16 (1), row-major x;
 values keep x's dtype and indices are int64. `plan` picks the columns per workgroup so the grid is one resident wave;
 rows split into several chunks merge in the kernel (the library keeps its hand-off workspaces; the reference's int64
-workspace and per-row int32 counters are still allocated and passed, zeroed once). The plan and workspace of the last shape are cached, so a repeated call allocates only its outputs.
+workspace and per-row int32 counters are still allocated and passed, zeroed once). The plan and workspace of the last
+shape are cached, so a repeated call allocates only its outputs.
 params.json (optional) may set "log2_threads" (7..9), "log2_depth" (1..3) -- the reference's knobs, validated and not
 needed by this build -- and "min_chunk". The library is $CKOPT_BUILD_DIR/libkernel.so when CKOPT_BUILD_DIR is set,
 else this package's build/topk/libkernel.so.

@@ -25,9 +25,9 @@ int launch(const void* q, const void* k, const void* cos_rows, const void* sin_r
 int rope_launch_freq(const void* q, const void* k, const void* ids, const float* inv_freq, void* q_out, void* k_out,
                      long long tokens, int q_heads, int kv_heads, int head_dim, int qk_dtype, hipStream_t stream);
 
-/* No counterpart in the reference (the step after RoPE in a decoder layer): RoPE fused with the
- * KV-cache write. q_out = rope(q) with cos/sin on the fly as rope_launch_freq (q_out may equal q); the rotated k and the
- * unrotated v of token t go to row slot_mapping[t] (int64) of k_cache and v_cache, each [slots, kv_heads, head_dim] in
+/* No counterpart in the reference (the step after RoPE in a decoder layer): RoPE fused with the KV-cache write.
+ * q_out = rope(q) with cos/sin on the fly as rope_launch_freq (q_out may equal q); the rotated k and the unrotated v
+ * of token t go to row slot_mapping[t] (int64) of k_cache and v_cache, each [slots, kv_heads, head_dim] in
  * the qk dtype -- a paged [blocks, block_size, kv_heads, head_dim] cache with slot = block * block_size + offset; a
  * negative slot writes nothing for its token. k and v are only read. Same checks and codes as rope_launch_freq; a null
  * v, cache or slot_mapping is -1. */

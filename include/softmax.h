@@ -3,8 +3,8 @@
  * softmax/seed.cu:68-81). x and y are device pointers to row-major contiguous [rows, cols] data; the call is
  * asynchronous on `stream` and allocates nothing except, for rows longer than 32768 fp32 / 65536 bf16 elements, small
  * per-(device, stream) workspaces the library keeps (chunk pairs; for the single-pass tier also per-row counters, which
- * every launch leaves at zero). Launches sharing a stream must not overlap (they do not: one stream is ordered). Return: 0 success (rows <= 0 or cols <= 0 is a no-op),
- * -1 unsupported dtype, otherwise the hipError_t of the launch. */
+ * every launch leaves at zero). Launches sharing a stream are ordered by it. Return: 0 success (rows <= 0 or cols <= 0
+ * is a no-op), -1 unsupported dtype, otherwise the hipError_t of the launch. */
 #ifndef ROWKERN_SOFTMAX_H
 #define ROWKERN_SOFTMAX_H
 #include <hip/hip_runtime_api.h>

@@ -17,7 +17,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-/* ---- formats ------------------------------------------------------------------------------------------------------- */
+/* ---- formats --- */
 
 static float f_from_bits(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static uint32_t bits_from_f(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
@@ -150,13 +150,14 @@ void oracle_rmsnorm_add(const uint16_t* x, const uint16_t* res, const uint16_t* 
   oracle_rmsnorm(h_out, w, y, rows, cols, dtype, eps, 0);
 }
 
-/* ---- RoPE (rope/kernel.cu:1-11, :73-79, :119-126; rope/candidate.py:3-5) ---------------------------------------------
+/* ---- RoPE (rope/kernel.cu:1-11, :73-79, :119-126; rope/candidate.py:3-5) --------------------------------------------
  * For each token, head and i < h = D/2, with a = x[i], b = x[i + h] of the head:
  *   out[i]     = T(fp32(fp32(a * c1) - fp32(b * s1)))
  *   out[i + h] = T(fp32(fp32(b * c2) + fp32(a * s2)))
  * cache form: c1 = cos[p][i], s1 = sin[p][i], c2 = cos[p][i + h], s2 = sin[p][i + h] with p = ids[token];
- * frequency form: c1 = c2 = fp32(cos(t)), s1 = s2 = fp32(sin(t)) with t = fp32(float(pos) * inv_freq[i]) and cos, sin in
- * fp64 (the correctly rounded fp32 values). q is [tokens, q_heads, D], k is [tokens, kv_heads, D]; outputs may alias. */
+ * frequency form: c1 = c2 = fp32(cos(t)), s1 = s2 = fp32(sin(t)) with t = fp32(float(pos) * inv_freq[i]) and cos,
+ * sin in fp64 (the correctly rounded fp32 values). q is [tokens, q_heads, D], k is [tokens, kv_heads, D]; outputs
+ * may alias. */
 static void rope_head(const void* x, void* out, long long o, int half, int fmt, const float* c1, const float* s1,
                       const float* c2, const float* s2) {
   for (int i = 0; i < half; ++i) {
@@ -230,7 +231,7 @@ void oracle_rope_table(const float* inv_freq, long long positions, int head_dim,
   }
 }
 
-/* ---- top-k (topk/kernel.cu:1-15, :56-81) ------------------------------------------------------------------------------
+/* ---- top-k (topk/kernel.cu:1-15, :56-81) ----------------------------------------------------------------------------
  * Each element is ranked by its composite (key << 32) | ~index with key = ~u for a set sign bit, else u | 0x80000000 (u
  * the fp32 bits; a bf16 element is widened to fp32 first): values descending, ties by the lowest index, +0 above -0,
  * +NaN above +inf and -NaN below -inf. The k largest composites, in descending order, give the values (the element

@@ -26,5 +26,6 @@ def test_quick_report_passes():
     assert {r["op"] for r in rows} == {"softmax", "rmsnorm", "rope", "topk"}
     assert all(r["correctness"] == "PASS" for r in rows), [r for r in rows if r["correctness"] != "PASS"]
     text = h.table(rows)
-    assert "| workload | correctness | timing | candidate ms | baseline ms | seed ms | vs baseline | vs seed | dtype |" \
-        in text
+    header = ("| workload | correctness | timing | candidate ms | baseline ms | seed ms | vs baseline | vs seed "
+              "| dtype |")
+    assert header in text

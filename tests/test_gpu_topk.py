@@ -4,8 +4,8 @@ values (the element bits) and int64 indices, sorted descending with ties by the 
 Covers single- and multi-chunk rows (the merge by the row's last workgroup to arrive, counted in the library's
 arrival counters), every k class (1, the lane-maxima bound up to 64, the general path up to 1024), ties and special
 values, negative rows and the all-ones NaN (the value the k <= 64 kernel pads tiles with), bf16, unaligned and ragged
-rows, workspace reuse, the arrival counters' growth, reset and self-reset, adversarial orders that force many prunes,
-and the top-k workload at k = 1, 50 and 1024.
+rows, short last tiles, workspace reuse, the arrival counters' growth, reset and self-reset, adversarial orders that
+force many prunes, and the top-k workload at k = 1, 50 and 1024.
 """
 
 import numpy as np
@@ -143,12 +143,27 @@ def test_handoff_workspace_across_shapes(pkg, oracle, dev):
     # back-to-back split launches on one stream, growing (a reallocation of the arrival counters) and shrinking:
     # every launch must leave the counters all zeros for the next; topk_reset clears them as well
     g = torch.Generator().manual_seed(7)
-    for rows, cols, k, chunk in [(2, 9000, 7, 2048), (512, 32000, 64, 1024), (3, 20000, 64, 1024), (64, 40000, 50, 4096),
-                                 (2, 9000, 7, 2048)]:
+    shapes = [(2, 9000, 7, 2048), (512, 32000, 64, 1024), (3, 20000, 64, 1024), (64, 40000, 50, 4096),
+              (2, 9000, 7, 2048)]
+    for rows, cols, k, chunk in shapes:
         check(pkg, oracle, torch.randn(rows, cols, generator=g), k, dev, chunk=chunk, what="hand-off reuse")
     counters = torch.zeros(8, dtype=torch.int32, device=dev)
     assert lib(pkg).topk_reset(counters.data_ptr(), 8, torch.cuda.current_stream().cuda_stream) == 0
     check(pkg, oracle, torch.randn(5, 30000, generator=g), 50, dev, chunk=4096, what="after reset")
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("k", [1, 13, 50, 64, 100, 1024])
+def test_short_last_tiles(pkg, oracle, dev, dt, k):
+    # chunks whose last register tile leaves whole waves without data (the bound is split over the waves holding data)
+    # or holds fewer lanes or groups than k (no bound: the tile is pushed exactly over its vectors holding data); the
+    # k > 64 kernel picks its own chunk, so its tails come from the column counts
+    g = torch.Generator().manual_seed(900 + k)
+    for cols, chunk in [(62 * 2048 + 1280, 2048), (3 * 2048 + 40, 2048), (2 * 17664, 17664), (2 * 16384 + 1280, 16384),
+                        (16384 + 136, None), (1000, None)]:
+        if k <= cols:
+            x = (torch.randn(3, cols, generator=g) * 2).to(dt)
+            check(pkg, oracle, x, k, dev, chunk=chunk, what="short last tile")
 
 
 def test_bf16_and_unaligned(pkg, oracle, dev):

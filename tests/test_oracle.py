@@ -337,7 +337,7 @@ def test_topk_golden(oracle):
         assert np.array_equal(v, f[f"v{k}"]) and np.array_equal(i, f[f"i{k}"])
 
 
-# ---- the checks catch planted mistakes --------------------------------------------------------------------------------
+# ---- the checks catch planted mistakes -------------------------------------------------------------------------------
 
 
 def test_planted_mistakes_are_caught(oracle):
