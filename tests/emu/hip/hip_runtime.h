@@ -1,0 +1,396 @@
+// A CPU emulation of the HIP surface that csrc/topk.hip uses, for running the kernels' own source on the host (test
+// infrastructure, never linked into the libraries):
+//  - every thread of a workgroup is a cooperative fiber (makecontext for its entry, _setjmp/_longjmp to switch);
+//  - every cross-lane operation (ballot, DPP, readlane, readfirstlane, shfl_up) is an exchange between two barriers of
+//    the wave's live lanes, and __syncthreads a barrier of the block's live threads; lanes that have returned take no
+//    part, as on the hardware. Lanes of one wave reaching a barrier from different source lines, or a schedule in
+//    which no fiber can run, abort with a report;
+//  - workgroups run one after another (shuffled on request), so __shared__ is a function-local static;
+//  - device buffers lie between PROT_NONE pages (flush against the upper one, or against the lower one with
+//    EMU_ALIGN_START set) and start filled with 0xA5, so an access outside a buffer faults at once;
+//  - the atomics are plain operations: fibers switch only at barriers.
+#pragma once
+#include <setjmp.h>
+#include <sys/mman.h>
+#include <ucontext.h>
+#include <unistd.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <random>
+#include <vector>
+
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+#define __shared__ static
+#define EMU_ASM(...) ((void)0)
+
+typedef int hipError_t;
+enum { hipSuccess = 0, hipErrorInvalidValue = 1 };
+typedef struct ihipStream_t* hipStream_t;
+enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 1 };
+
+struct dim3 {
+  unsigned x, y, z;
+  dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
+};
+
+namespace emu {
+constexpr int kW = 64;
+constexpr int kMaxThreads = 1024;
+constexpr size_t kStack = 256 * 1024;
+
+struct Idx { unsigned x, y, z; };
+
+struct Bar {
+  int arrived = 0;
+  unsigned gen = 0;
+  int line = -1;
+};
+
+struct Fiber {
+  jmp_buf jb;
+  ucontext_t uc;
+  char* stack = nullptr;
+  Idx tid;
+  bool done = false, started = false;
+  Bar* wait = nullptr;
+  unsigned wait_gen = 0;
+};
+
+struct State {
+  Fiber fib[kMaxThreads];
+  int n = 0;
+  Fiber* cur = nullptr;
+  jmp_buf sched;
+  ucontext_t sched_uc;
+  Idx block_idx{0, 0, 0};
+  dim3 grid, block;
+  Bar wbar[kMaxThreads / kW], bbar;
+  int wactive[kMaxThreads / kW], bactive = 0;
+  uint64_t slots[kMaxThreads / kW][kW];
+  std::function<void()> body;
+  unsigned long long switches = 0, inactive_reads = 0;
+  int shuffle_seed = -1;
+  std::mt19937 rng{1};
+};
+inline State& S() {
+  static State* s = new State;
+  return *s;
+}
+
+inline const Idx& tid() { return S().cur->tid; }
+inline int flat() { return (int)S().cur->tid.x; }
+inline int wid() { return flat() / kW; }
+inline int lid() { return flat() % kW; }
+
+[[noreturn]] inline void fail(const char* what, int line) {
+  std::fprintf(stderr, "EMU FAIL: %s (line %d) block (%u,%u) thread %d\n", what, line, S().block_idx.x,
+               S().block_idx.y, S().cur ? flat() : -1);
+  std::fflush(stderr);
+  std::abort();
+}
+
+inline void yield() {
+  State& s = S();
+  ++s.switches;
+  if (!_setjmp(s.cur->jb)) _longjmp(s.sched, 1);
+}
+
+inline void arrive(Bar& b, int active, int line) {
+  if (b.arrived == 0) b.line = line;
+  else if (b.line != line) {
+    std::fprintf(stderr, "EMU: barrier mismatch: line %d vs line %d\n", b.line, line);
+    fail("lanes of one barrier at different sites", line);
+  }
+  if (++b.arrived == active) {
+    b.arrived = 0;
+    ++b.gen;
+    return;
+  }
+  S().cur->wait = &b;
+  S().cur->wait_gen = b.gen;
+  yield();
+}
+inline void wave_sync(int line) { arrive(S().wbar[wid()], S().wactive[wid()], line); }
+inline void block_sync(int line) { arrive(S().bbar, S().bactive, line); }
+
+inline bool lane_done(int w, int l) { return S().fib[w * kW + l].done; }
+
+inline uint64_t ballot(bool p, int line) {
+  State& s = S();
+  const int w = wid();
+  s.slots[w][lid()] = p;
+  wave_sync(line);
+  uint64_t m = 0;
+  for (int i = 0; i < kW; ++i)
+    if (w * kW + i < s.n && !lane_done(w, i) && s.slots[w][i]) m |= 1ull << i;
+  wave_sync(line);
+  return m;
+}
+inline uint64_t read_from(uint64_t mine, int src, int line) {
+  State& s = S();
+  const int w = wid();
+  s.slots[w][lid()] = mine;
+  wave_sync(line);
+  uint64_t r = 0;
+  if (src < 0 || src >= kW || lane_done(w, src)) ++s.inactive_reads;
+  else r = s.slots[w][src];
+  wave_sync(line);
+  return r;
+}
+inline int first_active(int w) {
+  for (int i = 0; i < kW; ++i)
+    if (!lane_done(w, i)) return i;
+  return 0;
+}
+inline int readlane(int v, int lane, int line) { return (int)(uint32_t)read_from((uint32_t)v, lane, line); }
+inline int readfirstlane(int v, int line) {
+  // the first lane that is not done (every live lane takes part)
+  State& s = S();
+  const int w = wid();
+  s.slots[w][lid()] = (uint32_t)v;
+  wave_sync(line);
+  const int r = (int)(uint32_t)s.slots[w][first_active(w)];
+  wave_sync(line);
+  return r;
+}
+inline int dpp_src(int l, int ctrl, int line) {
+  switch (ctrl) {
+    case 0xB1: return l ^ 1;
+    case 0x4E: return l ^ 2;
+    case 0x141: return (l & ~7) | (7 - (l & 7));
+    case 0x140: return (l & ~15) | (15 - (l & 15));
+    default: fail("unsupported dpp control", line);
+  }
+}
+inline int update_dpp(int old, int src, int ctrl, int rm, int bm, bool bc, int line) {
+  (void)old;
+  (void)bc;
+  if (rm != 0xF || bm != 0xF) fail("dpp masks", line);
+  return (int)(uint32_t)read_from((uint32_t)src, dpp_src(lid(), ctrl, line), line);
+}
+inline unsigned mbcnt_lo(unsigned m, unsigned c) {
+  const int l = lid();
+  const uint64_t below = l >= 32 ? 0xffffffffull : ((1ull << l) - 1);
+  return c + (unsigned)__builtin_popcountll((uint64_t)m & below);
+}
+inline unsigned mbcnt_hi(unsigned m, unsigned c) {
+  const int l = lid() - 32;
+  const uint64_t below = l <= 0 ? 0ull : ((1ull << l) - 1);
+  return c + (unsigned)__builtin_popcountll((uint64_t)m & below);
+}
+template <typename T>
+inline T shfl_up(T v, unsigned d, int width, int line) {
+  static_assert(sizeof(T) <= 8, "");
+  uint64_t u = 0;
+  std::memcpy(&u, &v, sizeof(T));
+  const int l = lid();
+  const int src = (l % width) >= (int)d ? l - (int)d : l;
+  u = read_from(u, src, line);
+  T r;
+  std::memcpy(&r, &u, sizeof(T));
+  return r;
+}
+
+inline void trampoline() {
+  State& s = S();
+  s.body();
+  Fiber* f = s.cur;
+  f->done = true;
+  const int w = (int)f->tid.x / kW;
+  --s.wactive[w];
+  --s.bactive;
+  // a lane that ends releases barriers its peers wait at (ended lanes take no part, as on the hardware)
+  Bar& wb = s.wbar[w];
+  if (wb.arrived > 0 && wb.arrived == s.wactive[w]) {
+    wb.arrived = 0;
+    ++wb.gen;
+  }
+  if (s.bbar.arrived > 0 && s.bbar.arrived == s.bactive) {
+    s.bbar.arrived = 0;
+    ++s.bbar.gen;
+  }
+  _longjmp(s.sched, 1);
+}
+
+inline void run_block() {
+  State& s = S();
+  for (int i = 0; i < s.n; ++i) {
+    Fiber& f = s.fib[i];
+    if (!f.stack) {
+      char* base = (char*)mmap(nullptr, kStack + 4096, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS, -1, 0);
+      if (base == MAP_FAILED) fail("stack mmap", 0);
+      mprotect(base, 4096, PROT_NONE);
+      f.stack = base + 4096;
+    }
+    f.done = false;
+    f.started = false;
+    f.wait = nullptr;
+    f.tid = Idx{(unsigned)i, 0, 0};
+    getcontext(&f.uc);
+    f.uc.uc_stack.ss_sp = f.stack;
+    f.uc.uc_stack.ss_size = kStack;
+    f.uc.uc_link = nullptr;
+    makecontext(&f.uc, (void (*)())trampoline, 0);
+  }
+  for (int w = 0; w < (s.n + kW - 1) / kW; ++w) {
+    s.wactive[w] = (s.n - w * kW) < kW ? s.n - w * kW : kW;
+    s.wbar[w] = Bar{};
+  }
+  s.bactive = s.n;
+  s.bbar = Bar{};
+  std::vector<int> order(s.n);
+  for (int i = 0; i < s.n; ++i) order[i] = i;
+  int remaining = s.n;
+  while (remaining) {
+    bool progress = false;
+    if (s.shuffle_seed >= 0) std::shuffle(order.begin(), order.end(), s.rng);
+    for (int oi = 0; oi < s.n; ++oi) {
+      Fiber& f = s.fib[order[oi]];
+      if (f.done) continue;
+      if (f.wait && f.wait->gen == f.wait_gen) continue;
+      f.wait = nullptr;
+      s.cur = &f;
+      if (!_setjmp(s.sched)) {
+        if (!f.started) {
+          f.started = true;
+          swapcontext(&s.sched_uc, &f.uc);
+        } else {
+          _longjmp(f.jb, 1);
+        }
+      }
+      progress = true;
+      if (f.done) --remaining;
+    }
+    if (!progress) {
+      std::fprintf(stderr, "EMU DEADLOCK in block (%u,%u): %d lanes left\n", s.block_idx.x, s.block_idx.y, remaining);
+      for (int w = 0; w < (s.n + kW - 1) / kW; ++w)
+        std::fprintf(stderr, "  wave %d: active %d, wave barrier arrived %d at line %d\n", w, s.wactive[w],
+                     s.wbar[w].arrived, s.wbar[w].line);
+      std::fprintf(stderr, "  block barrier arrived %d of %d at line %d\n", s.bbar.arrived, s.bactive, s.bbar.line);
+      std::abort();
+    }
+  }
+  s.cur = nullptr;
+}
+
+inline void launch(dim3 grid, dim3 block, std::function<void()> body) {
+  State& s = S();
+  if (block.y != 1 || block.z != 1 || block.x > (unsigned)kMaxThreads) fail("block shape", 0);
+  s.grid = grid;
+  s.block = block;
+  s.n = (int)block.x;
+  s.body = std::move(body);
+  std::vector<Idx> blocks;
+  for (unsigned z = 0; z < grid.z; ++z)
+    for (unsigned y = 0; y < grid.y; ++y)
+      for (unsigned x = 0; x < grid.x; ++x) blocks.push_back(Idx{x, y, z});
+  if (s.shuffle_seed >= 0) std::shuffle(blocks.begin(), blocks.end(), s.rng);
+  for (const Idx& b : blocks) {
+    s.block_idx = b;
+    run_block();
+  }
+}
+
+// Device buffers end at a PROT_NONE page (an access past the end faults at once) and start after one; contents start
+// as a fill pattern, not zeros (device memory is not cleared by an allocation).
+struct Mapping {
+  char* base;
+  size_t len;
+};
+inline std::map<void*, Mapping>& maps() {
+  static std::map<void*, Mapping> m;
+  return m;
+}
+inline void* guarded_alloc(size_t n) {
+  const size_t pg = 4096;
+  const size_t body = (n + pg - 1) / pg * pg + pg;
+  char* base = (char*)mmap(nullptr, body + 2 * pg, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS, -1, 0);
+  if (base == MAP_FAILED) return nullptr;
+  mprotect(base, pg, PROT_NONE);
+  mprotect(base + pg + body, pg, PROT_NONE);
+  char* p = std::getenv("EMU_ALIGN_START") ? base + pg : base + pg + body - ((n + 15) & ~(size_t)15);
+  std::memset(base + pg, 0xA5, body);
+  maps()[p] = Mapping{base, body + 2 * pg};
+  return p;
+}
+inline void guarded_free(void* p) {
+  auto it = maps().find(p);
+  if (it == maps().end()) {
+    std::fprintf(stderr, "EMU: free of an unknown pointer %p\n", p);
+    std::abort();
+  }
+  munmap(it->second.base, it->second.len);
+  maps().erase(it);
+}
+}  // namespace emu
+
+#define threadIdx (emu::tid())
+#define blockIdx (emu::S().block_idx)
+#define __syncthreads() emu::block_sync(__LINE__)
+#define __ballot(p) emu::ballot((p), __LINE__)
+#define __builtin_amdgcn_readlane(v, l) emu::readlane((int)(v), (int)(l), __LINE__)
+#define __builtin_amdgcn_readfirstlane(v) emu::readfirstlane((int)(v), __LINE__)
+#define __builtin_amdgcn_update_dpp(o, s, c, r, b, bc) emu::update_dpp((int)(o), (int)(s), (c), (r), (b), (bc), __LINE__)
+#define __builtin_amdgcn_mbcnt_lo(m, c) emu::mbcnt_lo((unsigned)(m), (unsigned)(c))
+#define __builtin_amdgcn_mbcnt_hi(m, c) emu::mbcnt_hi((unsigned)(m), (unsigned)(c))
+#define __builtin_amdgcn_wave_barrier() emu::wave_sync(__LINE__)
+#define __shfl_up(v, d, w) emu::shfl_up((v), (unsigned)(d), (int)(w), __LINE__)
+
+#define __HIP_MEMORY_SCOPE_AGENT 0
+#define __hip_atomic_load(p, o, sc) (*(p))
+#define __hip_atomic_store(p, v, o, sc) (void)(*(p) = (v))
+template <typename T, typename U>
+inline T emu_fetch_add(T* p, U v) {
+  T old = *p;
+  *p = old + (T)v;
+  return old;
+}
+#define __hip_atomic_fetch_add(p, v, o, sc) emu_fetch_add((p), (v))
+template <typename T, typename U>
+inline T atomicAdd(T* p, U v) {
+  return emu_fetch_add(p, v);
+}
+
+inline int __popcll(unsigned long long v) { return __builtin_popcountll(v); }
+inline int __clzll(long long v) { return v ? __builtin_clzll((unsigned long long)v) : 64; }
+inline int __clz(int v) { return v ? __builtin_clz((unsigned)v) : 32; }
+inline float __uint_as_float(unsigned u) { return __builtin_bit_cast(float, u); }
+inline unsigned __float_as_uint(float f) { return __builtin_bit_cast(unsigned, f); }
+
+inline hipError_t hipGetDevice(int* d) {
+  *d = 0;
+  return hipSuccess;
+}
+inline hipError_t hipGetLastError() { return hipSuccess; }
+inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
+  *v = 256;
+  return hipSuccess;
+}
+template <typename F>
+inline hipError_t hipOccupancyMaxActiveBlocksPerMultiprocessor(int* n, F, int, size_t) {
+  *n = 4;
+  return hipSuccess;
+}
+inline hipError_t hipMalloc(void** p, size_t n) {
+  *p = emu::guarded_alloc(n);
+  return *p ? hipSuccess : hipErrorInvalidValue;
+}
+inline hipError_t hipFree(void* p) {
+  if (p) emu::guarded_free(p);
+  return hipSuccess;
+}
+inline hipError_t hipMemsetAsync(void* p, int v, size_t n, hipStream_t) {
+  std::memset(p, v, n);
+  return hipSuccess;
+}
+#define hipLaunchKernelGGL(K, G, B, SH, ST, ...) emu::launch(dim3(G), dim3(B), [&]() { K(__VA_ARGS__); })

@@ -1,0 +1,90 @@
+"""The top-k kernels' own source (csrc/topk.hip) run on the CPU under an emulation of the HIP surface it uses
+(tests/emu/hip/hip_runtime.h), every launch checked bit for bit against the oracle.
+
+Each workgroup thread is a cooperative fiber and each cross-lane operation an exchange between barriers of the wave's
+live lanes. Every buffer the kernels touch (input, outputs, work, counters and the library's own hand-off
+workspaces) lies between guard pages, so an out-of-bounds access ends the run with a fault. The cases cover
+single- and split-chunk rows, every k class (1, the lane-maxima bound up to 64, the wide path up to 1024), short last
+tiles, ties, monotone and all-negative rows, the all-ones NaN, repeated launches on the same buffers (the arrival
+counters' self-reset), and shuffled workgroup and lane schedules. What the emulation does not model is the
+hardware's memory ordering between workgroups (they run one after another) and the compiler's gfx950 code.
+"""
+
+import os
+import shutil
+import subprocess
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(ROOT, "cuda-kernels-optimized-for-rtx5090_amd", "csrc")
+EMU = os.path.join(HERE, "emu")
+
+
+def _clang():
+    for cand in ("/opt/rocm/llvm/bin/clang++", shutil.which("clang++")):
+        if cand and os.path.exists(cand):
+            return cand
+    return None
+
+
+@pytest.fixture(scope="module")
+def emu_topk(tmp_path_factory):
+    clang = _clang()
+    if clang is None or shutil.which("gcc") is None:
+        pytest.skip("clang++ (for the kernels' vector extensions on the host) or gcc is missing")
+    d = tmp_path_factory.mktemp("emu_topk")
+    # the source as the libraries build it, with its inline asm statements (scheduling fences and waits for the
+    # memory counters, which have no meaning here) turned into no-ops
+    with open(os.path.join(CSRC, "topk.hip")) as f:
+        src = f.read().replace("asm volatile(", "EMU_ASM(")
+    (d / "topk_emu.cpp").write_text(src)
+    subprocess.run(["gcc", "-O2", "-c", os.path.join(ROOT, "oracle", "oracle.c"), "-o", str(d / "oracle.o")],
+                   check=True)
+    exe = d / "emu_topk"
+    proc = subprocess.run([clang, "-std=c++17", "-O1", "-U_FORTIFY_SOURCE", "-D_FORTIFY_SOURCE=0",
+                           "-fno-strict-aliasing", "-w", "-I", EMU, "-I", CSRC, str(d / "topk_emu.cpp"),
+                           os.path.join(EMU, "emu_topk.cpp"), str(d / "oracle.o"), "-o", str(exe), "-lm"],
+                          capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stderr[-4000:]
+    return str(exe)
+
+
+ALL_K = "1,7,50,64,65,300,1024"
+# rows, cols, dtype (0 fp32, 1 bf16), ks, chunk (0: plan's), min_chunk, reps, seed, shuffle seed, pattern
+CASES = [
+    ("split_fp32", 2, 20000, 0, ALL_K, 4096, 2048, 2, 1, -1, "randn"),
+    ("split_bf16", 2, 20000, 1, ALL_K, 4096, 2048, 2, 2, -1, "randn"),
+    ("one_chunk", 3, 20000, 0, ALL_K, 20000, 2048, 1, 3, -1, "randn"),
+    ("planned", 4, 30000, 1, "1,50,1024", 0, 2048, 2, 4, -1, "randn"),
+    ("short_tail_bf16", 2, 62 * 2048 + 1280, 1, "1,13,50,64,100,1024", 2048, 2048, 1, 5, -1, "randn"),
+    ("short_tail_fp32", 2, 3 * 2048 + 40, 0, "1,13,50,64,100,1024", 2048, 2048, 1, 6, -1, "randn"),
+    ("tile_plus_tail", 2, 2 * 16384 + 1280, 1, "1,50,100,1024", 16384, 2048, 1, 7, -1, "randn"),
+    ("ties", 3, 30000, 0, "1,50,1024", 4096, 2048, 1, 8, -1, "ints"),
+    ("ascending", 2, 40000, 0, "1,50,1024", 8192, 2048, 1, 9, -1, "ascending"),
+    ("descending", 2, 40000, 1, "1,50,1024", 8192, 2048, 1, 10, -1, "descending"),
+    ("negative", 2, 40000, 0, "1,50,300", 8192, 2048, 1, 11, -1, "negative"),
+    ("all_ones_nan", 3, 20000, 0, "1,13,50,300", 4096, 2048, 1, 12, -1, "allones"),
+    ("all_ones_nan_bf16", 3, 20000, 1, "1,13,50,300", 4096, 2048, 1, 13, -1, "allones"),
+    ("k_equals_cols", 2, 1024, 0, "1024", 0, 2048, 1, 14, -1, "randn"),
+    ("shuffled", 2, 20000, 0, ALL_K, 4096, 2048, 2, 15, 99, "randn"),
+    ("shuffled_bf16", 2, 20000, 1, "1,50,1024", 2052, 2048, 2, 16, 7, "ints"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_emulated_topk_matches_oracle(emu_topk, case):
+    args = [str(a) for a in case[1:]]
+    proc = subprocess.run([emu_topk, *args], capture_output=True, text=True, timeout=600)
+    out = proc.stdout + proc.stderr
+    assert proc.returncode == 0 and "ALL OK" in proc.stdout, f"{case[0]}: rc {proc.returncode}\n{out[-3000:]}"
+
+
+def test_emulated_topk_guard_below_start(emu_topk):
+    # the same buffers placed flush against their lower guard page
+    env = dict(os.environ, EMU_ALIGN_START="1")
+    for case in (CASES[0], CASES[4], CASES[6]):
+        proc = subprocess.run([emu_topk, *[str(a) for a in case[1:]]], capture_output=True, text=True, timeout=600,
+                              env=env)
+        assert proc.returncode == 0 and "ALL OK" in proc.stdout, f"{case[0]}: {proc.stdout[-2000:]}{proc.stderr}"
