@@ -263,6 +263,8 @@ typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
 // A row's arrival counter sits alone in its 256 bytes: the device-scope atomics of the rows' last workgroups, which
 // come close together, are not serialized on a shared line (the caller's counters are 4 bytes apart).
 constexpr int kArrivalStride = 64;
+// k = 1: the row's best composite so far (u64, zero between launches) sits 8 bytes into the counter's 256 bytes
+constexpr int kBestOffset = 2;
 
 struct TileSmem {
   u64 seg[kWaves][kTileSeg];
@@ -944,6 +946,35 @@ __global__ void __launch_bounds__(kThreads)
   }
   if (nchunks == 1) {
     finish_list<T>(s, L, values, indices, nullptr, row, k, true);
+    return;
+  }
+  if (k == 1) {
+    // the chunk's largest composite goes into the row's slot beside its arrival counter by a device-scope maximum
+    // (completed before the arrival is counted); the row's last arrival writes the slot out and zeroes slot and
+    // counter for the next launch
+    u64 best = 0;
+    const int n = L.cnt < kTileSeg ? L.cnt : kTileSeg;
+    for (int i = lane_id(); i < n; i += kWave) best = L.seg[i] > best ? L.seg[i] : best;
+    best = wave_ext64<true>(best);
+    if (lane_id() == 0) s.sorted[wave_id()] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) best = s.sorted[w] > best ? s.sorted[w] : best;
+      unsigned* counter = arrivals + row * kArrivalStride;
+      u64* slot = reinterpret_cast<u64*>(counter + kBestOffset);
+      __hip_atomic_fetch_max(slot, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      const unsigned old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == (unsigned)nchunks - 1) {
+        const u64 c = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row] = composite_bits(c);
+        else static_cast<uint16_t*>(values)[row] = (uint16_t)(composite_bits(c) >> 16);
+        indices[row] = composite_index(c);
+        __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
     return;
   }
   u64* wr = work + row * (long long)nchunks * k;

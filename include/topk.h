@@ -3,7 +3,8 @@
  * reference), 1 <= k <= 1024. Library: build/topk/libkernel.so. Replaces the reference's topk/kernel.cu:520-570 (ctypes
  * binding topk/candidate.py:31-36). Device pointers; asynchronous on `stream`. The caller owns the workspace and
  * counters; a split row's chunks count their arrivals in counters of the library's own instead (one per 256 bytes,
- * so that the rows' counting atomics do not share a line, all zeros between launches), and for k > 64 hand their
+ * so that the rows' counting atomics do not share a line, all zeros between launches; for k = 1 the row's best
+ * composite so far sits beside its counter, so no list is handed over), and for k > 64 hand their
  * candidate lists over in a workspace of the library's (up to 2052 u64 per chunk); both are allocated on first use
  * per (device, stream) and grown when a launch needs more. */
 #ifndef ROWKERN_TOPK_H

@@ -340,7 +340,8 @@ inline void guarded_free(void* p) {
 #define __ballot(p) emu::ballot((p), __LINE__)
 #define __builtin_amdgcn_readlane(v, l) emu::readlane((int)(v), (int)(l), __LINE__)
 #define __builtin_amdgcn_readfirstlane(v) emu::readfirstlane((int)(v), __LINE__)
-#define __builtin_amdgcn_update_dpp(o, s, c, r, b, bc) emu::update_dpp((int)(o), (int)(s), (c), (r), (b), (bc), __LINE__)
+#define __builtin_amdgcn_update_dpp(o, s, c, r, b, bc) \
+  emu::update_dpp((int)(o), (int)(s), (c), (r), (b), (bc), __LINE__)
 #define __builtin_amdgcn_mbcnt_lo(m, c) emu::mbcnt_lo((unsigned)(m), (unsigned)(c))
 #define __builtin_amdgcn_mbcnt_hi(m, c) emu::mbcnt_hi((unsigned)(m), (unsigned)(c))
 #define __builtin_amdgcn_wave_barrier() emu::wave_sync(__LINE__)
@@ -356,6 +357,13 @@ inline T emu_fetch_add(T* p, U v) {
   return old;
 }
 #define __hip_atomic_fetch_add(p, v, o, sc) emu_fetch_add((p), (v))
+template <typename T, typename U>
+inline T emu_fetch_max(T* p, U v) {
+  T old = *p;
+  if ((T)v > old) *p = (T)v;
+  return old;
+}
+#define __hip_atomic_fetch_max(p, v, o, sc) emu_fetch_max((p), (v))
 template <typename T, typename U>
 inline T atomicAdd(T* p, U v) {
   return emu_fetch_add(p, v);
