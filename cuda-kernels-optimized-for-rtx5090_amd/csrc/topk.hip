@@ -1097,9 +1097,12 @@ __device__ void write_ranked(S& s, int m, int k, void* values, long long* indice
 
 // A lower bound of the k-th largest of the wave's values v[i] (N per lane; 0 marks no value and is never counted) with
 // at least k values at or above it; 0 when the wave holds fewer than k values. The bitwise search of wave_kth32 over N
-// values per lane.
+// values per lane, over [max(lo, smallest value), largest value]: `lo` (wave-uniform) must not exceed the k-th largest,
+// and a higher one resolves the same number of bits more finely. The range is first tried from two binades below the
+// largest value (one more ballot per value), kept when k values lie at or above that end: the smallest value is often
+// far below the k-th (group maxima of both signs), and 12 bits over the whole range resolve the bound to a quarter.
 template <int N>
-__device__ __forceinline__ uint32_t wave_kth_multi(const uint32_t (&v)[N], int k) {
+__device__ __forceinline__ uint32_t wave_kth_multi(const uint32_t (&v)[N], int k, uint32_t lo) {
   uint32_t mx = 0, mn = 0xffffffffu;
   int real = 0;
 #pragma unroll
@@ -1111,7 +1114,16 @@ __device__ __forceinline__ uint32_t wave_kth_multi(const uint32_t (&v)[N], int k
   if (real < k) return 0u;
   mx = wave_ext32<true>(mx);
   mn = wave_ext32<false>(mn);
-  if (mx == mn) return mx;
+  mn = lo > mn ? lo : mn;
+  if (mx <= mn) return mx;
+  constexpr uint32_t kTwoBinades = 2u << 23;
+  if (mx - mn > kTwoBinades) {
+    const uint32_t near = mx - kTwoBinades;
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) c += __popcll(__ballot(v[i] >= near));
+    if (c >= k) mn = near;
+  }
   const int top = 31 - __builtin_clz(mx ^ mn);
   uint32_t p = mx & ~((2u << top) - 1u);
   for (int b = top; b >= 0 && b > top - kThrBits; --b) {
@@ -1170,10 +1182,13 @@ __global__ void __launch_bounds__(kThreads)
     const int cnt0 = s.count;  // block-uniform: the buffer is settled between tiles
     uint32_t g[kWideGroups];
     tile.group_keys(g);
-    const uint32_t tb = red.min(wave_kth_multi<kWideGroups>(g, kw));
+    const uint32_t tw = wave_kth_multi<kWideGroups>(g, kw, 0u);
+    const uint32_t tb = red.min(tw);
     thr = tb > thr ? tb : thr;
     if (nchunks > 1) {
-      const uint32_t qb = red.min(wave_kth_multi<kWideGroups>(g, kwq));
+      // q <= k, so the wave's q-th largest group maximum is at or above its k-bound: the search starts there (the
+      // groups' smallest maximum is often negative, and 12 bits over that range resolve the bound to about 0.5)
+      const uint32_t qb = red.min(wave_kth_multi<kWideGroups>(g, kwq, tw));
       thq = qb > thq ? qb : thq;
     }
     tile.opaque();
