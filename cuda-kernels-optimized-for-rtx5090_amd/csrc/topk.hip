@@ -1020,7 +1020,7 @@ constexpr int kRankBuckets = 2048;  // buckets of write_ranked
 // its bucket's members above it. Nearly linear on spread-out values; a bucket holding many candidates (values
 // clustered far below an outlier) costs its size per member. Every thread calls it.
 template <typename T, typename S>
-__device__ void write_ranked(S& s, int m, int k, void* values, long long* indices, long long row) {
+__device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, long long* indices, long long row) {
   constexpr int P = kWideList / kThreads;
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan
   static_assert(kWideList * 2 <= kWideCap && kRankBuckets * 2 * sizeof(unsigned) <= kWideList * sizeof(u64),
@@ -1081,16 +1081,34 @@ __device__ void write_ranked(S& s, int m, int k, void* values, long long* indice
   for (int r = 0; r < P; ++r)
     if (r * kThreads + t < m) sorted[first[bk[r]] + slot[r]] = c[r];
   __syncthreads();
+  // Ranked in bucket order: lane i takes sorted[i], so neighbouring lanes read the same bucket's members (LDS
+  // broadcasts rather than scattered reads) and write neighbouring output positions. Every position first, then the
+  // stores; bucket members four at a time (reads past a bucket stay inside the buffer: m + 3 <= kWideList + 3 <
+  // kWideCap).
+  int pos[P];
 #pragma unroll
   for (int r = 0; r < P; ++r) {
-    if (r * kThreads + t >= m) continue;
-    const int f = (int)first[bk[r]], n = (int)cnt[bk[r]];
-    int pos = f;
-    for (int j = 0; j < n; ++j) pos += sorted[f + j] > c[r];
-    if (pos < k) {
-      if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + pos] = composite_bits(c[r]);
-      else static_cast<uint16_t*>(values)[row * k + pos] = (uint16_t)(composite_bits(c[r]) >> 16);
-      indices[row * k + pos] = composite_index(c[r]);
+    const int i = r * kThreads + t;
+    pos[r] = k;
+    if (i < m) {
+      c[r] = sorted[i];
+      const u64 d = (mx - c[r]) >> sh;
+      const int b = d < (u64)kRankBuckets ? (int)d : kRankBuckets - 1;
+      const int f = (int)first[b], n = (int)cnt[b];
+      int q = f;
+      for (int j = 0; j < n; j += 4) {
+        const u64 a = sorted[f + j], e1 = sorted[f + j + 1], e2 = sorted[f + j + 2], e3 = sorted[f + j + 3];
+        q += (a > c[r]) + (j + 1 < n && e1 > c[r]) + (j + 2 < n && e2 > c[r]) + (j + 3 < n && e3 > c[r]);
+      }
+      pos[r] = q;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    if (pos[r] < k) {
+      if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + pos[r]] = composite_bits(c[r]);
+      else static_cast<uint16_t*>(values)[row * k + pos[r]] = (uint16_t)(composite_bits(c[r]) >> 16);
+      indices[row * k + pos[r]] = composite_index(c[r]);
     }
   }
 }
