@@ -1018,9 +1018,12 @@ constexpr int kRankBuckets = 2048;  // buckets of write_ranked
 // kRankBuckets buckets, with LDS counters; an exclusive scan of the counts gives each bucket's first output position;
 // the candidates are scattered by bucket into LDS, and each one's position is its bucket's first plus the number of
 // its bucket's members above it. Nearly linear on spread-out values; a bucket holding many candidates (values
-// clustered far below an outlier) costs its size per member. Every thread calls it.
+// clustered far below an outlier) costs its size per member. `lo`, when not 0, is a lower bound of the candidates known
+// to the caller, used in place of their minimum (a candidate below it would still be ordered exactly: it lands in the
+// last bucket, below every other bucket's members). Every thread calls it.
 template <typename T, typename S>
-__device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, long long* indices, long long row) {
+__device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, long long* indices, long long row,
+                                             u64 lo) {
   constexpr int P = kWideList / kThreads;
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan
   static_assert(kWideList * 2 <= kWideCap && kRankBuckets * 2 * sizeof(unsigned) <= kWideList * sizeof(u64),
@@ -1038,7 +1041,7 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
     }
   }
   mx = block_ext64<true>(mx, s);  // also orders every read of s.buf above before the writes below
-  mn = block_ext64<false>(mn, s);
+  mn = lo ? lo : block_ext64<false>(mn, s);
   const u64 range = mx - mn;
   const int bits = range ? 64 - __clzll(range) : 0;
   const int sh = bits > 11 ? bits - 11 : 0;
@@ -1050,7 +1053,8 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   int bk[P], slot[P];
 #pragma unroll
   for (int r = 0; r < P; ++r) {
-    bk[r] = (int)((mx - c[r]) >> sh);
+    const u64 d = (mx - c[r]) >> sh;
+    bk[r] = d < (u64)kRankBuckets ? (int)d : kRankBuckets - 1;
     slot[r] = r * kThreads + t < m ? (int)atomicAdd(&cnt[bk[r]], 1u) : 0;
   }
   __syncthreads();
@@ -1237,7 +1241,7 @@ __global__ void __launch_bounds__(kThreads)
   }
   if (nchunks == 1) {
     if (s.count > kWideList) prune(s, k);
-    write_ranked<T>(s, s.count, k, values, indices, row);
+    write_ranked<T>(s, s.count, k, values, indices, row, 0ull);
     return;
   }
   if (s.count > kWideList) prune(s, k);
@@ -1281,7 +1285,8 @@ __global__ void __launch_bounds__(kThreads)
   }
   __syncthreads();
   constexpr int PER = kWideList / kThreads;
-  u64 ca[PER], cb[PER];
+  constexpr int kInFlight = 2;  // lists whose loads are in flight while one is taken (4 measured no faster)
+  u64 cv[kInFlight][PER];
   auto load = [&](int c, u64 (&v)[PER]) {
     const int cnt = counts[c];
 #pragma unroll
@@ -1303,17 +1308,20 @@ __global__ void __launch_bounds__(kThreads)
     if (__ballot(any)) append<PER>(s, v, keep);
     __syncthreads();
   };
-  load(0, ca);
-  for (int c = 0; c < nchunks; c += 2) {  // the next list's loads are in flight while one is taken
-    if (c + 1 < nchunks) load(c + 1, cb);
-    take(ca);
-    if (c + 1 < nchunks) {
-      if (c + 2 < nchunks) load(c + 2, ca);
-      take(cb);
+#pragma unroll
+  for (int j = 0; j < kInFlight; ++j)
+    if (j < nchunks) load(j, cv[j]);
+  for (int c = 0; c < nchunks; c += kInFlight) {
+#pragma unroll
+    for (int j = 0; j < kInFlight; ++j) {
+      if (c + j < nchunks) {
+        take(cv[j]);
+        if (c + j + kInFlight < nchunks) load(c + j + kInFlight, cv[j]);
+      }
     }
   }
   if (s.count > kWideList) prune(s, k);
-  write_ranked<T>(s, s.count, k, values, indices, row);
+  write_ranked<T>(s, s.count, k, values, indices, row, floor);  // every candidate kept is at or above the floor
   if (threadIdx.x == 0)
     __hip_atomic_store(arrivals + row * kArrivalStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
