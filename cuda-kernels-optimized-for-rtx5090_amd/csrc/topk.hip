@@ -110,6 +110,21 @@ __device__ __forceinline__ int lanes_below(u64 mask) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+// The exclusive prefix over the wave's lanes of a count n in [0, 2^B), and the wave's total in `total`: a ballot per
+// bit of n.
+template <int B>
+__device__ __forceinline__ int wave_excl_count(int n, int& total) {
+  int excl = 0, tot = 0;
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const u64 m = __ballot((n >> b) & 1);
+    excl += lanes_below(m) << b;
+    tot += __popcll(m) << b;
+  }
+  total = tot;
+  return excl;
+}
+
 // Appends the lane's composites c with keep to buf: one LDS atomic per wave reserves the wave's total. Returns the
 // buffer fill right after the wave's append (0 if it appended nothing); the largest over a block's appends is the
 // block's final count.
@@ -730,54 +745,47 @@ struct Tile {
     }
   }
 
+  // Whether element j of vector v has key >= K, where t = bits_of(K) (the compare of filter()).
+  template <bool NEG>
+  __device__ __forceinline__ bool admits(int v, int j, uint32_t t) const {
+    if constexpr (sizeof(T) == 4) {
+      return NEG ? r[v][j] <= t : (int)r[v][j] >= (int)t;
+    } else {
+      const uint32_t w = r[v][j >> 1];
+      if (j & 1) return NEG ? w <= (t | 0xffffu) : (int)w >= (int)t;
+      return NEG ? (uint16_t)w <= (uint16_t)(t >> 16) : (int16_t)(uint16_t)w >= (int16_t)(uint16_t)(t >> 16);
+    }
+  }
+
   // filter() into a shared buffer: appends every element with key >= K (K above the sentinel's key; NEG: K is a
-  // negative value) to s.buf, reserving each batch of 16 elements per lane with one LDS atomic per wave. Appends past
-  // the buffer's end are counted in s.count and not stored.
+  // negative value) to s.buf in two passes. Each lane counts its admitted elements. One exclusive prefix over the
+  // wave (a ballot per bit of the counts) and one LDS atomic per wave reserve the wave's positions, and each lane
+  // writes its elements in order. This needs no ballot per element, which at the wide kernel's admission rate (an
+  // admitted lane in nearly every 64-lane column) cost as many scalar instructions as the compares. Appends past the
+  // buffer's end are counted in s.count and not stored.
   template <bool NEG, typename S>
   __device__ __forceinline__ void filter_append(S& s, uint32_t K) {
-    constexpr int VB = 16 / W;  // vectors per batch
     const uint32_t t = bits_of(K);
+    int n = 0;
 #pragma unroll
-    for (int v0 = 0; v0 < NV; v0 += VB) {
-      bool a[VB][W];
-      u64 m[VB][W];
-      int tot = 0;
+    for (int v = 0; v < NV; ++v)
 #pragma unroll
-      for (int vb = 0; vb < VB; ++vb)
+      for (int j = 0; j < W; ++j) n += admits<NEG>(v, j, t) ? 1 : 0;
+    int total = 0;
+    const int excl = wave_excl_count<7>(n, total);  // n <= kTileE = 64
+    if (total == 0) return;
+    int base = 0;
+    if (lane_id() == 0) base = atomicAdd(&s.count, total);
+    int pos = __builtin_amdgcn_readfirstlane(base) + excl;
+    constexpr int kCap = (int)(sizeof(s.buf) / sizeof(u64));
 #pragma unroll
-        for (int j = 0; j < W; ++j) {
-          const int v = v0 + vb;
-          if constexpr (sizeof(T) == 4) {
-            a[vb][j] = NEG ? r[v][j] <= t : (int)r[v][j] >= (int)t;
-          } else {
-            const uint32_t w = r[v][j >> 1];
-            if (j & 1) a[vb][j] = NEG ? w <= (t | 0xffffu) : (int)w >= (int)t;
-            else a[vb][j] = NEG ? (uint16_t)w <= (uint16_t)(t >> 16)
-                                : (int16_t)(uint16_t)w >= (int16_t)(uint16_t)(t >> 16);
-          }
-          m[vb][j] = __ballot(a[vb][j]);
-          tot += __popcll(m[vb][j]);
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+      for (int j = 0; j < W; ++j)
+        if (admits<NEG>(v, j, t)) {
+          if (pos < kCap) s.buf[pos] = comp(v, j);
+          ++pos;
         }
-      if (tot) {
-        int base = 0;
-        if (lane_id() == 0) base = atomicAdd(&s.count, tot);
-        base = __builtin_amdgcn_readfirstlane(base);
-#pragma unroll
-        for (int vb = 0; vb < VB; ++vb)
-#pragma unroll
-          for (int j = 0; j < W; ++j) {
-            const u64 mm = m[vb][j];
-            if (mm) {
-              if (a[vb][j]) {
-                const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32),
-                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)mm, (uint32_t)base));
-                if (pos < (int)(sizeof(s.buf) / sizeof(u64))) s.buf[pos] = comp(v0 + vb, j);
-              }
-              base += __popcll(mm);
-            }
-          }
-      }
-    }
   }
 
   // Appends the elements of vector v, held in r[0], with composites >= floor to s.buf (exact validity; the caller
