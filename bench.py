@@ -163,12 +163,11 @@ class Case:
                 counters = torch.zeros(rows, dtype=torch.int32, device=dev)
                 keep = (x, vals, idx, drawn, work, counters)
 
-                def run():
-                    err = lib.launch(keep[0].data_ptr(), vals.data_ptr(), idx.data_ptr(), work.data_ptr(),
-                                     counters.data_ptr(), rows, cols, k, 0, cand._THREADS, cand._DEPTH, chunk,
-                                     stream())
-                    return err or lib.topk_sample_launch(vals.data_ptr(), idx.data_ptr(), uni.data_ptr(),
-                                                         drawn.data_ptr(), rows, k, 0, temp, top_p, stream())
+                def run():  # top-k with the draw fused into its launch
+                    return lib.topk_launch_sample(keep[0].data_ptr(), vals.data_ptr(), idx.data_ptr(),
+                                                  work.data_ptr(), counters.data_ptr(), rows, cols, k, 0,
+                                                  cand._THREADS, cand._DEPTH, chunk, uni.data_ptr(), drawn.data_ptr(),
+                                                  temp, top_p, stream())
                 return run
             footprint = inp["x"].numel() * 4
         elif name.startswith("topk"):

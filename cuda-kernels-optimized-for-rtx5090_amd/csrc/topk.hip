@@ -284,6 +284,7 @@ constexpr int kBestOffset = 2;
 struct TileSmem {
   u64 seg[kWaves][kTileSeg];
   alignas(16) u64 sorted[kTileSort];
+  u64 top[kSeedMaxK];  // an output row's composites in order (for the fused draw)
   uint32_t red[2][kWaves];
   int cnt[kWaves];
   u64 pick;
@@ -574,6 +575,7 @@ __device__ __forceinline__ void finish_list(TileSmem& s, const TileList& L, void
         if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + rank] = composite_bits(mine);
         else static_cast<uint16_t*>(values)[row * k + rank] = (uint16_t)(composite_bits(mine) >> 16);
         indices[row * k + rank] = composite_index(mine);
+        s.top[rank] = mine;
       } else {
         __hip_atomic_store(wr + rank, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
@@ -889,6 +891,143 @@ __device__ __forceinline__ void merge_lists(TileSmem& s, BlockRed& red, TileList
   finish_list<T>(s, L, values, indices, nullptr, row, k, true);
 }
 
+// ---- sampling from the top k ---------------------------------------------------------------------------------------
+
+constexpr int kSamplePer = kMaxK / kWave;  // list entries per lane (k <= 1024)
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), lane));
+}
+
+// Inclusive prefix sum over the wave's lanes (lane order).
+__device__ __forceinline__ float wave_prefix(float v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const float o = __shfl_up(v, d, kWave);
+    v += lane >= d ? o : 0.0f;
+  }
+  return v;
+}
+
+// The draw from row `row` of a top-k list (values [rows, k] in T, int64 indices, as topk writes them) by one wave
+// (every lane returns it): temperature, top-p and a draw with the caller's uniform u[row] in [0, 1). With x = value /
+// temperature, e_i = exp(x_i - max x) and S_i = e_0 + ... + e_i (list order), the draw keeps the entries i with S_(i-1)
+// < top_p * S_(k-1) (always the first; every entry when top_p >= 1), and picks the first kept i with S_i > u *
+// S_last_kept (the last kept if rounding leaves none). temperature <= 0 is greedy: position 0, the list's largest value
+// (lowest index among ties). Values must be finite when temperature > 0. Lane l holds positions [l E, l E + E), E =
+// ceil(k / 64).
+template <typename Value, typename Index>
+__device__ __forceinline__ long long sample_row(const Value& value_at, const Index& index_at, long long row, int k,
+                                                const float* u, float temperature, float top_p) {
+  const int lane = lane_id();
+  const int per = (k + kWave - 1) / kWave;
+  const int base = lane * per;
+  float x[kSamplePer];
+#pragma unroll
+  for (int e = 0; e < kSamplePer; ++e) {
+    const int i = base + e;
+    x[e] = e < per && i < k ? value_at(i) : -INFINITY;
+  }
+  int chosen;
+  if (temperature <= 0.0f) {
+    chosen = 0;  // greedy: the list's first entry, its largest value (lowest position among ties)
+  } else {
+    float m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < kSamplePer; ++e) {
+      x[e] = x[e] / temperature;
+      m = fmaxf(m, x[e]);
+    }
+    m = wave_max(m);
+    float run = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kSamplePer; ++e) {
+      const float ex = (e < per && base + e < k) ? expf(x[e] - m) : 0.0f;
+      run += ex;
+      x[e] = run;  // lane-local inclusive sums
+    }
+    const float lane_excl = wave_prefix(run) - run;
+    const float total = readlane_f(wave_prefix(run), kWave - 1);
+    const float cut = top_p * total;
+    // kept: positions whose exclusive sum is below the cut (a prefix of the list; at least position 0)
+    int keep = 0;
+#pragma unroll
+    for (int e = 0; e < kSamplePer; ++e) {
+      const float excl = lane_excl + (e ? x[e - 1] : 0.0f);
+      keep += (e < per && base + e < k && (base + e == 0 || top_p >= 1.0f || excl < cut)) ? 1 : 0;
+    }
+    const int kept = (int)wave_sum((float)keep);
+    // the kept mass is the inclusive sum at position kept - 1
+    float mass = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kSamplePer; ++e)
+      if (e < per && base + e == kept - 1) mass = lane_excl + x[e];
+    mass = wave_max(mass);
+    const float target = u[row] * mass;
+    int first = kept - 1;
+#pragma unroll
+    for (int e = 0; e < kSamplePer; ++e) {
+      const int i = base + e;
+      if (e < per && i < kept && lane_excl + x[e] > target && i < first) first = i;
+    }
+    chosen = (int)wave_ext32<false>((uint32_t)first);
+  }
+  return index_at(chosen);
+}
+
+// Accessors of row `row` of a top-k list in memory (values in T, int64 indices), for sample_row.
+template <typename T>
+struct ListInMemory {
+  const void* values;
+  const long long* indices;
+  long long row;
+  int k;
+  __device__ __forceinline__ float operator()(int i) const {
+    if constexpr (sizeof(T) == 4) return static_cast<const float*>(values)[row * k + i];
+    else return __uint_as_float((uint32_t) static_cast<const uint16_t*>(values)[row * k + i] << 16);
+  }
+  __device__ __forceinline__ long long index(int i) const { return indices[row * k + i]; }
+};
+
+// Sampling fused into the top-k launch (topk_launch_sample): when out is not null, the workgroup that writes a row's
+// values and indices then draws out[row] from them as topk_sample does (k = 1: the one index).
+struct SampleArgs {
+  const float* u;
+  long long* out;
+  float temperature;
+  float top_p;
+};
+
+// The fused draw of a row whose list this workgroup's waves have just written: every thread calls it (the barrier
+// makes the list visible to the first wave, which draws).
+template <typename T>
+__device__ __forceinline__ void sample_list(const SampleArgs& sa, const void* values, const long long* indices,
+                                            long long row, int k) {
+  if (!sa.out) return;
+  __syncthreads();
+  if (wave_id() != 0) return;
+  const ListInMemory<T> list{values, indices, row, k};
+  const long long drawn =
+      sample_row(list, [&](int i) { return list.index(i); }, row, k, sa.u, sa.temperature, sa.top_p);
+  if (lane_id() == 0) sa.out[row] = drawn;
+}
+
+// sample_list for a row whose composites finish_list also left in order in top[] (LDS): the values are decoded from
+// the composites (the bits written to the output), so the draw equals the one from memory.
+__device__ __forceinline__ void sample_top(const SampleArgs& sa, const u64* top, long long row, int k) {
+  if (!sa.out) return;
+  __syncthreads();
+  if (wave_id() != 0) return;
+  const long long drawn = sample_row([&](int i) { return __uint_as_float(composite_bits(top[i])); },
+                                     [&](int i) { return composite_index(top[i]); }, row, k, sa.u, sa.temperature,
+                                     sa.top_p);
+  if (lane_id() == 0) sa.out[row] = drawn;
+}
+
+
+// ---- the k <= 64 kernel --------------------------------------------------------------------------------------------
+
 // k <= 64: one 256-thread workgroup per (chunk, row). The chunk is taken in register tiles of 16384 elements, all of a
 // tile's loads in flight at once. Per tile: each wave takes (a lower bound of) the ceil(k / 4)-th largest of its 64
 // lane maxima, which has that many distinct elements at or above it, and the smallest of the four waves' keys has at
@@ -903,7 +1042,7 @@ template <typename T, bool VEC>
 __global__ void __launch_bounds__(kThreads)
     topk_tile(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
               u64* __restrict__ work, unsigned* __restrict__ arrivals, long long cols, long long chunk, int nchunks,
-              int k) {
+              int k, SampleArgs sa) {
   __shared__ TileSmem s;
   const long long row = blockIdx.y;
   const int part = blockIdx.x;
@@ -954,6 +1093,7 @@ __global__ void __launch_bounds__(kThreads)
   }
   if (nchunks == 1) {
     finish_list<T>(s, L, values, indices, nullptr, row, k, true);
+    sample_top(sa, s.top, row, k);
     return;
   }
   if (k == 1) {
@@ -979,6 +1119,7 @@ __global__ void __launch_bounds__(kThreads)
         if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row] = composite_bits(c);
         else static_cast<uint16_t*>(values)[row] = (uint16_t)(composite_bits(c) >> 16);
         indices[row] = composite_index(c);
+        if (sa.out) sa.out[row] = composite_index(c);  // the draw from a one-entry list
         __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
@@ -1002,6 +1143,7 @@ __global__ void __launch_bounds__(kThreads)
   merge_lists<T>(s, red, L, values, indices, wr, row, nchunks, k);
   if (threadIdx.x == 0)
     __hip_atomic_store(arrivals + row * kArrivalStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  sample_top(sa, s.top, row, k);
 }
 
 // ---- wide kernel (64 < k <= 1024) ----------------------------------------------------------------------------------
@@ -1183,7 +1325,7 @@ template <typename T, bool VEC>
 __global__ void __launch_bounds__(kThreads)
     topk_wide(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
               u64* __restrict__ lists, unsigned* __restrict__ arrivals, long long cols, long long chunk, int nchunks,
-              int k) {
+              int k, SampleArgs sa) {
   __shared__ Smem<kWideCap> s;
   __shared__ uint32_t redslots[2][kWaves];
   __shared__ int counts[kWideMaxChunks];
@@ -1250,6 +1392,7 @@ __global__ void __launch_bounds__(kThreads)
   if (nchunks == 1) {
     if (s.count > kWideList) prune(s, k);
     write_ranked<T>(s, s.count, k, values, indices, row, 0ull);
+    sample_list<T>(sa, values, indices, row, k);
     return;
   }
   if (s.count > kWideList) prune(s, k);
@@ -1332,98 +1475,19 @@ __global__ void __launch_bounds__(kThreads)
   write_ranked<T>(s, s.count, k, values, indices, row, floor);  // every candidate kept is at or above the floor
   if (threadIdx.x == 0)
     __hip_atomic_store(arrivals + row * kArrivalStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  sample_list<T>(sa, values, indices, row, k);
 }
 
-// ---- sampling from the top k ----------------------------------------------------------------------------------------
-
-constexpr int kSamplePer = kMaxK / kWave;  // list entries per lane (k <= 1024)
-
-__device__ __forceinline__ float readlane_f(float v, int lane) {
-  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), lane));
-}
-
-// Inclusive prefix sum over the wave's lanes (lane order).
-__device__ __forceinline__ float wave_prefix(float v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const float o = __shfl_up(v, d, kWave);
-    v += lane >= d ? o : 0.0f;
-  }
-  return v;
-}
-
-// One wave per row of a top-k list (values [rows, k] in T, int64 indices, as topk writes them): temperature, top-p
-// and a draw with the caller's uniform u[row] in [0, 1). With x = value / temperature, e_i = exp(x_i - max x) and
-// S_i = e_0 + ... + e_i (list order), the draw keeps the entries i with S_(i-1) < top_p * S_(k-1) (always the
-// first; every entry when top_p >= 1), and picks the first kept i with S_i > u * S_last_kept (the last kept if
-// rounding leaves none). temperature
-// <= 0 is greedy: position 0, the list's largest value (lowest index among ties). Values must be finite when
-// temperature > 0. Lane l holds positions [l E, l E + E), E = ceil(k / 64).
+// One wave per row of a top-k list (values [rows, k] in T, int64 indices, as topk writes them): out[row] drawn by
+// sample_row.
 template <typename T>
 __global__ void __launch_bounds__(kWave)
     topk_sample(const void* __restrict__ values, const long long* __restrict__ indices, const float* __restrict__ u,
                 long long* __restrict__ out, int k, float temperature, float top_p) {
   const long long row = blockIdx.x;
-  const int lane = lane_id();
-  const int per = (k + kWave - 1) / kWave;
-  const int base = lane * per;
-  float x[kSamplePer];
-#pragma unroll
-  for (int e = 0; e < kSamplePer; ++e) {
-    const int i = base + e;
-    float v = -INFINITY;
-    if (e < per && i < k) {
-      if constexpr (sizeof(T) == 4) v = static_cast<const float*>(values)[row * k + i];
-      else v = __uint_as_float((uint32_t) static_cast<const uint16_t*>(values)[row * k + i] << 16);
-    }
-    x[e] = v;
-  }
-  int chosen;
-  if (temperature <= 0.0f) {
-    chosen = 0;  // greedy: the list's first entry, its largest value (lowest position among ties)
-  } else {
-    float m = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < kSamplePer; ++e) {
-      x[e] = x[e] / temperature;
-      m = fmaxf(m, x[e]);
-    }
-    m = wave_max(m);
-    float run = 0.0f;
-#pragma unroll
-    for (int e = 0; e < kSamplePer; ++e) {
-      const float ex = (e < per && base + e < k) ? expf(x[e] - m) : 0.0f;
-      run += ex;
-      x[e] = run;  // lane-local inclusive sums
-    }
-    const float lane_excl = wave_prefix(run) - run;
-    const float total = readlane_f(wave_prefix(run), kWave - 1);
-    const float cut = top_p * total;
-    // kept: positions whose exclusive sum is below the cut (a prefix of the list; at least position 0)
-    int keep = 0;
-#pragma unroll
-    for (int e = 0; e < kSamplePer; ++e) {
-      const float excl = lane_excl + (e ? x[e - 1] : 0.0f);
-      keep += (e < per && base + e < k && (base + e == 0 || top_p >= 1.0f || excl < cut)) ? 1 : 0;
-    }
-    const int kept = (int)wave_sum((float)keep);
-    // the kept mass is the inclusive sum at position kept - 1
-    float mass = 0.0f;
-#pragma unroll
-    for (int e = 0; e < kSamplePer; ++e)
-      if (e < per && base + e == kept - 1) mass = lane_excl + x[e];
-    mass = wave_max(mass);
-    const float target = u[row] * mass;
-    int first = kept - 1;
-#pragma unroll
-    for (int e = 0; e < kSamplePer; ++e) {
-      const int i = base + e;
-      if (e < per && i < kept && lane_excl + x[e] > target && i < first) first = i;
-    }
-    chosen = (int)wave_ext32<false>((uint32_t)first);
-  }
-  if (lane == 0) out[row] = indices[row * k + chosen];
+  const ListInMemory<T> list{values, indices, row, k};
+  const long long drawn = sample_row(list, [&](int i) { return list.index(i); }, row, k, u, temperature, top_p);
+  if (lane_id() == 0) out[row] = drawn;
 }
 
 // ---- host side ------------------------------------------------------------------------------------------------------
@@ -1435,7 +1499,7 @@ constexpr int kListsPurpose = 3;     // stream_workspace key of the 64 < k kerne
 
 template <typename T, bool VEC>
 int launch_chunks(const void* x, void* values, void* indices, void* work, long long rows,
-                  long long cols, long long chunk, int nchunks, int k, hipStream_t stream) {
+                  long long cols, long long chunk, int nchunks, int k, const SampleArgs& sa, hipStream_t stream) {
   const dim3 grid((unsigned)nchunks, (unsigned)rows);
   if (k <= kSeedMaxK) {
     unsigned* arrivals = nullptr;
@@ -1446,7 +1510,7 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, long l
       if (!arrivals) return err;
     }
     hipLaunchKernelGGL((topk_tile<T, VEC>), grid, dim3(kThreads), 0, stream, (const T*)x, values, (long long*)indices,
-                       (u64*)work, arrivals, cols, chunk, nchunks, k);
+                       (u64*)work, arrivals, cols, chunk, nchunks, k, sa);
     return (int)hipGetLastError();
   }
   // The result does not depend on the chunking, so the chunks are made long enough for a useful bound (16k elements:
@@ -1470,7 +1534,7 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, long l
   }
   const dim3 wgrid((unsigned)nchunks, (unsigned)rows);
   hipLaunchKernelGGL((topk_wide<T, VEC>), wgrid, dim3(kThreads), 0, stream, (const T*)x, values, (long long*)indices,
-                     lists, arrivals, cols, chunk, nchunks, k);
+                     lists, arrivals, cols, chunk, nchunks, k, sa);
   return (int)hipGetLastError();
 }
 
@@ -1517,8 +1581,9 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
 // reference's, except that k may be up to 1024 (the reference stops at 512): rows <= 0 or k <= 0 is a no-op; -1 for k
 // > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0, a split row with chunk % 4 or nchunks * k > INT_MAX
 // / 2, threads not 128, 256 or 512, depth not 2, 4 or 8, or a dtype other than 0 and 1.
-extern "C" int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
-                      long long cols, int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream) {
+namespace {
+int launch_impl(const void* x, void* values, void* indices, void* work, long long rows, long long cols, int k,
+                int dtype, int threads, int depth, long long chunk, const SampleArgs& sa, hipStream_t stream) {
   if (rows <= 0 || k <= 0) return rw_host::kOk;
   if (k > cols || k > kMaxK || cols > INT_MAX / 2 || rows > 65535 || chunk <= 0) return rw_host::kInvalid;
   const long long nchunks = (cols + chunk - 1) / chunk;
@@ -1527,15 +1592,38 @@ extern "C" int launch(const void* x, void* values, void* indices, void* work, vo
     return rw_host::kInvalid;
   if (dtype == 0) {
     if (cols % 4 == 0 && rw_host::aligned16(x))
-      return launch_chunks<float, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
-    return launch_chunks<float, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
+      return launch_chunks<float, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, sa, stream);
+    return launch_chunks<float, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, sa, stream);
   }
   if (dtype == 1) {
     if (cols % 8 == 0 && (chunk % 8 == 0 || nchunks == 1) && rw_host::aligned16(x))
-      return launch_chunks<uint16_t, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
-    return launch_chunks<uint16_t, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, stream);
+      return launch_chunks<uint16_t, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, sa, stream);
+    return launch_chunks<uint16_t, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, sa, stream);
   }
   return rw_host::kInvalid;
+}
+}  // namespace
+
+extern "C" int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
+                      long long cols, int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream) {
+  (void)counters;
+  return launch_impl(x, values, indices, work, rows, cols, k, dtype, threads, depth, chunk,
+                     SampleArgs{nullptr, nullptr, 0.0f, 0.0f}, stream);
+}
+
+// No counterpart in the reference (the top-k launch of a decoder's sampler with the draw fused in): launch(), and in
+// the same kernel the draw of topk_sample_launch() from each row's list -- the workgroup that writes a row's values and
+// indices draws out[row] from them, so out equals topk_sample_launch() on launch()'s output. Same arguments and checks
+// as launch(), plus uniforms[rows] (fp32 in [0, 1)), out (int64 [rows]), temperature (<= 0: greedy) and top_p (>= 1:
+// no nucleus cut); -1 also for a null uniforms or out when rows > 0.
+extern "C" int topk_launch_sample(const void* x, void* values, void* indices, void* work, void* counters,
+                                  long long rows, long long cols, int k, int dtype, int threads, int depth,
+                                  long long chunk, const float* uniforms, void* out, float temperature, float top_p,
+                                  hipStream_t stream) {
+  (void)counters;
+  if (rows > 0 && k > 0 && (!uniforms || !out)) return rw_host::kInvalid;
+  return launch_impl(x, values, indices, work, rows, cols, k, dtype, threads, depth, chunk,
+                     SampleArgs{uniforms, (long long*)out, temperature, top_p}, stream);
 }
 
 // No counterpart in the reference (whose counters self-reset only when a launch completes): zeroes counters[0, rows)

@@ -47,6 +47,10 @@ _lib.topk_reset.restype = ctypes.c_int
 _lib.topk_sample_launch.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
                                                              ctypes.c_float, ctypes.c_float, ctypes.c_void_p]
 _lib.topk_sample_launch.restype = ctypes.c_int
+_lib.topk_launch_sample.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_longlong, ctypes.c_longlong] + [ctypes.c_int] * 4 + \
+                                   [ctypes.c_longlong, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_float,
+                                    ctypes.c_void_p]
+_lib.topk_launch_sample.restype = ctypes.c_int
 
 _counters = {}
 _last = None  # (key, chunk, work pointer, counters pointer, work, counters) of the last shape
@@ -116,3 +120,29 @@ def sample(values, indices, uniforms, temperature=1.0, top_p=1.0):
     if err:
         raise RuntimeError(f"kernel launch failed: HIP error {err}")
     return out
+
+
+def run_and_sample(inputs, uniforms, temperature=1.0, top_p=1.0):
+    """run() and sample() in one launch: the workgroup that writes a row's values and indices also draws the row's
+    index (topk_launch_sample). Returns (values, indices, drawn int64 [rows]), equal to run() followed by sample()."""
+    x = inputs["x"]
+    k = int(inputs.get("k", K))
+    dtype = _DTYPES.get(x.dtype)
+    if dtype is None or x.dim() != 2 or not 1 <= k <= K_MAX or x.shape[1] < k or x.device.type != "cuda":
+        raise ValueError(f"topk candidate takes a 2-D fp32 or bf16 GPU tensor with at least k columns and "
+                         f"1 <= k <= {K_MAX}, got {x.dtype} with shape {tuple(x.shape)} on {x.device}, k = {k}")
+    if uniforms.dtype != torch.float32 or tuple(uniforms.shape) != (x.shape[0],) or uniforms.device != x.device:
+        raise ValueError(f"topk sample takes fp32 uniforms [rows] on x's device, got {uniforms.dtype} "
+                         f"{tuple(uniforms.shape)} on {uniforms.device}")
+    x, uniforms = x.contiguous(), uniforms.contiguous()
+    rows, cols = x.shape
+    _, chunk, work_ptr, counters_ptr, _, _ = _plan(x, rows, cols, dtype, k)
+    values = torch.empty((rows, k), dtype=x.dtype, device=x.device)
+    indices = torch.empty((rows, k), dtype=torch.int64, device=x.device)
+    drawn = torch.empty(rows, dtype=torch.int64, device=x.device)
+    err = _lib.topk_launch_sample(x.data_ptr(), values.data_ptr(), indices.data_ptr(), work_ptr, counters_ptr, rows,
+                                  cols, k, dtype, _THREADS, _DEPTH, chunk, uniforms.data_ptr(), drawn.data_ptr(),
+                                  float(temperature), float(top_p), torch.cuda.current_stream(x.device).cuda_stream)
+    if err:
+        raise RuntimeError(f"kernel launch failed: HIP error {err}")
+    return values, indices, drawn

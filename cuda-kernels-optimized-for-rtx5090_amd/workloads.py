@@ -81,7 +81,7 @@ def topk_128x128256():
 
 def topk_sample_128x128256():
     """Top-k (k = 50) and a draw from it per row (temperature 0.8, top_p 0.9) over the top-k workload's logits, with
-    seeded uniforms, seed 4."""
+    seeded uniforms, seed 4 (one launch: topk_launch_sample)."""
     inp = topk_128x128256()
     g = torch.Generator().manual_seed(4)
     inp.update({"k": 50, "temperature": 0.8, "top_p": 0.9, "uniforms": torch.rand(128, generator=g)})

@@ -46,6 +46,15 @@ int topk_reset(void* counters, long long rows, hipStream_t stream);
 int topk_sample_launch(const void* values, const void* indices, const float* uniforms, void* out, long long rows, int k,
                        int dtype, float temperature, float top_p, hipStream_t stream);
 
+/* No counterpart in the reference (the top-k launch of a decoder's sampler, with the draw fused in): launch() plus, in
+ * the same kernel, topk_sample_launch()'s draw from each row's list -- the workgroup that writes a row's values and
+ * indices draws out[row] from them, so out equals topk_sample_launch() on launch()'s output and one launch (and its
+ * launch gap) is saved. Arguments and checks of launch(), plus uniforms[rows] (fp32 in [0, 1)), out (int64 [rows]),
+ * temperature (<= 0: greedy) and top_p (>= 1: no nucleus cut); -1 also for a null uniforms or out when rows > 0. */
+int topk_launch_sample(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
+                       long long cols, int k, int dtype, int threads, int depth, long long chunk, const float* uniforms,
+                       void* out, float temperature, float top_p, hipStream_t stream);
+
 /* No counterpart in the reference: tuning override for parameter sweeps. Slot 0: resident workgroups per CU assumed by
  * plan(). Returns 0 or -1. */
 int topk_tune(int slot, int value);

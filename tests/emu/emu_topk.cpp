@@ -1,7 +1,8 @@
 // Runs csrc/topk.hip's plan() and launch() under the CPU emulation (hip/hip_runtime.h beside this file) and compares
 // every launch with the oracle (oracle/oracle.c: oracle_topk), bit for bit: values, int64 indices, and the caller's
-// counters left at zero. Every buffer the kernels touch (input, outputs, work, counters and the library's own
-// workspaces) lies between guard pages.
+// counters left at zero. Each launch is followed by topk_launch_sample(), whose values, indices and draws must equal
+// launch()'s and topk_sample_launch()'s on them. Every buffer the kernels touch (input, outputs, work, counters and
+// the library's own workspaces) lies between guard pages.
 //
 // usage: emu_topk rows cols dtype ks chunk min_chunk reps seed [shuffle_seed [pattern]]
 //   dtype 0 fp32, 1 bf16; ks comma-separated; chunk 0 takes plan()'s (min_chunk max 16k for k > 64, as the
@@ -21,6 +22,13 @@
 extern "C" long long plan(long long rows, long long cols, int dtype, int threads, int depth, int min_chunk);
 extern "C" int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
                       long long cols, int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream);
+extern "C" int topk_launch_sample(const void* x, void* values, void* indices, void* work, void* counters,
+                                  long long rows, long long cols, int k, int dtype, int threads, int depth,
+                                  long long chunk, const float* uniforms, void* out, float temperature, float top_p,
+                                  hipStream_t stream);
+extern "C" int topk_sample_launch(const void* values, const void* indices, const float* uniforms, void* out,
+                                  long long rows, int k, int dtype, float temperature, float top_p,
+                                  hipStream_t stream);
 extern "C" void oracle_topk(const void* x, void* values, int64_t* indices, long long rows, long long cols, int k,
                             int dtype);
 
@@ -79,6 +87,9 @@ int main(int argc, char** argv) {
   void* x = nullptr;
   if (hipMalloc(&x, n * esz) != hipSuccess) return 3;
   std::memcpy(x, host.data(), n * esz);
+  float* uni = nullptr;
+  hipMalloc((void**)&uni, rows * 4);
+  for (long long r = 0; r < rows; ++r) uni[r] = (float)((r * 37 + 11) % 100) / 100.0f;
   int bad = 0;
   for (int k : ks) {
     if (k > cols) continue;
@@ -107,6 +118,26 @@ int main(int argc, char** argv) {
       const bool ok_v = std::memcmp(vals, rv.data(), rows * k * esz) == 0;
       bool zero = true;
       for (long long i = 0; i < rows; ++i) zero &= ((unsigned*)cnt)[i] == 0;
+      // the fused draw: the same list, and the draw of topk_sample_launch() on it
+      void *vals2, *idx2, *drawn1, *drawn2;
+      hipMalloc(&vals2, rows * k * esz);
+      hipMalloc(&idx2, rows * k * 8);
+      hipMalloc(&drawn1, rows * 8);
+      hipMalloc(&drawn2, rows * 8);
+      const float temperature = rep % 2 ? 0.0f : 0.8f, top_p = 0.9f;
+      const int err2 = topk_launch_sample(x, vals2, idx2, work, cnt, rows, cols, k, dtype, 256, 4, chunk, uni,
+                                          drawn2, temperature, top_p, nullptr);
+      const int err3 = topk_sample_launch(vals, idx, uni, drawn1, rows, k, dtype, temperature, top_p, nullptr);
+      const bool fused_ok = !err2 && !err3 && std::memcmp(vals2, vals, rows * k * esz) == 0 &&
+                            std::memcmp(idx2, idx, rows * k * 8) == 0 && std::memcmp(drawn1, drawn2, rows * 8) == 0;
+      hipFree(vals2);
+      hipFree(idx2);
+      hipFree(drawn1);
+      hipFree(drawn2);
+      if (!fused_ok) {
+        ++bad;
+        std::printf("k=%d chunk=%lld rep %d: fused draw differs (errors %d %d)\n", k, chunk, rep, err2, err3);
+      }
       if (!ok_i || !ok_v || !zero) {
         ++bad;
         long long first = -1;
@@ -124,6 +155,7 @@ int main(int argc, char** argv) {
     hipFree(cnt);
   }
   hipFree(x);
+  hipFree(uni);
   std::printf(bad ? "FAILED %d\n" : "ALL OK\n", bad);
   return bad ? 1 : 0;
 }

@@ -5,7 +5,7 @@ Covers single- and multi-chunk rows (the merge by the row's last workgroup to ar
 arrival counters), every k class (1, the lane-maxima bound up to 64, the general path up to 1024), ties and special
 values, negative rows and the all-ones NaN (the value the k <= 64 kernel pads tiles with), bf16, unaligned and ragged
 rows, short last tiles, workspace reuse, the arrival counters' growth, reset and self-reset, adversarial orders that
-force many prunes, and the top-k workload at k = 1, 50 and 1024.
+force many prunes, the top-k workload at k = 1, 50 and 1024, and the draw fused into the launch.
 """
 
 import numpy as np
@@ -252,3 +252,41 @@ def test_sample_after_topk_config(pkg, oracle, dev):
     rv, ri = oracle.topk(x.numpy(), k)
     ref, amb = oracle.topk_sample(rv, ri, inp["uniforms"].numpy(), inp["temperature"], inp["top_p"])
     assert np.array_equal(got[~amb], ref[~amb]) and amb.mean() < 0.1
+
+
+@pytest.mark.parametrize("k", [1, 2, 50, 64, 65, 300, 1024])
+def test_launch_sample_equals_two_steps(pkg, dev, k):
+    """topk_launch_sample (the draw fused into the top-k launch) against launch() then topk_sample_launch(): values,
+    indices and the drawn indices bit for bit, for split and unsplit rows, both dtypes, and greedy, nucleus and full
+    draws."""
+    cand = pkg.candidate("topk")
+    g = torch.Generator().manual_seed(1000 + k)
+    for rows, cols in [(5, 30000), (3, 1500)]:
+        if k > cols:
+            continue
+        for dt in (torch.float32, torch.bfloat16):
+            x = (torch.randn(rows, cols, generator=g) * 2).to(dt).to(dev)
+            u = torch.rand(rows, generator=g).to(dev)
+            for temperature, top_p in [(0.8, 0.9), (0.0, 1.0), (1.3, 1.0)]:
+                print(f"[topk] fused draw {rows}x{cols} {dt} k={k} T={temperature} p={top_p}", flush=True)
+                v2, i2, d2 = cand.run_and_sample({"x": x, "k": k}, u, temperature, top_p)
+                out = cand.run({"x": x, "k": k})
+                d1 = cand.sample(out["values"], out["indices"], u, temperature, top_p)
+                torch.cuda.synchronize()
+                assert torch.equal(i2, out["indices"]) and torch.equal(v2.view(-1), out["values"].view(-1))
+                assert torch.equal(d2, d1), (d2.tolist(), d1.tolist())
+
+
+def test_launch_sample_rejects_missing_buffers(pkg, dev):
+    L = lib(pkg)
+    x = torch.randn(2, 1000, device=dev)
+    vals = torch.empty(2, 5, device=dev)
+    idx = torch.empty(2, 5, dtype=torch.int64, device=dev)
+    u = torch.rand(2, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    work = torch.empty(1, dtype=torch.int64, device=dev)
+    cnt = torch.zeros(2, dtype=torch.int32, device=dev)
+    assert L.topk_launch_sample(x.data_ptr(), vals.data_ptr(), idx.data_ptr(), work.data_ptr(), cnt.data_ptr(), 2,
+                                1000, 5, 0, 256, 4, 1000, None, idx.data_ptr(), 1.0, 1.0, s) == -1
+    assert L.topk_launch_sample(x.data_ptr(), vals.data_ptr(), idx.data_ptr(), work.data_ptr(), cnt.data_ptr(), 2,
+                                1000, 5, 0, 256, 4, 1000, u.data_ptr(), None, 1.0, 1.0, s) == -1
