@@ -1,0 +1,110 @@
+// Runs csrc/softmax.hip's launch() under the CPU emulation (hip/hip_runtime.h beside this file) and compares the
+// output with the oracle (oracle/oracle.c: oracle_softmax, the fp64 softmax rounded once) within the softmax
+// tolerance: fp32 |y - oracle| <= 1e-5 |oracle| (one ulp for subnormal results), bf16 within 1 ulp (NaN must meet
+// NaN). Every device buffer lies between guard pages. The co-resident tier is not run: its workgroups wait for one
+// another, and the emulation runs workgroups one after another.
+//
+// usage: emu_softmax rows cols dtype(0 fp32, 1 bf16) tier seed [waves nv [offset [pattern]]]
+//   tier: 1 row, 2 split, 3 generic (forced through softmax_tune); waves / nv: the row tier's (tier 1) or the split
+//   tier's (tier 2) shape, 0 automatic; offset shifts x and y by that many elements from a 16-byte boundary (a
+//   misaligned row takes the generic tier); pattern: randn (N(0, 4)) or special (-inf elements, an all -inf row, a
+//   row of one huge value).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <random>
+#include <string>
+#include <vector>
+
+extern "C" int launch(const void* x, void* y, long long rows, long long cols, int dtype, int threads, int aux,
+                      hipStream_t stream);
+extern "C" int softmax_tune(int slot, int value);
+extern "C" void oracle_softmax(const void* x, void* y, long long rows, long long cols, int dtype);
+
+static uint16_t bf16_rne(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+static int ordered(uint16_t b) { return b & 0x8000 ? 0x8000 - (int)b : (int)b; }
+static bool nan16(uint16_t b) { return (b & 0x7f80) == 0x7f80 && (b & 0x7f); }
+
+int main(int argc, char** argv) {
+  if (argc < 6) {
+    std::fprintf(stderr, "usage: rows cols dtype tier seed [waves nv [offset [pattern]]]\n");
+    return 2;
+  }
+  const long long rows = atoll(argv[1]), cols = atoll(argv[2]);
+  const int dtype = atoi(argv[3]), tier = atoi(argv[4]), seed = atoi(argv[5]);
+  const int waves = argc > 6 ? atoi(argv[6]) : 0, nv = argc > 7 ? atoi(argv[7]) : 0;
+  const int offset = argc > 8 ? atoi(argv[8]) : 0;
+  const std::string pattern = argc > 9 ? argv[9] : "randn";
+  softmax_tune(5, tier);
+  softmax_tune(tier == 2 ? 3 : 0, waves);
+  softmax_tune(tier == 2 ? 4 : 1, nv);
+  const size_t esz = dtype == 0 ? 4 : 2, n = (size_t)rows * cols;
+  std::mt19937_64 g(seed);
+  std::normal_distribution<float> nd(0.0f, 4.0f);
+  std::vector<float> f(n);
+  for (size_t i = 0; i < n; ++i) {
+    const long long r = (long long)(i / cols), c = (long long)(i % cols);
+    f[i] = nd(g);
+    if (pattern == "special") {
+      if (r % 4 == 0 && c % 5 == 1) f[i] = -INFINITY;
+      if (r % 4 == 1) f[i] = -INFINITY;
+      if (r % 4 == 2 && c == cols / 2) f[i] = 80.0f;
+    } else if (pattern != "randn") {
+      std::fprintf(stderr, "unknown pattern %s\n", pattern.c_str());
+      return 2;
+    }
+  }
+  std::vector<char> host(n * esz);
+  for (size_t i = 0; i < n; ++i) {
+    if (dtype == 0) std::memcpy(&host[i * 4], &f[i], 4);
+    else {
+      const uint16_t b = bf16_rne(f[i]);
+      std::memcpy(&host[i * 2], &b, 2);
+    }
+  }
+  char *xb, *yb;
+  hipMalloc((void**)&xb, (n + offset) * esz);
+  hipMalloc((void**)&yb, (n + offset) * esz);
+  char* x = xb + offset * esz;
+  char* y = yb + offset * esz;
+  std::memcpy(x, host.data(), n * esz);
+  std::vector<char> ref(n * esz);
+  oracle_softmax(host.data(), ref.data(), rows, cols, dtype);
+  const int err = launch(x, y, rows, cols, dtype, 256, 0, nullptr);
+  long long bad = 0, first = -1;
+  for (size_t i = 0; i < n && !err; ++i) {
+    bool ok;
+    if (dtype == 0) {
+      float a, b;
+      std::memcpy(&a, y + i * 4, 4);
+      std::memcpy(&b, &ref[i * 4], 4);
+      // below the normal range one ulp (2^-149) is more than 1e-5 of the value: one ulp is allowed there
+      const double tol = std::fmax(1e-5 * std::fabs((double)b), 0x1p-149);
+      ok = std::isnan(b) ? std::isnan(a) : std::fabs((double)a - b) <= tol;
+    } else {
+      uint16_t a, b;
+      std::memcpy(&a, y + i * 2, 2);
+      std::memcpy(&b, &ref[i * 2], 2);
+      ok = nan16(b) ? nan16(a) : !nan16(a) && std::abs(ordered(a) - ordered(b)) <= 1;
+    }
+    if (!ok && first < 0) first = (long long)i;
+    bad += !ok;
+  }
+  const bool input_kept = std::memcmp(x, host.data(), n * esz) == 0;
+  const bool ok = !err && !bad && input_kept;
+  std::printf("rows %lld cols %lld dtype %d tier %d: %s (err %d, %lld outside tolerance, first %lld, input kept %d)\n",
+              rows, cols, dtype, tier, ok ? "ALL OK" : "FAILED", err, bad, first, input_kept);
+  hipFree(xb);
+  hipFree(yb);
+  return ok ? 0 : 1;
+}

@@ -38,6 +38,11 @@ enum { hipSuccess = 0, hipErrorInvalidValue = 1 };
 typedef struct ihipStream_t* hipStream_t;
 enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 1 };
 
+struct float2 {
+  float x, y;
+};
+inline float2 make_float2(float a, float b) { return float2{a, b}; }
+
 struct dim3 {
   unsigned x, y, z;
   dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
@@ -336,6 +341,8 @@ inline void guarded_free(void* p) {
 
 #define threadIdx (emu::tid())
 #define blockIdx (emu::S().block_idx)
+#define gridDim (emu::S().grid)
+#define blockDim (emu::S().block)
 #define __syncthreads() emu::block_sync(__LINE__)
 #define __ballot(p) emu::ballot((p), __LINE__)
 #define __builtin_amdgcn_readlane(v, l) emu::readlane((int)(v), (int)(l), __LINE__)
@@ -345,6 +352,7 @@ inline void guarded_free(void* p) {
 #define __builtin_amdgcn_mbcnt_lo(m, c) emu::mbcnt_lo((unsigned)(m), (unsigned)(c))
 #define __builtin_amdgcn_mbcnt_hi(m, c) emu::mbcnt_hi((unsigned)(m), (unsigned)(c))
 #define __builtin_amdgcn_wave_barrier() emu::wave_sync(__LINE__)
+#define __builtin_amdgcn_s_sleep(n) ((void)0)
 #define __shfl_up(v, d, w) emu::shfl_up((v), (unsigned)(d), (int)(w), __LINE__)
 
 #define __HIP_MEMORY_SCOPE_AGENT 0

@@ -11,44 +11,15 @@ hardware's memory ordering between workgroups (they run one after another) and t
 """
 
 import os
-import shutil
-import subprocess
 
 import pytest
 
-HERE = os.path.dirname(os.path.abspath(__file__))
-ROOT = os.path.dirname(HERE)
-CSRC = os.path.join(ROOT, "cuda-kernels-optimized-for-rtx5090_amd", "csrc")
-EMU = os.path.join(HERE, "emu")
-
-
-def _clang():
-    for cand in ("/opt/rocm/llvm/bin/clang++", shutil.which("clang++")):
-        if cand and os.path.exists(cand):
-            return cand
-    return None
+from _emu import build, run
 
 
 @pytest.fixture(scope="module")
 def emu_topk(tmp_path_factory):
-    clang = _clang()
-    if clang is None or shutil.which("gcc") is None:
-        pytest.skip("clang++ (for the kernels' vector extensions on the host) or gcc is missing")
-    d = tmp_path_factory.mktemp("emu_topk")
-    # the source as the libraries build it, with its inline asm statements (scheduling fences and waits for the
-    # memory counters, which have no meaning here) turned into no-ops
-    with open(os.path.join(CSRC, "topk.hip")) as f:
-        src = f.read().replace("asm volatile(", "EMU_ASM(")
-    (d / "topk_emu.cpp").write_text(src)
-    subprocess.run(["gcc", "-O2", "-c", os.path.join(ROOT, "oracle", "oracle.c"), "-o", str(d / "oracle.o")],
-                   check=True)
-    exe = d / "emu_topk"
-    proc = subprocess.run([clang, "-std=c++17", "-O1", "-U_FORTIFY_SOURCE", "-D_FORTIFY_SOURCE=0",
-                           "-fno-strict-aliasing", "-w", "-I", EMU, "-I", CSRC, str(d / "topk_emu.cpp"),
-                           os.path.join(EMU, "emu_topk.cpp"), str(d / "oracle.o"), "-o", str(exe), "-lm"],
-                          capture_output=True, text=True)
-    assert proc.returncode == 0, proc.stderr[-4000:]
-    return str(exe)
+    return build(tmp_path_factory.mktemp("emu_topk"), "topk.hip", "emu_topk.cpp")
 
 
 ALL_K = "1,7,50,64,65,300,1024"
@@ -75,16 +46,11 @@ CASES = [
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_emulated_topk_matches_oracle(emu_topk, case):
-    args = [str(a) for a in case[1:]]
-    proc = subprocess.run([emu_topk, *args], capture_output=True, text=True, timeout=600)
-    out = proc.stdout + proc.stderr
-    assert proc.returncode == 0 and "ALL OK" in proc.stdout, f"{case[0]}: rc {proc.returncode}\n{out[-3000:]}"
+    run(emu_topk, case[1:])
 
 
 def test_emulated_topk_guard_below_start(emu_topk):
     # the same buffers placed flush against their lower guard page
     env = dict(os.environ, EMU_ALIGN_START="1")
     for case in (CASES[0], CASES[4], CASES[6]):
-        proc = subprocess.run([emu_topk, *[str(a) for a in case[1:]]], capture_output=True, text=True, timeout=600,
-                              env=env)
-        assert proc.returncode == 0 and "ALL OK" in proc.stdout, f"{case[0]}: {proc.stdout[-2000:]}{proc.stderr}"
+        run(emu_topk, case[1:], env=env)
