@@ -894,66 +894,64 @@ __device__ __forceinline__ void merge_lists(TileSmem& s, BlockRed& red, TileList
 // ---- sampling from the top k ---------------------------------------------------------------------------------------
 
 constexpr int kSamplePer = kMaxK / kWave;  // list entries per lane (k <= 1024)
+constexpr int kDppRowShr = 0x110;          // + n: row_shr:n, lane l reads lane l - n of its 16-lane row (0 below it)
 
 __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), lane));
 }
 
-// Inclusive prefix sum over the wave's lanes (lane order).
+// Inclusive prefix sum over the wave's lanes (lane order): a scan inside each 16-lane row by DPP row shifts, then the
+// sums of the rows below (read from lanes 15, 31 and 47) added.
 __device__ __forceinline__ float wave_prefix(float v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const float o = __shfl_up(v, d, kWave);
-    v += lane >= d ? o : 0.0f;
-  }
-  return v;
+  v += dpp<kDppRowShr + 1>(v);
+  v += dpp<kDppRowShr + 2>(v);
+  v += dpp<kDppRowShr + 4>(v);
+  v += dpp<kDppRowShr + 8>(v);
+  const float r0 = readlane_f(v, 15), r01 = r0 + readlane_f(v, 31), r012 = r01 + readlane_f(v, 47);
+  const int wrow = lane_id() >> 4;
+  return wrow == 0 ? v : v + (wrow == 1 ? r0 : wrow == 2 ? r01 : r012);
 }
 
-// The draw from row `row` of a top-k list (values [rows, k] in T, int64 indices, as topk writes them) by one wave
-// (every lane returns it): temperature, top-p and a draw with the caller's uniform u[row] in [0, 1). With x = value /
-// temperature, e_i = exp(x_i - max x) and S_i = e_0 + ... + e_i (list order), the draw keeps the entries i with S_(i-1)
-// < top_p * S_(k-1) (always the first; every entry when top_p >= 1), and picks the first kept i with S_i > u *
-// S_last_kept (the last kept if rounding leaves none). temperature <= 0 is greedy: position 0, the list's largest value
-// (lowest index among ties). Values must be finite when temperature > 0. Lane l holds positions [l E, l E + E), E =
-// ceil(k / 64).
-template <typename Value, typename Index>
-__device__ __forceinline__ long long sample_row(const Value& value_at, const Index& index_at, long long row, int k,
-                                                const float* u, float temperature, float top_p) {
+// The draw from a row of a top-k list by one wave (every lane returns it): temperature, top-p and a draw with the
+// caller's uniform u in [0, 1). With x = value / temperature, e_i = exp(x_i - max x) and S_i = e_0 + ... + e_i (list
+// order), the draw keeps the entries i with S_(i-1) < top_p * S_(k-1) (always the first; every entry when top_p >= 1),
+// and picks the first kept i with S_i > u * S_last_kept (the last kept if rounding leaves none). temperature <= 0 is
+// greedy: position 0, the list's largest value (lowest index among ties). Values must be finite when temperature > 0.
+// Lane l holds positions [l E, l E + E), E = ceil(k / 64) <= PER: the result does not depend on PER.
+template <int PER, typename Value, typename Index>
+__device__ __forceinline__ long long sample_row(const Value& value_at, const Index& index_at, int k, float u,
+                                                float temperature, float top_p) {
   const int lane = lane_id();
-  const int per = (k + kWave - 1) / kWave;
+  const int per = PER == 1 ? 1 : (k + kWave - 1) / kWave;
   const int base = lane * per;
-  float x[kSamplePer];
-#pragma unroll
-  for (int e = 0; e < kSamplePer; ++e) {
-    const int i = base + e;
-    x[e] = e < per && i < k ? value_at(i) : -INFINITY;
-  }
   int chosen;
   if (temperature <= 0.0f) {
     chosen = 0;  // greedy: the list's first entry, its largest value (lowest position among ties)
   } else {
+    float x[PER];
     float m = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < kSamplePer; ++e) {
-      x[e] = x[e] / temperature;
+    for (int e = 0; e < PER; ++e) {
+      const int i = base + e;
+      x[e] = e < per && i < k ? value_at(i) / temperature : -INFINITY;
       m = fmaxf(m, x[e]);
     }
     m = wave_max(m);
     float run = 0.0f;
 #pragma unroll
-    for (int e = 0; e < kSamplePer; ++e) {
+    for (int e = 0; e < PER; ++e) {
       const float ex = (e < per && base + e < k) ? expf(x[e] - m) : 0.0f;
       run += ex;
       x[e] = run;  // lane-local inclusive sums
     }
-    const float lane_excl = wave_prefix(run) - run;
-    const float total = readlane_f(wave_prefix(run), kWave - 1);
+    const float incl = wave_prefix(run);
+    const float lane_excl = incl - run;
+    const float total = readlane_f(incl, kWave - 1);
     const float cut = top_p * total;
     // kept: positions whose exclusive sum is below the cut (a prefix of the list; at least position 0)
     int keep = 0;
 #pragma unroll
-    for (int e = 0; e < kSamplePer; ++e) {
+    for (int e = 0; e < PER; ++e) {
       const float excl = lane_excl + (e ? x[e - 1] : 0.0f);
       keep += (e < per && base + e < k && (base + e == 0 || top_p >= 1.0f || excl < cut)) ? 1 : 0;
     }
@@ -961,13 +959,13 @@ __device__ __forceinline__ long long sample_row(const Value& value_at, const Ind
     // the kept mass is the inclusive sum at position kept - 1
     float mass = 0.0f;
 #pragma unroll
-    for (int e = 0; e < kSamplePer; ++e)
+    for (int e = 0; e < PER; ++e)
       if (e < per && base + e == kept - 1) mass = lane_excl + x[e];
     mass = wave_max(mass);
-    const float target = u[row] * mass;
+    const float target = u * mass;
     int first = kept - 1;
 #pragma unroll
-    for (int e = 0; e < kSamplePer; ++e) {
+    for (int e = 0; e < PER; ++e) {
       const int i = base + e;
       if (e < per && i < kept && lane_excl + x[e] > target && i < first) first = i;
     }
@@ -997,31 +995,33 @@ struct SampleArgs {
   long long* out;
   float temperature;
   float top_p;
+  // the row's uniform, loaded by the workgroup that will draw well before its draw (0 without a draw)
+  __device__ __forceinline__ float uniform(long long row) const { return out ? u[row] : 0.0f; }
 };
 
-// The fused draw of a row whose list this workgroup's waves have just written: every thread calls it (the barrier
-// makes the list visible to the first wave, which draws).
+// The fused draw of a row of k > 64 whose list this workgroup's waves have just written: every thread calls it (the
+// barrier makes the list visible to the first wave, which draws). u is the row's uniform.
 template <typename T>
-__device__ __forceinline__ void sample_list(const SampleArgs& sa, const void* values, const long long* indices,
-                                            long long row, int k) {
+__device__ __forceinline__ void sample_list(const SampleArgs& sa, float u, const void* values,
+                                            const long long* indices, long long row, int k) {
   if (!sa.out) return;
   __syncthreads();
   if (wave_id() != 0) return;
   const ListInMemory<T> list{values, indices, row, k};
   const long long drawn =
-      sample_row(list, [&](int i) { return list.index(i); }, row, k, sa.u, sa.temperature, sa.top_p);
+      sample_row<kSamplePer>(list, [&](int i) { return list.index(i); }, k, u, sa.temperature, sa.top_p);
   if (lane_id() == 0) sa.out[row] = drawn;
 }
 
-// sample_list for a row whose composites finish_list also left in order in top[] (LDS): the values are decoded from
-// the composites (the bits written to the output), so the draw equals the one from memory.
-__device__ __forceinline__ void sample_top(const SampleArgs& sa, const u64* top, long long row, int k) {
+// The fused draw of a row of k <= 64 whose composites finish_list also left in order in top[] (LDS): the values are
+// decoded from the composites (the bits written to the output), so the draw equals the one from memory.
+__device__ __forceinline__ void sample_top(const SampleArgs& sa, float u, const u64* top, long long row, int k) {
   if (!sa.out) return;
   __syncthreads();
   if (wave_id() != 0) return;
-  const long long drawn = sample_row([&](int i) { return __uint_as_float(composite_bits(top[i])); },
-                                     [&](int i) { return composite_index(top[i]); }, row, k, sa.u, sa.temperature,
-                                     sa.top_p);
+  const long long drawn = sample_row<1>([&](int i) { return __uint_as_float(composite_bits(top[i])); },
+                                        [&](int i) { return composite_index(top[i]); }, k, u, sa.temperature,
+                                        sa.top_p);
   if (lane_id() == 0) sa.out[row] = drawn;
 }
 
@@ -1092,8 +1092,9 @@ __global__ void __launch_bounds__(kThreads)
     process(tile, end - t0 > TE);
   }
   if (nchunks == 1) {
+    const float u = sa.uniform(row);
     finish_list<T>(s, L, values, indices, nullptr, row, k, true);
-    sample_top(sa, s.top, row, k);
+    sample_top(sa, u, s.top, row, k);
     return;
   }
   if (k == 1) {
@@ -1139,11 +1140,12 @@ __global__ void __launch_bounds__(kThreads)
   }
   __syncthreads();
   if (!s.last) return;
+  const float u = sa.uniform(row);
   L.cnt = 0;
   merge_lists<T>(s, red, L, values, indices, wr, row, nchunks, k);
   if (threadIdx.x == 0)
     __hip_atomic_store(arrivals + row * kArrivalStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  sample_top(sa, s.top, row, k);
+  sample_top(sa, u, s.top, row, k);
 }
 
 // ---- wide kernel (64 < k <= 1024) ----------------------------------------------------------------------------------
@@ -1390,9 +1392,10 @@ __global__ void __launch_bounds__(kThreads)
     }
   }
   if (nchunks == 1) {
+    const float u = sa.uniform(row);
     if (s.count > kWideList) prune(s, k);
     write_ranked<T>(s, s.count, k, values, indices, row, 0ull);
-    sample_list<T>(sa, values, indices, row, k);
+    sample_list<T>(sa, u, values, indices, row, k);
     return;
   }
   if (s.count > kWideList) prune(s, k);
@@ -1417,6 +1420,7 @@ __global__ void __launch_bounds__(kThreads)
   }
   __syncthreads();
   if (!s.last) return;
+  const float u = sa.uniform(row);
   // merge (the row's last arrival): the floor from the headers, then every list's candidates at or above it
   auto ld = [&](long long at) { return __hip_atomic_load(wr + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   u64 kmax = 0, qmn = ~0ull;
@@ -1475,7 +1479,7 @@ __global__ void __launch_bounds__(kThreads)
   write_ranked<T>(s, s.count, k, values, indices, row, floor);  // every candidate kept is at or above the floor
   if (threadIdx.x == 0)
     __hip_atomic_store(arrivals + row * kArrivalStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  sample_list<T>(sa, values, indices, row, k);
+  sample_list<T>(sa, u, values, indices, row, k);
 }
 
 // One wave per row of a top-k list (values [rows, k] in T, int64 indices, as topk writes them): out[row] drawn by
@@ -1486,7 +1490,9 @@ __global__ void __launch_bounds__(kWave)
                 long long* __restrict__ out, int k, float temperature, float top_p) {
   const long long row = blockIdx.x;
   const ListInMemory<T> list{values, indices, row, k};
-  const long long drawn = sample_row(list, [&](int i) { return list.index(i); }, row, k, u, temperature, top_p);
+  const auto index_at = [&](int i) { return list.index(i); };
+  const long long drawn = k <= kWave ? sample_row<1>(list, index_at, k, u[row], temperature, top_p)
+                                     : sample_row<kSamplePer>(list, index_at, k, u[row], temperature, top_p);
   if (lane_id() == 0) out[row] = drawn;
 }
 

@@ -103,9 +103,9 @@ def algorithmic_bytes(name, k=50):
     if name == "rope_4x4096_32q_8kv_128":
         return 2 * (4 * 4096 * 32 * 128 + 4 * 4096 * 8 * 128) * 2 + 4 * 4096 * 8
     if name == "topk_sample_128x128256":
-        # the logits read once, the uniforms read, the drawn int64 indices written (the top-k list stays on chip
-        # between the two kernels' L2 and is not counted)
-        return 128 * 128256 * 4 + 128 * 4 + 128 * 8
+        # the logits read once, the uniforms read, the top-k list (fp32 values, int64 indices) and the drawn int64
+        # indices written; the draw reads the list from the launch's own LDS or L2, not from HBM
+        return 128 * 128256 * 4 + 128 * 4 + 128 * 50 * (4 + 8) + 128 * 8
     if name == "topk_128x128256":
         return 128 * 128256 * 4 + 128 * k * (4 + 8)
     raise KeyError(name)

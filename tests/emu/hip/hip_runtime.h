@@ -168,7 +168,9 @@ inline int readfirstlane(int v, int line) {
   wave_sync(line);
   return r;
 }
+// the lane that lane l reads under DPP control ctrl, or -1 where the source is out of range
 inline int dpp_src(int l, int ctrl, int line) {
+  if (ctrl > 0x110 && ctrl < 0x120) return (l & 15) >= ctrl - 0x110 ? l - (ctrl - 0x110) : -1;  // row_shr:n
   switch (ctrl) {
     case 0xB1: return l ^ 1;
     case 0x4E: return l ^ 2;
@@ -178,10 +180,10 @@ inline int dpp_src(int l, int ctrl, int line) {
   }
 }
 inline int update_dpp(int old, int src, int ctrl, int rm, int bm, bool bc, int line) {
-  (void)old;
-  (void)bc;
   if (rm != 0xF || bm != 0xF) fail("dpp masks", line);
-  return (int)(uint32_t)read_from((uint32_t)src, dpp_src(lid(), ctrl, line), line);
+  const int from = dpp_src(lid(), ctrl, line);
+  const int r = (int)(uint32_t)read_from((uint32_t)src, from < 0 ? lid() : from, line);
+  return from < 0 ? (bc ? 0 : old) : r;  // an out-of-range source writes 0 (bound_ctrl) or keeps old
 }
 inline unsigned mbcnt_lo(unsigned m, unsigned c) {
   const int l = lid();
