@@ -41,6 +41,7 @@ CASES = [
     ("k_equals_cols", 2, 1024, 0, "1024", 0, 2048, 1, 14, -1, "randn"),
     ("shuffled", 2, 20000, 0, ALL_K, 4096, 2048, 2, 15, 99, "randn"),
     ("shuffled_bf16", 2, 20000, 1, "1,50,1024", 2052, 2048, 2, 16, 7, "ints"),
+    ("many_chunks_wide", 2, 100000, 0, "65", 1024, 2048, 1, 17, -1, "randn"),
 ]
 
 
