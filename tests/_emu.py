@@ -40,14 +40,19 @@ def build(tmpdir, source, driver):
         subprocess.run(["gcc", "-O2", "-c", os.path.join(ROOT, "oracle", "oracle.c"), "-o", obj], check=True)
     exe = os.path.join(str(tmpdir), "emu_" + stem)
     proc = subprocess.run([clang, "-std=c++17", "-O1", "-U_FORTIFY_SOURCE", "-D_FORTIFY_SOURCE=0",
-                           "-fno-strict-aliasing", "-w", "-I", EMU, "-I", CSRC, kern, os.path.join(EMU, driver), obj,
-                           "-o", exe, "-lm"], capture_output=True, text=True)
+                           "-fno-strict-aliasing", "-w", "-pthread", "-I", EMU, "-I", CSRC, kern,
+                           os.path.join(EMU, driver), obj, "-o", exe, "-lm"], capture_output=True, text=True)
     assert proc.returncode == 0, proc.stderr[-4000:]
     return exe
 
 
-def run(exe, args, env=None, timeout=600):
-    """Runs the emulation with the given arguments and asserts that it reports ALL OK."""
+def run(exe, args, env=None, timeout=600, concurrent=False):
+    """Runs the emulation with the given arguments and asserts that it reports ALL OK. concurrent: every workgroup on an
+    OS thread of its own, all at once (EMU_CONCURRENT)."""
+    env = dict(os.environ if env is None else env)
+    env.pop("EMU_CONCURRENT", None)
+    if concurrent:
+        env["EMU_CONCURRENT"] = "1"
     proc = subprocess.run([exe, *[str(a) for a in args]], capture_output=True, text=True, timeout=timeout, env=env)
     out = proc.stdout + proc.stderr
     assert proc.returncode == 0 and "ALL OK" in proc.stdout, f"{args}: rc {proc.returncode}\n{out[-3000:]}"

@@ -1,14 +1,15 @@
 // Runs csrc/softmax.hip's launch() under the CPU emulation (hip/hip_runtime.h beside this file) and compares the
 // output with the oracle (oracle/oracle.c: oracle_softmax, the fp64 softmax rounded once) within the softmax
 // tolerance: fp32 |y - oracle| <= 1e-5 |oracle| (one ulp for subnormal results), bf16 within 1 ulp (NaN must meet
-// NaN). Every device buffer lies between guard pages. The co-resident tier is not run: its workgroups wait for one
-// another, and the emulation runs workgroups one after another.
+// NaN). Every device buffer lies between guard pages. The co-resident tier (4) needs EMU_CONCURRENT: its workgroups
+// wait for one another.
 //
-// usage: emu_softmax rows cols dtype(0 fp32, 1 bf16) tier seed [waves nv [offset [pattern]]]
-//   tier: 1 row, 2 split, 3 generic (forced through softmax_tune); waves / nv: the row tier's (tier 1) or the split
-//   tier's (tier 2) shape, 0 automatic; offset shifts x and y by that many elements from a 16-byte boundary (a
-//   misaligned row takes the generic tier); pattern: randn (N(0, 4)) or special (-inf elements, an all -inf row, a
-//   row of one huge value).
+// usage: emu_softmax rows cols dtype(0 fp32, 1 bf16) tier seed [waves nv [offset [pattern [reps]]]]
+//   tier: 1 row, 2 split, 3 generic, 4 co-resident (forced through softmax_tune); waves / nv: the row tier's (tier 1)
+//   or the split tier's (tier 2) shape, 0 automatic; offset shifts x and y by that many elements from a 16-byte
+//   boundary (a misaligned row takes the generic tier); pattern: randn (N(0, 4)) or special (-inf elements, an all
+//   -inf row, a row of one huge value); reps: launches on the same buffers, each checked (the co-resident tier's
+//   hand-off slots must be clear again for the next).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -45,6 +46,7 @@ int main(int argc, char** argv) {
   const int waves = argc > 6 ? atoi(argv[6]) : 0, nv = argc > 7 ? atoi(argv[7]) : 0;
   const int offset = argc > 8 ? atoi(argv[8]) : 0;
   const std::string pattern = argc > 9 ? argv[9] : "randn";
+  const int reps = argc > 10 ? atoi(argv[10]) : 1;
   softmax_tune(5, tier);
   softmax_tune(tier == 2 ? 3 : 0, waves);
   softmax_tune(tier == 2 ? 4 : 1, nv);
@@ -80,25 +82,29 @@ int main(int argc, char** argv) {
   std::memcpy(x, host.data(), n * esz);
   std::vector<char> ref(n * esz);
   oracle_softmax(host.data(), ref.data(), rows, cols, dtype);
-  const int err = launch(x, y, rows, cols, dtype, 256, 0, nullptr);
+  int err = 0;
   long long bad = 0, first = -1;
-  for (size_t i = 0; i < n && !err; ++i) {
-    bool ok;
-    if (dtype == 0) {
-      float a, b;
-      std::memcpy(&a, y + i * 4, 4);
-      std::memcpy(&b, &ref[i * 4], 4);
-      // below the normal range one ulp (2^-149) is more than 1e-5 of the value: one ulp is allowed there
-      const double tol = std::fmax(1e-5 * std::fabs((double)b), 0x1p-149);
-      ok = std::isnan(b) ? std::isnan(a) : std::fabs((double)a - b) <= tol;
-    } else {
-      uint16_t a, b;
-      std::memcpy(&a, y + i * 2, 2);
-      std::memcpy(&b, &ref[i * 2], 2);
-      ok = nan16(b) ? nan16(a) : !nan16(a) && std::abs(ordered(a) - ordered(b)) <= 1;
+  for (int rep = 0; rep < reps && !err && !bad; ++rep) {
+    std::memset(y, 0xA5, n * esz);
+    err = launch(x, y, rows, cols, dtype, 256, 0, nullptr);
+    for (size_t i = 0; i < n && !err; ++i) {
+      bool ok;
+      if (dtype == 0) {
+        float a, b;
+        std::memcpy(&a, y + i * 4, 4);
+        std::memcpy(&b, &ref[i * 4], 4);
+        // below the normal range one ulp (2^-149) is more than 1e-5 of the value: one ulp is allowed there
+        const double tol = std::fmax(1e-5 * std::fabs((double)b), 0x1p-149);
+        ok = std::isnan(b) ? std::isnan(a) : std::fabs((double)a - b) <= tol;
+      } else {
+        uint16_t a, b;
+        std::memcpy(&a, y + i * 2, 2);
+        std::memcpy(&b, &ref[i * 2], 2);
+        ok = nan16(b) ? nan16(a) : !nan16(a) && std::abs(ordered(a) - ordered(b)) <= 1;
+      }
+      if (!ok && first < 0) first = (long long)i;
+      bad += !ok;
     }
-    if (!ok && first < 0) first = (long long)i;
-    bad += !ok;
   }
   const bool input_kept = std::memcmp(x, host.data(), n * esz) == 0;
   const bool ok = !err && !bad && input_kept;

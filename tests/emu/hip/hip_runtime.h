@@ -5,11 +5,14 @@
 //    the wave's live lanes, and __syncthreads a barrier of the block's live threads; lanes that have returned take no
 //    part, as on the hardware. Lanes of one wave reaching a barrier from different source lines, or a schedule in
 //    which no fiber can run, abort with a report;
-//  - workgroups run one after another (shuffled on request), so __shared__ is a function-local static;
+//  - workgroups run one after another (shuffled on request), or, with EMU_CONCURRENT set, each on an OS thread of its
+//    own, all at once (as co-resident workgroups that wait for one another need); __shared__ is a function-local
+//    thread_local static, so each workgroup's thread has its own;
 //  - device buffers lie between PROT_NONE pages (flush against the upper one, or against the lower one with
 //    EMU_ALIGN_START set) and start filled with 0xA5, so an access outside a buffer faults at once;
-//  - the atomics are plain operations: fibers switch only at barriers.
+//  - the atomics are sequentially consistent operations (fibers of one workgroup switch only at barriers).
 #pragma once
+#include <sched.h>
 #include <setjmp.h>
 #include <sys/mman.h>
 #include <ucontext.h>
@@ -23,6 +26,7 @@
 #include <functional>
 #include <map>
 #include <random>
+#include <thread>
 #include <vector>
 
 #define __global__
@@ -30,7 +34,7 @@
 #define __host__
 #define __forceinline__ inline
 #define __launch_bounds__(...)
-#define __shared__ static
+#define __shared__ static thread_local
 #define EMU_ASM(...) ((void)0)
 
 typedef int hipError_t;
@@ -87,9 +91,15 @@ struct State {
   int shuffle_seed = -1;
   std::mt19937 rng{1};
 };
+// The calling OS thread's state (a workgroup's thread in concurrent mode takes one from a pool).
+inline State*& tls_state() {
+  static thread_local State* p = nullptr;
+  return p;
+}
 inline State& S() {
-  static State* s = new State;
-  return *s;
+  State*& p = tls_state();
+  if (!p) p = new State;
+  return *p;
 }
 
 inline const Idx& tid() { return S().cur->tid; }
@@ -290,6 +300,8 @@ inline void run_block() {
   s.cur = nullptr;
 }
 
+inline bool concurrent() { return std::getenv("EMU_CONCURRENT") != nullptr; }
+
 inline void launch(dim3 grid, dim3 block, std::function<void()> body) {
   State& s = S();
   if (block.y != 1 || block.z != 1 || block.x > (unsigned)kMaxThreads) fail("block shape", 0);
@@ -302,10 +314,32 @@ inline void launch(dim3 grid, dim3 block, std::function<void()> body) {
     for (unsigned y = 0; y < grid.y; ++y)
       for (unsigned x = 0; x < grid.x; ++x) blocks.push_back(Idx{x, y, z});
   if (s.shuffle_seed >= 0) std::shuffle(blocks.begin(), blocks.end(), s.rng);
-  for (const Idx& b : blocks) {
-    s.block_idx = b;
-    run_block();
+  if (!concurrent()) {
+    for (const Idx& b : blocks) {
+      s.block_idx = b;
+      run_block();
+    }
+    return;
   }
+  // every workgroup on its own thread, with a state from the pool (kept for the next launch)
+  static std::vector<State*> pool;
+  while (pool.size() < blocks.size()) pool.push_back(new State);
+  std::vector<std::thread> threads;
+  for (size_t j = 0; j < blocks.size(); ++j) {
+    State* w = pool[j];
+    w->grid = grid;
+    w->block = block;
+    w->n = s.n;
+    w->body = s.body;
+    w->block_idx = blocks[j];
+    w->shuffle_seed = s.shuffle_seed;
+    if (s.shuffle_seed >= 0) w->rng.seed((unsigned)(s.shuffle_seed * 7919 + j));
+    threads.emplace_back([w] {
+      tls_state() = w;
+      run_block();
+    });
+  }
+  for (std::thread& t : threads) t.join();
 }
 
 // Device buffers end at a PROT_NONE page (an access past the end faults at once) and start after one; contents start
@@ -354,23 +388,22 @@ inline void guarded_free(void* p) {
 #define __builtin_amdgcn_mbcnt_lo(m, c) emu::mbcnt_lo((unsigned)(m), (unsigned)(c))
 #define __builtin_amdgcn_mbcnt_hi(m, c) emu::mbcnt_hi((unsigned)(m), (unsigned)(c))
 #define __builtin_amdgcn_wave_barrier() emu::wave_sync(__LINE__)
-#define __builtin_amdgcn_s_sleep(n) ((void)0)
+#define __builtin_amdgcn_s_sleep(n) (emu::concurrent() ? (void)sched_yield() : (void)0)
 #define __shfl_up(v, d, w) emu::shfl_up((v), (unsigned)(d), (int)(w), __LINE__)
 
 #define __HIP_MEMORY_SCOPE_AGENT 0
-#define __hip_atomic_load(p, o, sc) (*(p))
-#define __hip_atomic_store(p, v, o, sc) (void)(*(p) = (v))
+#define __hip_atomic_load(p, o, sc) __atomic_load_n((p), __ATOMIC_SEQ_CST)
+#define __hip_atomic_store(p, v, o, sc) __atomic_store_n((p), (v), __ATOMIC_SEQ_CST)
 template <typename T, typename U>
 inline T emu_fetch_add(T* p, U v) {
-  T old = *p;
-  *p = old + (T)v;
-  return old;
+  return __atomic_fetch_add(p, (T)v, __ATOMIC_SEQ_CST);
 }
 #define __hip_atomic_fetch_add(p, v, o, sc) emu_fetch_add((p), (v))
 template <typename T, typename U>
 inline T emu_fetch_max(T* p, U v) {
-  T old = *p;
-  if ((T)v > old) *p = (T)v;
+  T old = __atomic_load_n(p, __ATOMIC_SEQ_CST);
+  while ((T)v > old && !__atomic_compare_exchange_n(p, &old, (T)v, false, __ATOMIC_SEQ_CST, __ATOMIC_SEQ_CST)) {
+  }
   return old;
 }
 #define __hip_atomic_fetch_max(p, v, o, sc) emu_fetch_max((p), (v))

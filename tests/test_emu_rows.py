@@ -6,8 +6,9 @@ RMSNorm and RoPE bit for bit, softmax within its tolerance (fp32 rtol 1e-5, one 
 Every device buffer lies between guard pages, so a read or write past either end of an input, output or cache ends
 the run with a fault. The cases force each tier and register shape through the libraries' tuning slots, and cover
 ragged rows and tails, misaligned buffers (the scalar paths), in-place forms, -inf and all -inf rows, RoPE's head
-sizes down to 24 and its fused KV-cache write with skipped (-1) slots. The softmax co-resident tier is not run: its
-workgroups wait for one another, and the emulation runs workgroups one after another.
+sizes down to 24 and its fused KV-cache write with skipped (-1) slots. The softmax co-resident tier, whose
+workgroups wait for one another, runs with every workgroup on an OS thread of its own, over repeated launches (its
+hand-off slots must be clear again for the next).
 """
 
 import pytest
@@ -53,6 +54,15 @@ SOFTMAX = [
     ("generic_special", 8, 999, 1, 3, 12, 0, 0, 0, "special"),
 ]
 
+# the co-resident tier (its workgroups wait for one another: run concurrently), with repeated launches on the same
+# buffers: rows, cols, dtype, seed, pattern, reps
+COOP = [
+    ("coop_fp32", 2, 70000, 0, 3, "randn", 3),
+    ("coop_bf16", 3, 100000, 1, 4, "randn", 2),
+    ("coop_special", 4, 40000, 0, 5, "special", 2),
+    ("coop_one_chunk_bf16", 2, 16384, 1, 6, "randn", 2),
+]
+
 # rows, cols, dtype (1 bf16, 2 fp16), mode (0 launch, 1 weighted, 2 add, 3 add in place), seed, waves, nv,
 # blocks per CU, offset
 RMSNORM = [
@@ -89,6 +99,12 @@ ROPE = [
 @pytest.mark.parametrize("case", SOFTMAX, ids=[c[0] for c in SOFTMAX])
 def test_emulated_softmax_matches_oracle(emu_softmax, case):
     run(emu_softmax, case[1:])
+
+
+@pytest.mark.parametrize("case", COOP, ids=[c[0] for c in COOP])
+def test_emulated_softmax_coresident_tier(emu_softmax, case):
+    rows, cols, dtype, seed, pattern, reps = case[1:]
+    run(emu_softmax, [rows, cols, dtype, 4, seed, 0, 0, 0, pattern, reps], concurrent=True)
 
 
 @pytest.mark.parametrize("case", RMSNORM, ids=[c[0] for c in RMSNORM])

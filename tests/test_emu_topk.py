@@ -6,8 +6,10 @@ live lanes. Every buffer the kernels touch (input, outputs, work, counters and t
 workspaces) lies between guard pages, so an out-of-bounds access ends the run with a fault. The cases cover
 single- and split-chunk rows, every k class (1, the lane-maxima bound up to 64, the wide path up to 1024), short last
 tiles, ties, monotone and all-negative rows, the all-ones NaN, repeated launches on the same buffers (the arrival
-counters' self-reset), and shuffled workgroup and lane schedules. What the emulation does not model is the
-hardware's memory ordering between workgroups (they run one after another) and the compiler's gfx950 code.
+counters' self-reset), and shuffled workgroup and lane schedules. The concurrent cases run every workgroup of a launch
+on an OS thread of its own, so chunks publish and count their arrivals while the row's other chunks and merger run.
+What the emulation does not model is the hardware's memory ordering between workgroups (the host's is stronger) and
+the compiler's gfx950 code.
 """
 
 import os
@@ -48,6 +50,21 @@ CASES = [
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_emulated_topk_matches_oracle(emu_topk, case):
     run(emu_topk, case[1:])
+
+
+# rows, cols, dtype, ks, chunk, min_chunk, reps, seed, shuffle seed, pattern: split rows whose chunks hand their lists
+# to the row's last arrival while the other workgroups run
+CONCURRENT = [
+    ("c5_rows_fp32", 8, 128256, 0, "1,50,1024", 0, 16384, 3, 31, 5, "randn"),
+    ("split_bf16_ties", 4, 40000, 1, "1,13,64,65,300", 4096, 2048, 3, 32, 6, "ints"),
+    # 59 workgroups (their fiber stacks stay within the host's limit on memory mappings)
+    ("many_chunks", 1, 60000, 0, "7,65", 1024, 2048, 2, 33, -1, "randn"),
+]
+
+
+@pytest.mark.parametrize("case", CONCURRENT, ids=[c[0] for c in CONCURRENT])
+def test_emulated_topk_concurrent_workgroups(emu_topk, case):
+    run(emu_topk, case[1:], concurrent=True)
 
 
 def test_emulated_topk_guard_below_start(emu_topk):
