@@ -1163,11 +1163,12 @@ constexpr int kWideHead = 4;      // a published list's header: count, k-bound, 
 constexpr int kWideSlot = kWideHead + kWideList;
 constexpr int kWideMaxChunks = 256;
 
-constexpr int kRankBuckets = 2048;  // buckets of write_ranked
+constexpr int kRankBuckets = 4096;  // buckets of write_ranked (16-bit counters and first positions)
 
 // Writes the k largest of the m candidates s.buf[0, m) (k <= m <= kWideList), in order, as the output row: the
 // candidates are bucketed by their distance below the largest, (max - c) >> sh with sh chosen so that the range fills
-// kRankBuckets buckets, with LDS counters; an exclusive scan of the counts gives each bucket's first output position;
+// kRankBuckets buckets, with 16-bit LDS counters (two to a word, so that counters and first positions fit beside the
+// bucketed copy); an exclusive scan of the counts gives each bucket's first output position;
 // the candidates are scattered by bucket into LDS, and each one's position is its bucket's first plus the number of
 // its bucket's members above it. Nearly linear on spread-out values; a bucket holding many candidates (values
 // clustered far below an outlier) costs its size per member. `lo`, when not 0, is a lower bound of the candidates known
@@ -1178,8 +1179,9 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
                                              u64 lo) {
   constexpr int P = kWideList / kThreads;
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan
-  static_assert(kWideList * 2 <= kWideCap && kRankBuckets * 2 * sizeof(unsigned) <= kWideList * sizeof(u64),
-                "the bucketed copy and the counters share the buffer");
+  static_assert(kWideList * 2 <= kWideCap && kRankBuckets * 2 * sizeof(uint16_t) <= kWideList * sizeof(u64) &&
+                    kWideList < 65536 && BPT % 2 == 0,
+                "the bucketed copy, the counters and the first positions share the buffer; counts fit 16 bits");
   const int t = (int)threadIdx.x;
   u64 c[P];
   u64 mx = 0, mn = ~0ull;
@@ -1196,26 +1198,30 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   mn = lo ? lo : block_ext64<false>(mn, s);
   const u64 range = mx - mn;
   const int bits = range ? 64 - __clzll(range) : 0;
-  const int sh = bits > 11 ? bits - 11 : 0;
+  const int sh = bits > 12 ? bits - 12 : 0;  // (mx - mn) >> sh < 4096 = kRankBuckets
   u64* sorted = s.buf;
-  unsigned* cnt = reinterpret_cast<unsigned*>(s.buf + kWideList);
-  unsigned* first = cnt + kRankBuckets;
-  for (int b = t; b < kRankBuckets; b += kThreads) cnt[b] = 0;
+  unsigned* cnt2 = reinterpret_cast<unsigned*>(s.buf + kWideList);  // bucket b's count: half b & 1 of word b >> 1
+  uint16_t* first = reinterpret_cast<uint16_t*>(cnt2 + kRankBuckets / 2);
+  auto count_of = [&](int b) { return (int)((cnt2[b >> 1] >> (16 * (b & 1))) & 0xffffu); };
+  for (int w = t; w < kRankBuckets / 2; w += kThreads) cnt2[w] = 0;
   __syncthreads();
   int bk[P], slot[P];
 #pragma unroll
   for (int r = 0; r < P; ++r) {
     const u64 d = (mx - c[r]) >> sh;
     bk[r] = d < (u64)kRankBuckets ? (int)d : kRankBuckets - 1;
-    slot[r] = r * kThreads + t < m ? (int)atomicAdd(&cnt[bk[r]], 1u) : 0;
+    const int half = 16 * (bk[r] & 1);
+    slot[r] = r * kThreads + t < m ? (int)((atomicAdd(&cnt2[bk[r] >> 1], 1u << half) >> half) & 0xffffu) : 0;
   }
   __syncthreads();
   // exclusive scan of the counts, bucket 0 (the largest candidates) first
   unsigned own[BPT], sum = 0;
 #pragma unroll
-  for (int i = 0; i < BPT; ++i) {
-    own[i] = cnt[t * BPT + i];
-    sum += own[i];
+  for (int i = 0; i < BPT; i += 2) {
+    const unsigned w = cnt2[(t * BPT + i) >> 1];
+    own[i] = w & 0xffffu;
+    own[i + 1] = w >> 16;
+    sum += own[i] + own[i + 1];
   }
   unsigned incl = sum;
 #pragma unroll
@@ -1229,7 +1235,7 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   for (int w = 0; w < wave_id(); ++w) run += s.wsum[w];
 #pragma unroll
   for (int i = 0; i < BPT; ++i) {
-    first[t * BPT + i] = run;
+    first[t * BPT + i] = (uint16_t)run;
     run += own[i];
   }
   __syncthreads();
@@ -1239,24 +1245,34 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   __syncthreads();
   // Ranked in bucket order: lane i takes sorted[i], so neighbouring lanes read the same bucket's members (LDS
   // broadcasts rather than scattered reads) and write neighbouring output positions. Every position first, then the
-  // stores; bucket members four at a time (reads past a bucket stay inside the buffer: m + 3 <= kWideList + 3 <
-  // kWideCap).
-  int pos[P];
+  // stores. A thread's reads are issued together, stage by stage (its entries, their buckets' ranges, the buckets'
+  // first four members), with no branch between them: every index stays inside the buffer whether or not the entry
+  // exists (i < kWideList; f + 3 <= m + 3 < kWideCap), and a missing entry's position is discarded. Buckets of more
+  // than four members (rare) are finished after.
+  int pos[P], f[P], n[P];
 #pragma unroll
   for (int r = 0; r < P; ++r) {
-    const int i = r * kThreads + t;
-    pos[r] = k;
-    if (i < m) {
-      c[r] = sorted[i];
-      const u64 d = (mx - c[r]) >> sh;
-      const int b = d < (u64)kRankBuckets ? (int)d : kRankBuckets - 1;
-      const int f = (int)first[b], n = (int)cnt[b];
-      int q = f;
-      for (int j = 0; j < n; j += 4) {
-        const u64 a = sorted[f + j], e1 = sorted[f + j + 1], e2 = sorted[f + j + 2], e3 = sorted[f + j + 3];
-        q += (a > c[r]) + (j + 1 < n && e1 > c[r]) + (j + 2 < n && e2 > c[r]) + (j + 3 < n && e3 > c[r]);
-      }
-      pos[r] = q;
+    c[r] = sorted[r * kThreads + t];
+    const u64 d = (mx - c[r]) >> sh;
+    const int b = d < (u64)kRankBuckets ? (int)d : kRankBuckets - 1;
+    f[r] = (int)first[b];
+    n[r] = count_of(b);
+  }
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    const u64 a = sorted[f[r]], e1 = sorted[f[r] + 1], e2 = sorted[f[r] + 2], e3 = sorted[f[r] + 3];
+    pos[r] = f[r] + (a > c[r]) + (1 < n[r] && e1 > c[r]) + (2 < n[r] && e2 > c[r]) + (3 < n[r] && e3 > c[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    if (r * kThreads + t >= m) {
+      pos[r] = k;
+      continue;
+    }
+    for (int j = 4; j < n[r]; j += 4) {
+      const int g = f[r] + j;
+      const u64 a = sorted[g], e1 = sorted[g + 1], e2 = sorted[g + 2], e3 = sorted[g + 3];
+      pos[r] += (a > c[r]) + (j + 1 < n[r] && e1 > c[r]) + (j + 2 < n[r] && e2 > c[r]) + (j + 3 < n[r] && e3 > c[r]);
     }
   }
 #pragma unroll
