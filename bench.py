@@ -2,6 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cold] [--no-cpu]
     python bench.py --copy-calibration          # plain kernels of known traffic, for the counter scaling
+    python bench.py --ceiling                   # the practical HBM ceiling at each workload's size (probe kernels)
     python bench.py --traffic-from DIR          # turn FETCH_SIZE / WRITE_SIZE counter runs into profiles/traffic.json
 
 A step is one launch of the op over its whole workload with the inputs already resident in HBM. Each workload is
@@ -62,6 +63,9 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="only launch a 256 MiB read-only and a 256 MiB write-only kernel --steps times (for the "
                         "counter scaling)")
+    p.add_argument("--ceiling", action="store_true",
+                   help="only time the bandwidth probes (build/probe): a 1R + 1W copy moving each workload's "
+                        "algorithmic bytes, and a read of the top-k input")
     p.add_argument("--traffic-from", default=None,
                    help="directory with rocprofv3 counter CSVs (fetch/ and write/ runs of this script and of "
                         "--copy-calibration); writes profiles/traffic.json")
@@ -307,6 +311,59 @@ def copy_calibration(steps):
     print(json.dumps({"calibration_bytes": COPY_BYTES, "launches": steps}))
 
 
+class ProbeCase:
+    """A bandwidth probe bound to R device copies, timed as the workloads are: a copy (probe_copy) of `bytes` / 2
+    bytes read and as many written, or a read (probe_read) of `bytes` bytes."""
+
+    def __init__(self, pkg, label, nbytes, kind, dev):
+        import ctypes
+        import torch
+        lib = ctypes.CDLL(pkg.lib_path("probe"))
+        lib.probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+        lib.probe_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_void_p]
+        self.label, self.k = label, None
+        moved = (nbytes // 2 if kind == "copy" else nbytes) // 16 * 16
+        stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
+
+        def make():
+            x = torch.ones(moved // 4, dtype=torch.float32, device=dev)
+            if kind == "copy":
+                y = torch.empty_like(x)
+                return lambda: lib.probe_copy(x.data_ptr(), y.data_ptr(), moved, stream())
+            return lambda: lib.probe_read(x.data_ptr(), moved, sink.data_ptr(), stream())
+        footprint = 2 * moved if kind == "copy" else moved
+        self.copies = max(4, -(-ROTATE_BYTES // footprint))
+        self.launchers = [make() for _ in range(self.copies)]
+        self.bytes = 2 * moved if kind == "copy" else moved
+
+    def launch(self, i=0):
+        return self.launchers[i % self.copies]()
+
+
+def ceiling(pkg, steps, warmup):
+    """The practical HBM ceiling at each workload's size: the copy probe moving the workload's algorithmic bytes (half
+    read, half written: the 1R + 1W pattern of the row kernels) and the read probe over the top-k input. One JSON line
+    {label: {us_mean, bytes, gbs, pct_peak}}."""
+    import torch
+    dev = torch.device("cuda:0")
+    w = pkg.workloads
+    plan = [(f"copy_like_{n}", w.algorithmic_bytes(n), "copy")
+            for n in ("softmax_4096x4096", "rmsnorm_16384x4096", "rope_4x4096_32q_8kv_128", "rmsnorm_add_16384x4096",
+                      "rope_kv_4x4096_32q_8kv_128")]
+    plan.append(("read_like_topk_128x128256", 128 * 128256 * 4, "read"))
+    out = {}
+    for label, nbytes, kind in plan:
+        case = ProbeCase(pkg, label, nbytes, kind, dev)
+        res = time_rotating(case, steps, warmup)
+        print(f"[ceiling] {label}: {res['us_mean']:.2f} us/call  {res['gbs']:.0f} GB/s  "
+              f"{res['pct_peak']:.1f}% of peak", file=sys.stderr, flush=True)
+        out[label] = {key: round(res[key], 3) for key in ("us_mean", "bytes", "gbs", "pct_peak")}
+        del case
+        torch.cuda.empty_cache()
+    print(json.dumps(out))
+
+
 def counter_means(run_dir, counter):
     """Mean per dispatch of `counter` for each kernel name in the rocprofv3 counter CSVs under run_dir."""
     sums, counts = {}, {}
@@ -375,6 +432,9 @@ def main():
     import torch
     from __graft_entry__ import load_package
     pkg = load_package()
+    if args.ceiling:
+        ceiling(pkg, args.steps, args.warmup)
+        return
     dev = torch.device("cuda:0")
     flush_buf = None if args.no_cold else torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
     sink = torch.empty((), device=dev)

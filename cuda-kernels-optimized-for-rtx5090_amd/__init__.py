@@ -14,6 +14,7 @@ from . import workloads  # noqa: F401  (named workloads: shapes, seeds, byte cou
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 OPS = ("softmax", "rmsnorm", "rope", "topk")
+PROBES = ("probe",)  # the bandwidth probes of the measurement (bench.py --ceiling), not an op
 
 
 def lib_path(op):
@@ -21,8 +22,8 @@ def lib_path(op):
     return os.path.join(PKG_DIR, "build", op, "libkernel.so")
 
 
-def build(ops=OPS):
-    """Compiles the libraries of the given ops for gfx950; returns {op: path}."""
+def build(ops=OPS + PROBES):
+    """Compiles the libraries of the given ops (and the probes) for gfx950; returns {op: path}."""
     from . import make_libs
     return make_libs.build(ops)
 

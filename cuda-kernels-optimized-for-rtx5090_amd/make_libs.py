@@ -14,7 +14,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
-OPS = ("softmax", "rmsnorm", "rope", "topk")
+LIBS = ("softmax", "rmsnorm", "rope", "topk", "probe")  # the four ops and the bandwidth probes of bench.py --ceiling
 ARCH = os.environ.get("ROWKERN_ARCH", "gfx950")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 (some of their forms are unreliable on this part); hipcc's host pass
@@ -57,7 +57,7 @@ def build_one(op):
     return op, out, "\n".join(lines)
 
 
-def build(ops=OPS, jobs=4):
+def build(ops=LIBS, jobs=4):
     """Compiles the given ops; returns {op: path}. Raises RuntimeError on a compiler error."""
     results = {}
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
@@ -69,6 +69,6 @@ def build(ops=OPS, jobs=4):
 
 
 if __name__ == "__main__":
-    ops = sys.argv[1:] or OPS
+    ops = sys.argv[1:] or LIBS
     for op, path in build(ops).items():
         print(op, path)

@@ -40,6 +40,20 @@ def test_library_exports_the_header(pkg, op):
     assert c_symbols == set(names), f"{op}: exported {sorted(c_symbols)} vs declared {sorted(names)}"
 
 
+def test_probe_library_exports_and_codes_without_gpu(pkg):
+    # the measurement's bandwidth probes (bench.py --ceiling): a library of their own, outside the op boundary
+    path = pkg.lib_path("probe")
+    assert os.path.exists(path), f"{path} not built"
+    c_symbols = {s for s in exported(path) if not s.startswith("_Z") and not s.startswith("_")}
+    assert c_symbols == {"probe_copy", "probe_read"}
+    lib = ctypes.CDLL(path)
+    lib.probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+    lib.probe_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_void_p]
+    assert lib.probe_copy(None, None, 0, None) == 0
+    assert lib.probe_copy(16, 16, 24, None) == -1  # not whole 16-byte vectors
+    assert lib.probe_read(16, 32, None, None) == -1  # no sink
+
+
 def test_softmax_codes_without_gpu(pkg):
     lib = ctypes.CDLL(pkg.lib_path("softmax"))
     assert lib.launch(None, None, ctypes.c_longlong(0), ctypes.c_longlong(5), 0, 256, 1024, None) == 0
