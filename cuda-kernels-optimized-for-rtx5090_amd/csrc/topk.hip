@@ -649,6 +649,35 @@ struct Tile {
     asm volatile("" ::: "memory");  // issue the loads here: the scheduler must not sink them past later work
   }
 
+  // The lane's largest composite: its largest key and the lowest index holding it (raw bits equal the key's bits, the
+  // key mapping being one to one). A sentinel element (past the chunk's end, key 0, after every real element of the
+  // lane in index order) never wins over a real one.
+  __device__ __forceinline__ u64 best_composite() {
+    const uint32_t m = max_key();  // vector by vector as the loads complete
+    const uint32_t t = bits_of(m);
+    opaque();
+    // the first match's vector and element, visited from the last element to the first; both are inline constants
+    // (a select of each element's offset would hold 64 literal offsets in registers)
+    int vb = 0, jb = 0;
+#pragma unroll
+    for (int v = NV - 1; v >= 0; --v) {
+#pragma unroll
+      for (int j = W - 1; j >= 0; --j) {
+        bool eq;
+        if constexpr (sizeof(T) == 4) {
+          eq = r[v][j] == t;
+        } else {
+          const uint32_t w = r[v][j >> 1];
+          eq = ((j & 1) ? (w & 0xffff0000u) : (w << 16)) == t;
+        }
+        vb = eq ? v : vb;
+        jb = eq ? j : jb;
+      }
+    }
+    const int off = vb * kThreads * W + jb;
+    return ((u64)m << 32) | (u64)(~(uint32_t)(lane0 + off));
+  }
+
   // The key of this lane's largest element (the sentinel's key for a lane holding none).
   __device__ __forceinline__ uint32_t max_key() const {
     if constexpr (sizeof(T) == 4) {
@@ -1038,7 +1067,7 @@ __device__ __forceinline__ void sample_top(const SampleArgs& sa, float u, const 
 // descending, to the workspace with device-coherent stores, waits for them to complete and counts its arrival on the
 // row's counter (arrivals[row * kArrivalStride]); the row's last arrival merges the lists (merge_lists) and zeroes the
 // counter for the next launch -- no L2 write-back or invalidate, and no second kernel.
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool ONE>
 __global__ void __launch_bounds__(kThreads)
     topk_tile(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
               u64* __restrict__ work, unsigned* __restrict__ arrivals, long long cols, long long chunk, int nchunks,
@@ -1059,6 +1088,43 @@ __global__ void __launch_bounds__(kThreads)
   const int kw = (k + kWaves - 1) / kWaves;
   using TL = Tile<T, VEC>;
   constexpr int TE = kThreads * kTileE;
+  if constexpr (ONE) {
+    // k = 1 (its own instance): the chunk's largest composite, straight from the registers (no bound, list or block
+    // reductions per tile)
+    u64 best = 0;
+    for (int t0 = begin; t0 < end; t0 += TE) {
+      TL tile;
+      tile.load(xr, t0, end);
+      const u64 c = tile.best_composite();
+      best = c > best ? c : best;
+    }
+    best = wave_ext64<true>(best);
+    if (lane_id() == 0) s.sorted[wave_id()] = best;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) best = s.sorted[w] > best ? s.sorted[w] : best;
+    u64 c = best;
+    if (nchunks > 1) {
+      // the chunk's best goes into the row's slot beside its arrival counter by a device-scope maximum (completed
+      // before the arrival is counted); the row's last arrival writes the slot out and zeroes slot and counter for
+      // the next launch
+      unsigned* counter = arrivals + row * kArrivalStride;
+      u64* slot = reinterpret_cast<u64*>(counter + kBestOffset);
+      __hip_atomic_fetch_max(slot, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      const unsigned old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old != (unsigned)nchunks - 1) return;
+      c = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row] = composite_bits(c);
+    else static_cast<uint16_t*>(values)[row] = (uint16_t)(composite_bits(c) >> 16);
+    indices[row] = composite_index(c);
+    if (sa.out) sa.out[row] = composite_index(c);  // the draw from a one-entry list
+    return;
+  }
   auto process = [&](TL& tile, bool more) __attribute__((always_inline)) {
     const bool has = tile.lane0 < tile.b1;
     const uint32_t m = tile.max_key();  // vector by vector as the loads complete
@@ -1095,36 +1161,6 @@ __global__ void __launch_bounds__(kThreads)
     const float u = sa.uniform(row);
     finish_list<T>(s, L, values, indices, nullptr, row, k, true);
     sample_top(sa, u, s.top, row, k);
-    return;
-  }
-  if (k == 1) {
-    // the chunk's largest composite goes into the row's slot beside its arrival counter by a device-scope maximum
-    // (completed before the arrival is counted); the row's last arrival writes the slot out and zeroes slot and
-    // counter for the next launch
-    u64 best = 0;
-    const int n = L.cnt < kTileSeg ? L.cnt : kTileSeg;
-    for (int i = lane_id(); i < n; i += kWave) best = L.seg[i] > best ? L.seg[i] : best;
-    best = wave_ext64<true>(best);
-    if (lane_id() == 0) s.sorted[wave_id()] = best;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-#pragma unroll
-      for (int w = 1; w < kWaves; ++w) best = s.sorted[w] > best ? s.sorted[w] : best;
-      unsigned* counter = arrivals + row * kArrivalStride;
-      u64* slot = reinterpret_cast<u64*>(counter + kBestOffset);
-      __hip_atomic_fetch_max(slot, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      const unsigned old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (old == (unsigned)nchunks - 1) {
-        const u64 c = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row] = composite_bits(c);
-        else static_cast<uint16_t*>(values)[row] = (uint16_t)(composite_bits(c) >> 16);
-        indices[row] = composite_index(c);
-        if (sa.out) sa.out[row] = composite_index(c);  // the draw from a one-entry list
-        __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
     return;
   }
   u64* wr = work + row * (long long)nchunks * k;
@@ -1531,8 +1567,12 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, long l
                                                       kArrivalsPurpose, true);
       if (!arrivals) return err;
     }
-    hipLaunchKernelGGL((topk_tile<T, VEC>), grid, dim3(kThreads), 0, stream, (const T*)x, values, (long long*)indices,
-                       (u64*)work, arrivals, cols, chunk, nchunks, k, sa);
+    if (k == 1)
+      hipLaunchKernelGGL((topk_tile<T, VEC, true>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
+                         (long long*)indices, (u64*)work, arrivals, cols, chunk, nchunks, k, sa);
+    else
+      hipLaunchKernelGGL((topk_tile<T, VEC, false>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
+                         (long long*)indices, (u64*)work, arrivals, cols, chunk, nchunks, k, sa);
     return (int)hipGetLastError();
   }
   // The result does not depend on the chunking, so the chunks are made long enough for a useful bound (16k elements:
@@ -1577,7 +1617,7 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
   if (per_cu <= 0) {
     if (occ <= 0) {
       int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_tile<float, true>, kThreads, 0) != hipSuccess ||
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_tile<float, true, false>, kThreads, 0) != hipSuccess ||
           n <= 0) {
         (void)hipGetLastError();
         n = 4;
