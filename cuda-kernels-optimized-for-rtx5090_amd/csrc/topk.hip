@@ -7,7 +7,9 @@
 // for bit, so x is read once.
 //
 // k <= 64: topk_tile, one kernel (see its comment); the row's last workgroup merges the chunk lists, handed over
-// through device-coherent stores and loads and a per-row arrival counter, as the reference's last-block merge.
+// through device-coherent stores and loads and a per-row arrival counter, as the reference's last-block merge. k = 1
+// is an instance of its own: each lane's largest composite straight from the registers, the chunks' best folded by a
+// device-scope maximum beside the arrival counter.
 //
 // 64 < k <= 1024: topk_wide, one kernel of the same shape (see its comment): a bound from group maxima admits about
 // 1.4k elements per tile, the row's last workgroup merges the chunks' candidate lists from a floor made of their
