@@ -218,8 +218,11 @@ __global__ void __launch_bounds__(WAVES * 64)
 // and a NaN chunk NaNs). Wave 0 polls the row's slots with device-coherent loads until all are published, merges them
 // (the same lanes and order in every workgroup of the row, so all agree bit for bit) and hands M and S to the other
 // waves; the chunk is then written from the registers. Last, a departure counter finds the row's last workgroup, which
-// zeroes the row's slots and the counter for the next launch (the workspace starts zeroed). The wait is bounded: it
-// always ends, even if a row's workgroups could not all run.
+// zeroes the row's slots and the counter for the next launch (the workspace starts zeroed). The wait is bounded
+// (spin_limit polls): it always ends, even if a row's workgroups could not all run at once (other kernels holding
+// CUs, or two such launches on two streams). A workgroup whose wait ends before every pair is published takes the
+// row's M and S from x itself (every thread an online max and sum over a share of the whole row), so the result
+// stays within the tolerance either way; only the time suffers.
 constexpr unsigned kSpinLimit = 1u << 22;
 constexpr int kCoopMaxChunks = 64;  // slots a row may have (one per lane of the polling wave)
 
@@ -230,12 +233,13 @@ __device__ __forceinline__ unsigned long long pair_bits(float m, float s) {
 template <typename T, int WAVES, int NV, bool NTL, bool NTS>
 __global__ void __launch_bounds__(WAVES * 64)
     softmax_coop(const void* __restrict__ x, void* __restrict__ y, unsigned long long* __restrict__ pairs,
-                 unsigned* __restrict__ departs, long long nvec, long long chunks) {
+                 unsigned* __restrict__ departs, long long nvec, long long chunks, unsigned spin_limit) {
   constexpr int G = WAVES * kWave;
   constexpr long long CH = (long long)G * NV;
   constexpr int PER = kCoopMaxChunks / kWave;
   __shared__ float slots[2][WAVES];
   __shared__ float ms[2];
+  __shared__ int partial;  // the wait ended before every pair of the row was published
   const long long b = blockIdx.x;
   const long long row = b / chunks, c = b - row * chunks;
   const long long first = c * CH;
@@ -279,7 +283,7 @@ __global__ void __launch_bounds__(WAVES * 64)
     unsigned long long v[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) v[i] = 0;
-    for (unsigned n = 0; n < kSpinLimit; ++n) {
+    for (unsigned n = 0; n < spin_limit; ++n) {
       bool ready = true;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
@@ -291,6 +295,10 @@ __global__ void __launch_bounds__(WAVES * 64)
       if (__ballot(!ready) == 0) break;
       __builtin_amdgcn_s_sleep(1);
     }
+    bool have = true;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) have = have && ((long long)i * kWave + lane >= chunks || v[i] != 0);
+    const bool complete = __ballot(!have) == 0;
     float pm = -INFINITY, ps = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -308,9 +316,37 @@ __global__ void __launch_bounds__(WAVES * 64)
     if (lane == 0) {
       ms[0] = M;
       ms[1] = S;
+      partial = complete ? 0 : 1;
     }
   }
   __syncthreads();
+  if (partial) {
+    // the row's M and S from x: an online max and sum per thread over its share of the row, merged over the block
+    // (-inf elements add nothing; a NaN makes the sum NaN, as in the pairs)
+    float tm = -INFINITY, ts = 0.0f;
+    for (long long i = t; i < nvec; i += G) {
+      float f[T::V];
+      unpack<T>(load16<false>(x, row * nvec + i), f);
+#pragma unroll
+      for (int e = 0; e < T::V; ++e) {
+        if (f[e] == -INFINITY) continue;
+        if (f[e] > tm) {
+          ts = ts * expf(tm - f[e]) + 1.0f;
+          tm = f[e];
+        } else {
+          ts += expf(f[e] - tm);
+        }
+      }
+    }
+    const float RM = group_reduce<WAVES>(tm, OpMax{}, slots[0], wave_id(), 0);
+    const float RS = group_reduce<WAVES>(tm == -INFINITY ? 0.0f : ts * expf(tm - RM), OpSum{}, slots[1], wave_id(), 0);
+    __syncthreads();  // every wave has read ms and the slots before they are written
+    if (t == 0) {
+      ms[0] = RM;
+      ms[1] = RS;
+    }
+    __syncthreads();
+  }
   const float M = ms[0], S = ms[1];
   if constexpr (KEEP) {
     // y = e * exp(m - M) / S; an all -inf chunk (e = 0) gives 0, or NaN when the whole row is -inf (M = -inf)
@@ -369,9 +405,9 @@ __global__ void __launch_bounds__(256)
 
 // Tuning slots (0 = automatic): row-tier waves per row, row-tier vectors per lane, row-tier resident blocks per CU,
 // split-tier waves, split-tier vectors per lane, forced tier (1 row, 2 split, 3 generic, 4 co-resident), non-temporal
-// loads (1 on, 2 off).
+// loads (1 on, 2 off), the co-resident tier's bound on its polls (tests force its fallback with a small one).
 enum { kTuneWaves = 0, kTuneNv = 1, kTuneBlocksPerCu = 2, kTuneSplitWaves = 3, kTuneSplitNv = 4, kTuneTier = 5,
-       kTuneNtLoads = 6 };
+       kTuneNtLoads = 6, kTuneSpinLimit = 7 };
 
 int pow2_at_least(long long v) {
   int p = 1;
@@ -495,7 +531,9 @@ int launch_coop(const void* x, void* y, long long rows, long long nvec, hipStrea
   if (!ws) return err;
   unsigned* departs = (unsigned*)ws;
   unsigned long long* pairs = (unsigned long long*)(ws + kCoopCounterBytes);
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(WAVES * kWave), 0, stream, x, y, pairs, departs, nvec, chunks);
+  const int limit = rw_host::tune_get(kTuneSpinLimit);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(WAVES * kWave), 0, stream, x, y, pairs, departs, nvec, chunks,
+                     limit > 0 ? (unsigned)limit : kSpinLimit);
   return (int)hipGetLastError();
 }
 

@@ -4,12 +4,13 @@
 // NaN). Every device buffer lies between guard pages. The co-resident tier (4) needs EMU_CONCURRENT: its workgroups
 // wait for one another.
 //
-// usage: emu_softmax rows cols dtype(0 fp32, 1 bf16) tier seed [waves nv [offset [pattern [reps]]]]
+// usage: emu_softmax rows cols dtype(0 fp32, 1 bf16) tier seed [waves nv [offset [pattern [reps [spin_limit]]]]]
 //   tier: 1 row, 2 split, 3 generic, 4 co-resident (forced through softmax_tune); waves / nv: the row tier's (tier 1)
 //   or the split tier's (tier 2) shape, 0 automatic; offset shifts x and y by that many elements from a 16-byte
 //   boundary (a misaligned row takes the generic tier); pattern: randn (N(0, 4)) or special (-inf elements, an all
 //   -inf row, a row of one huge value); reps: launches on the same buffers, each checked (the co-resident tier's
-//   hand-off slots must be clear again for the next).
+//   hand-off slots must be clear again for the next); spin_limit bounds the co-resident tier's polls (a small one
+//   makes its workgroups stop waiting and take the row's statistics from x).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -47,6 +48,7 @@ int main(int argc, char** argv) {
   const int offset = argc > 8 ? atoi(argv[8]) : 0;
   const std::string pattern = argc > 9 ? argv[9] : "randn";
   const int reps = argc > 10 ? atoi(argv[10]) : 1;
+  if (argc > 11) softmax_tune(7, atoi(argv[11]));
   softmax_tune(5, tier);
   softmax_tune(tier == 2 ? 3 : 0, waves);
   softmax_tune(tier == 2 ? 4 : 1, nv);

@@ -107,6 +107,15 @@ def test_emulated_softmax_coresident_tier(emu_softmax, case):
     run(emu_softmax, [rows, cols, dtype, 4, seed, 0, 0, 0, pattern, reps], concurrent=True)
 
 
+@pytest.mark.parametrize("concurrent", [False, True], ids=["one_after_another", "concurrent"])
+@pytest.mark.parametrize("case", COOP, ids=[c[0] for c in COOP])
+def test_emulated_softmax_coresident_fallback(emu_softmax, case, concurrent):
+    # the wait bounded to one poll: workgroups that find their row incomplete (all but the row's last when they run one
+    # after another) take the row's statistics from x
+    rows, cols, dtype, seed, pattern, reps = case[1:]
+    run(emu_softmax, [rows, cols, dtype, 4, seed, 0, 0, 0, pattern, reps, 1], concurrent=concurrent)
+
+
 @pytest.mark.parametrize("case", RMSNORM, ids=[c[0] for c in RMSNORM])
 def test_emulated_rmsnorm_matches_oracle(emu_rmsnorm, case):
     run(emu_rmsnorm, case[1:])
