@@ -1078,7 +1078,7 @@ __global__ void __launch_bounds__(kThreads)
   const long long row = blockIdx.y;
   const int part = blockIdx.x;
   const int begin = (int)((long long)part * chunk);
-  const int end = (int)(begin + chunk < cols ? begin + chunk : cols);
+  const int end = (int)(part == nchunks - 1 ? cols : begin + chunk);  // the last chunk may hold a merged tail
   const T* xr = x + row * cols;
   BlockRed red;  // fields assigned at run time (an aggregate initializer of LDS addresses does not compile)
   red.slot = s.red;
@@ -1560,8 +1560,13 @@ constexpr int kListsPurpose = 3;     // stream_workspace key of the 64 < k kerne
 template <typename T, bool VEC>
 int launch_chunks(const void* x, void* values, void* indices, void* work, long long rows,
                   long long cols, long long chunk, int nchunks, int k, const SampleArgs& sa, hipStream_t stream) {
-  const dim3 grid((unsigned)nchunks, (unsigned)rows);
   if (k <= kSeedMaxK) {
+    // A last chunk too short to give each of the four waves a vector would leave a wave without a bound, and the tile
+    // would take the exact re-push path; when the previous chunk can take it within one register tile, it does.
+    const long long tail = cols - (long long)(nchunks - 1) * chunk;
+    if (nchunks > 1 && tail < (long long)kThreads * Tile<T, VEC>::W && chunk + tail <= (long long)kThreads * kTileE)
+      --nchunks;
+    const dim3 grid((unsigned)nchunks, (unsigned)rows);
     unsigned* arrivals = nullptr;
     if (nchunks > 1) {  // the arrival counters: zeros between launches, kept per (device, stream)
       int err = rw_host::kOk;
