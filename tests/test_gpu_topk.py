@@ -166,6 +166,22 @@ def test_short_last_tiles(pkg, oracle, dev, dt, k):
             check(pkg, oracle, x, k, dev, chunk=chunk, what="short last tile")
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_folded_last_chunk_bounds(pkg, oracle, dev, dt):
+    # a last chunk shorter than one vector per lane is folded into the previous chunk when both fit one register tile:
+    # tails on either side of that length, and previous chunks on either side of the tile's end
+    w = 4 if dt == torch.float32 else 8
+    short = 256 * w  # the length at which each of the four waves holds a vector
+    g = torch.Generator().manual_seed(77)
+    cases = [(2048, short - w), (2048, short), (2048, w), (16384 - (short - w), short - w),
+             (16384 - (short - w) + 8, short - w)]
+    for chunk, tail in cases:
+        cols = 3 * chunk + tail
+        x = (torch.randn(2, cols, generator=g) * 2).to(dt)
+        for k in (1, 13, 64):
+            check(pkg, oracle, x, k, dev, chunk=chunk, what=f"fold chunk={chunk} tail={tail}")
+
+
 def test_bf16_and_unaligned(pkg, oracle, dev):
     g = torch.Generator().manual_seed(5)
     xb = torch.randn(8, 50000, generator=g).bfloat16()
