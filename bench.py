@@ -153,7 +153,7 @@ class Case:
             lib = cand._lib
             rows, cols = inp["x"].shape
             k, temp, top_p = inp["k"], inp["temperature"], inp["top_p"]
-            chunk = cand._plan(inp["x"].to(dev), rows, cols, 0, k)[1]
+            chunk = cand._plan(inp["x"].to(dev), rows, cols, 0, k)[0]
             nchunks = -(-cols // chunk)
             uni = inp["uniforms"].to(dev)
             self.dtype = "fp32"
@@ -178,7 +178,7 @@ class Case:
             cand = pkg.candidate("topk")
             lib = cand._lib
             rows, cols = inp["x"].shape
-            chunk = cand._plan(inp["x"].to(dev), rows, cols, 0, k)[1]
+            chunk = cand._plan(inp["x"].to(dev), rows, cols, 0, k)[0]
             nchunks = -(-cols // chunk)
             self.dtype = "fp32"
 

@@ -277,12 +277,6 @@ static_assert(kTileSort == kThreads, "the rank sort and the merge heads use one 
 
 typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
 
-// A row's arrival counter sits alone in its 256 bytes: the device-scope atomics of the rows' last workgroups, which
-// come close together, are not serialized on a shared line (the caller's counters are 4 bytes apart).
-constexpr int kArrivalStride = 64;
-// k = 1: the row's best composite so far (u64, zero between launches) sits 8 bytes into the counter's 256 bytes
-constexpr int kBestOffset = 2;
-
 struct TileSmem {
   u64 seg[kWaves][kTileSeg];
   alignas(16) u64 sorted[kTileSort];
@@ -586,6 +580,45 @@ __device__ __forceinline__ void finish_list(TileSmem& s, const TileList& L, void
   if (!to_output)
     for (int j = n + t; j < k; j += kThreads)
       __hip_atomic_store(wr + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- the chunk hand-off ----------------------------------------------------------------------------------------------
+
+// A split row's chunks hand their results to the row's last arrival as the reference's topk_filter does
+// (topk/kernel.cu:411-442): each chunk stores its result in its slots of the caller's work, then counts its arrival
+// on the caller's counters[row]; the arrival that finds every other chunk counted merges, and zeroes the counter for
+// the next launch. Results are written and read with agent-scope atomic (relaxed) stores and loads, which gfx950
+// performs coherently across its XCDs (each XCD has its own L2), and the counter is an agent-scope atomic add. The
+// order between them:
+//  - writer: `s_waitcnt vmcnt(0)` after the result stores waits until the memory system has acknowledged every store
+//    of the wave (on gfx9 that counter covers stores as well as loads), and the add is issued after it, so the results
+//    are complete at agent scope before the add can be observed;
+//  - reader: the last arrival branches on the value the add returned, so its loads issue after the add has completed,
+//    and as agent-scope loads they take the coherent value, not a stale L1 or L2 copy.
+// This is LLVM's agent-scope release and acquire for gfx942/gfx950 (the AMDGPU memory model) without the L2 write-back
+// (buffer_wbl2) and invalidate (buffer_inv) that make non-atomic data visible: every location handed over here is
+// accessed only through agent-scope atomics, so there is no such data, and per-workgroup whole-L2 maintenance measured
+// about 100 us over a 1024-workgroup grid.
+
+// One wave's arrival: waits for the wave's result stores, then lane 0 counts the arrival on *counter. Returns, uniform
+// over the wave, whether it was the last of n.
+__device__ __forceinline__ bool hand_off_arrive(unsigned* counter, int n) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  unsigned old = 0;
+  if (lane_id() == 0) old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return (unsigned)__builtin_amdgcn_readfirstlane(old) == (unsigned)n - 1;
+}
+
+// A workgroup's arrival: each wave waits for its own result stores, the barrier gathers the waves, and thread 0 counts
+// the arrival on *counter. Returns, uniform over the workgroup, whether it was the last of n.
+template <typename S>
+__device__ __forceinline__ bool block_hand_off(S& s, unsigned* counter, int n) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s.last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)n - 1;
+  __syncthreads();
+  return s.last != 0;
 }
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
@@ -1066,13 +1099,14 @@ __device__ __forceinline__ void sample_top(const SampleArgs& sa, float u, const 
 // continuous data) are appended to the waves' LDS segments; a list beyond kTileKeep is pruned to k, and an overflowing
 // tile (ties, or adversarial orders) is pushed again in index order with a prune whenever the list passes kTileKeep.
 // The list is then rank-sorted and written out for an unsplit row. A split row's chunk writes its k largest,
-// descending, to the workspace with device-coherent stores, waits for them to complete and counts its arrival on the
-// row's counter (arrivals[row * kArrivalStride]); the row's last arrival merges the lists (merge_lists) and zeroes the
-// counter for the next launch -- no L2 write-back or invalidate, and no second kernel.
+// descending, to its slots of the caller's work [rows, nchunks, k] with device-coherent stores, waits for them to
+// complete and counts its arrival on the caller's counters[row]; the row's last arrival merges the lists (merge_lists)
+// and zeroes the counter for the next launch -- no L2 write-back or invalidate, and no second kernel (the protocol of
+// topk/kernel.cu:411-442, without its __threadfence: see hand_off_arrive).
 template <typename T, bool VEC, bool ONE>
 __global__ void __launch_bounds__(kThreads)
     topk_tile(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
-              u64* __restrict__ work, unsigned* __restrict__ arrivals, long long cols, long long chunk, int nchunks,
+              u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
               int k, SampleArgs sa) {
   __shared__ TileSmem s;
   const long long row = blockIdx.y;
@@ -1103,24 +1137,25 @@ __global__ void __launch_bounds__(kThreads)
     best = wave_ext64<true>(best);
     if (lane_id() == 0) s.sorted[wave_id()] = best;
     __syncthreads();
-    if (threadIdx.x != 0) return;
+    if (wave_id() != 0) return;
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) best = s.sorted[w] > best ? s.sorted[w] : best;
     u64 c = best;
     if (nchunks > 1) {
-      // the chunk's best goes into the row's slot beside its arrival counter by a device-scope maximum (completed
-      // before the arrival is counted); the row's last arrival writes the slot out and zeroes slot and counter for
-      // the next launch
-      unsigned* counter = arrivals + row * kArrivalStride;
-      u64* slot = reinterpret_cast<u64*>(counter + kBestOffset);
-      __hip_atomic_fetch_max(slot, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      const unsigned old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (old != (unsigned)nchunks - 1) return;
-      c = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the chunk's best goes to its slot work[row * nchunks + part]; the row's last arrival takes the largest slot
+      // and zeroes the row's counter for the next launch
+      u64* slots = work + row * (long long)nchunks;
+      if (lane_id() == 0) __hip_atomic_store(slots + part, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!hand_off_arrive(counters + row, nchunks)) return;
+      u64 m = 0;
+      for (int i = lane_id(); i < nchunks; i += kWave) {
+        const u64 v = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        m = v > m ? v : m;
+      }
+      c = wave_ext64<true>(m);
+      if (lane_id() == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (lane_id() != 0) return;
     if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row] = composite_bits(c);
     else static_cast<uint16_t*>(values)[row] = (uint16_t)(composite_bits(c) >> 16);
     indices[row] = composite_index(c);
@@ -1167,22 +1202,12 @@ __global__ void __launch_bounds__(kThreads)
   }
   u64* wr = work + row * (long long)nchunks * k;
   finish_list<T>(s, L, values, indices, wr + (long long)part * k, row, k, false);
-  // hand-off: the chunk list is device-visible before its arrival is counted; the row's last arrival merges the lists
-  // and zeroes the row's counter for the next launch
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned old =
-        __hip_atomic_fetch_add(arrivals + row * kArrivalStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s.last = old == (unsigned)nchunks - 1;
-  }
-  __syncthreads();
-  if (!s.last) return;
+  // hand-off: the row's last arrival merges the lists and zeroes the row's counter for the next launch
+  if (!block_hand_off(s, counters + row, nchunks)) return;
   const float u = sa.uniform(row);
   L.cnt = 0;
   merge_lists<T>(s, red, L, values, indices, wr, row, nchunks, k);
-  if (threadIdx.x == 0)
-    __hip_atomic_store(arrivals + row * kArrivalStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   sample_top(sa, u, s.top, row, k);
 }
 
@@ -1196,9 +1221,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 constexpr int kWideCap = 4096;    // the wide kernel's candidate buffer (composites)
-constexpr int kWideList = 2048;   // the most candidates a chunk publishes (it prunes to k beyond)
-constexpr int kWideHead = 4;      // a published list's header: count, k-bound, q-bound, unused
-constexpr int kWideSlot = kWideHead + kWideList;
+constexpr int kWideList = 2048;   // the most candidates ranked at once (write_ranked)
 constexpr int kWideMaxChunks = 256;
 
 constexpr int kRankBuckets = 4096;  // buckets of write_ranked (16-bit counters and first positions)
@@ -1371,20 +1394,21 @@ __device__ __forceinline__ uint32_t wave_kth_multi(const uint32_t (&v)[N], int k
 // data). The same bound for q = ceil(k / nchunks) gives a q-bound. Admitted elements are appended to an LDS buffer (one
 // LDS atomic per wave and 16 elements per lane); a tile that overflows it (ties, adversarial orders) is appended again
 // vector by vector from the buffer's k-th, pruning to k (histogram narrowing) whenever a vector might not fit. An
-// unsplit row ranks its candidates (write_ranked) and writes the first k. A split row's chunk publishes its candidates
-// (at most kWideList: pruned to k beyond) with its k- and q-bounds to its list in the library's workspace with
-// device-coherent stores, waits for them and counts its arrival; the row's last arrival merges: every chunk has k
-// elements at or above its k-bound and q at or above its q-bound, so the largest k-bound and, when every chunk has one,
-// the smallest q-bound (nchunks * q >= k elements at or above it) bound the row's k-th from below; the lists'
-// candidates at or above that floor (about k * 1.4) are gathered, ranked and the first k written out.
+// unsplit row ranks its candidates (write_ranked) and writes the first k. A split row's chunk keeps its k largest
+// (pruned to exactly k when it holds more), writes them to its k slots of the caller's work [rows, nchunks, k] (0 past
+// the end of a shorter list) and its k- and q-bound keys to indices[row * k + part] (the row's output, not yet written:
+// nchunks <= k), all with device-coherent stores, and counts its arrival on counters[row] (block_hand_off). The row's
+// last arrival merges: every chunk has k elements at or above its k-bound and q at or above its q-bound, so the largest
+// k-bound and, when every chunk has one, the smallest q-bound (nchunks * q >= k elements at or above it) bound the
+// row's k-th from below; the lists' entries at or above that floor (about k * 1.4) are gathered, ranked and the first
+// k written out, and the counter is zeroed for the next launch.
 template <typename T, bool VEC>
 __global__ void __launch_bounds__(kThreads)
     topk_wide(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
-              u64* __restrict__ lists, unsigned* __restrict__ arrivals, long long cols, long long chunk, int nchunks,
+              u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
               int k, SampleArgs sa) {
   __shared__ Smem<kWideCap> s;
   __shared__ uint32_t redslots[2][kWaves];
-  __shared__ int counts[kWideMaxChunks];
   const long long row = blockIdx.y;
   const int part = blockIdx.x;
   const int begin = (int)((long long)part * chunk);
@@ -1452,35 +1476,26 @@ __global__ void __launch_bounds__(kThreads)
     sample_list<T>(sa, u, values, indices, row, k);
     return;
   }
-  if (s.count > kWideList) prune(s, k);
+  if (s.count > k) prune(s, k);  // the chunk's k largest (its k-th raises s.thr)
   const int n = s.count;
-  // publish: header (count, k-bound, q-bound) and the candidates
-  u64* wr = lists + row * (long long)nchunks * kWideSlot;
-  u64* mine = wr + (long long)part * kWideSlot;
-  auto put = [&](int at, u64 v) { __hip_atomic_store(mine + at, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-  for (int i = threadIdx.x; i < n; i += kThreads) put(kWideHead + i, s.buf[i]);
+  // publish: the list, zero-padded to k, and the header (k-bound key << 32 | q-bound key) in the row's output
+  u64* wr = work + row * (long long)nchunks * k;
+  u64* mine = wr + (long long)part * k;
+  for (int i = threadIdx.x; i < k; i += kThreads)
+    __hip_atomic_store(mine + i, i < n ? s.buf[i] : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  u64* heads = reinterpret_cast<u64*>(indices + row * k);
   if (threadIdx.x == 0) {
-    const u64 kb = (u64)thr << 32;
-    put(0, (u64)n);
-    put(1, s.thr > kb ? s.thr : kb);
-    put(2, (u64)thq << 32);
+    const uint32_t kb = (uint32_t)(s.thr >> 32) > thr ? (uint32_t)(s.thr >> 32) : thr;
+    __hip_atomic_store(heads + part, ((u64)kb << 32) | thq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned old =
-        __hip_atomic_fetch_add(arrivals + row * kArrivalStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s.last = old == (unsigned)nchunks - 1;
-  }
-  __syncthreads();
-  if (!s.last) return;
+  if (!block_hand_off(s, counters + row, nchunks)) return;
   const float u = sa.uniform(row);
-  // merge (the row's last arrival): the floor from the headers, then every list's candidates at or above it
-  auto ld = [&](long long at) { return __hip_atomic_load(wr + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  // merge (the row's last arrival): the floor from the headers, then every list's entries at or above it
+  auto ld = [&](const u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   u64 kmax = 0, qmn = ~0ull;
   for (int c = threadIdx.x; c < nchunks; c += kThreads) {
-    counts[c] = (int)ld((long long)c * kWideSlot);
-    const u64 kb = ld((long long)c * kWideSlot + 1), qb = ld((long long)c * kWideSlot + 2);
+    const u64 h = ld(heads + c);
+    const u64 kb = h & 0xffffffff00000000ull, qb = h << 32;
     kmax = kb > kmax ? kb : kmax;
     qmn = qb < qmn ? qb : qmn;
   }
@@ -1493,15 +1508,16 @@ __global__ void __launch_bounds__(kThreads)
     s.thr = floor;
   }
   __syncthreads();
-  constexpr int PER = kWideList / kThreads;
-  constexpr int kInFlight = 2;  // lists whose loads are in flight while one is taken (4 measured no faster)
+  constexpr int PER = kMaxK / kThreads;  // list entries per thread (k <= kMaxK)
+  constexpr int kInFlight = 2;           // lists whose loads are in flight while one is taken (4 measured no faster)
+  static_assert(PER * kThreads <= kWideCap - kWideList, "room for a whole list above a buffer of kWideList");
   u64 cv[kInFlight][PER];
   auto load = [&](int c, u64 (&v)[PER]) {
-    const int cnt = counts[c];
+    const u64* list = wr + (long long)c * k;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int at = i * kThreads + (int)threadIdx.x;
-      v[i] = at < cnt ? ld((long long)c * kWideSlot + kWideHead + at) : 0ull;
+      v[i] = at < k ? ld(list + at) : 0ull;
     }
   };
   auto take = [&](const u64 (&v)[PER]) {  // appends the entries at or above the floor (room for a list is kept)
@@ -1531,8 +1547,7 @@ __global__ void __launch_bounds__(kThreads)
   }
   if (s.count > kWideList) prune(s, k);
   write_ranked<T>(s, s.count, k, values, indices, row, floor);  // every candidate kept is at or above the floor
-  if (threadIdx.x == 0)
-    __hip_atomic_store(arrivals + row * kArrivalStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   sample_list<T>(sa, u, values, indices, row, k);
 }
 
@@ -1554,11 +1569,12 @@ __global__ void __launch_bounds__(kWave)
 
 // Tuning slot (0 = automatic): 0 resident workgroups per CU assumed by plan().
 enum { kTuneBlocksPerCu = 0 };
-constexpr int kArrivalsPurpose = 2;  // stream_workspace key of the arrival counters
-constexpr int kListsPurpose = 3;     // stream_workspace key of the 64 < k kernel's published lists
 
+// The kernels of a launch whose rows are split into nchunks chunks of `chunk` columns. work and counters are the
+// caller's (work: u64 [rows * nchunks * k]; counters: u32 [rows], zero); the launch may join chunks (fewer, longer
+// ones), which keeps every slot it uses inside that work.
 template <typename T, bool VEC>
-int launch_chunks(const void* x, void* values, void* indices, void* work, long long rows,
+int launch_chunks(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
                   long long cols, long long chunk, int nchunks, int k, const SampleArgs& sa, hipStream_t stream) {
   if (k <= kSeedMaxK) {
     // A last chunk too short to give each of the four waves a vector would leave a wave without a bound, and the tile
@@ -1567,44 +1583,34 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, long l
     if (nchunks > 1 && tail < (long long)kThreads * Tile<T, VEC>::W && chunk + tail <= (long long)kThreads * kTileE)
       --nchunks;
     const dim3 grid((unsigned)nchunks, (unsigned)rows);
-    unsigned* arrivals = nullptr;
-    if (nchunks > 1) {  // the arrival counters: zeros between launches, kept per (device, stream)
-      int err = rw_host::kOk;
-      arrivals = (unsigned*)rw_host::stream_workspace(stream, (size_t)rows * kArrivalStride * sizeof(unsigned), &err,
-                                                      kArrivalsPurpose, true);
-      if (!arrivals) return err;
-    }
     if (k == 1)
       hipLaunchKernelGGL((topk_tile<T, VEC, true>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
-                         (long long*)indices, (u64*)work, arrivals, cols, chunk, nchunks, k, sa);
+                         (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k, sa);
     else
       hipLaunchKernelGGL((topk_tile<T, VEC, false>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
-                         (long long*)indices, (u64*)work, arrivals, cols, chunk, nchunks, k, sa);
+                         (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k, sa);
     return (int)hipGetLastError();
   }
   // The result does not depend on the chunking, so the chunks are made long enough for a useful bound (16k elements:
-  // a tile holds the 4 * ceil(k / 4) group maxima the bound needs) and few enough for the merge (kWideMaxChunks).
+  // a tile holds the 4 * ceil(k / 4) group maxima the bound needs) and few enough for the merge: at most
+  // kWideMaxChunks, and at most k, so that the chunks' bound headers fit the row's output indices.
+  const long long most = k < kWideMaxChunks ? k : kWideMaxChunks;
   long long want = 16LL * k;
-  if (want < (cols + kWideMaxChunks - 1) / kWideMaxChunks) want = (cols + kWideMaxChunks - 1) / kWideMaxChunks;
+  if (want < (cols + most - 1) / most) want = (cols + most - 1) / most;
   if (chunk < want && nchunks > 1) {
     chunk = want < cols ? (want + 7) / 8 * 8 : cols;
     nchunks = (int)((cols + chunk - 1) / chunk);
   }
-  unsigned* arrivals = nullptr;
-  u64* lists = nullptr;
-  if (nchunks > 1) {
-    int err = rw_host::kOk;
-    arrivals = (unsigned*)rw_host::stream_workspace(stream, (size_t)rows * kArrivalStride * sizeof(unsigned), &err,
-                                                    kArrivalsPurpose, true);
-    if (!arrivals) return err;
-    lists = (u64*)rw_host::stream_workspace(stream, (size_t)rows * nchunks * kWideSlot * sizeof(u64), &err,
-                                            kListsPurpose);
-    if (!lists) return err;
-  }
   const dim3 wgrid((unsigned)nchunks, (unsigned)rows);
   hipLaunchKernelGGL((topk_wide<T, VEC>), wgrid, dim3(kThreads), 0, stream, (const T*)x, values, (long long*)indices,
-                     lists, arrivals, cols, chunk, nchunks, k, sa);
+                     (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k, sa);
   return (int)hipGetLastError();
+}
+
+// Zeroes counters[0, n).
+__global__ void __launch_bounds__(kThreads) topk_zero(unsigned* __restrict__ counters, long long n) {
+  for (long long i = (long long)blockIdx.x * kThreads + threadIdx.x; i < n; i += (long long)gridDim.x * kThreads)
+    counters[i] = 0u;
 }
 
 }  // namespace
@@ -1644,30 +1650,34 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
 }
 
 // topk/kernel.cu:549 `launch`: values [rows, k] in x's dtype and int64 indices [rows, k], sorted descending with ties
-// by the lowest index. work: u64 [rows * nchunks * k] with nchunks = ceil(cols / chunk), the chunk lists of split rows
-// for k <= 64 (for k > 64 they go through a workspace of the library's); counters: u32 [>= rows], zero on entry and
-// left zero (the arrivals are counted in the library's counters, kept per device and stream). Checks as the
-// reference's, except that k may be up to 1024 (the reference stops at 512): rows <= 0 or k <= 0 is a no-op; -1 for k
-// > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0, a split row with chunk % 4 or nchunks * k > INT_MAX
-// / 2, threads not 128, 256 or 512, depth not 2, 4 or 8, or a dtype other than 0 and 1.
+// by the lowest index. work: u64 [rows * nchunks * k] with nchunks = ceil(cols / chunk), the chunk lists of split rows;
+// counters: u32 [>= rows], zero on entry and left zero (each split row's arrivals are counted on counters[row] and its
+// last arrival zeroes it). Both belong to the caller, as in the reference (topk/candidate.py:38-63), and the library
+// allocates nothing. Checks as the reference's, except that k may be up to 1024 (the reference stops at 512): rows <= 0
+// or k <= 0 is a no-op; -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0, a split row with
+// chunk % 4 or nchunks * k > INT_MAX / 2, threads not 128, 256 or 512, depth not 2, 4 or 8, a dtype other than 0 and
+// 1, or (this build's addition) a split row with a null work or counters.
 namespace {
-int launch_impl(const void* x, void* values, void* indices, void* work, long long rows, long long cols, int k,
-                int dtype, int threads, int depth, long long chunk, const SampleArgs& sa, hipStream_t stream) {
+int launch_impl(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
+                long long cols, int k, int dtype, int threads, int depth, long long chunk, const SampleArgs& sa,
+                hipStream_t stream) {
   if (rows <= 0 || k <= 0) return rw_host::kOk;
   if (k > cols || k > kMaxK || cols > INT_MAX / 2 || rows > 65535 || chunk <= 0) return rw_host::kInvalid;
   const long long nchunks = (cols + chunk - 1) / chunk;
   if (nchunks > 1 && (chunk % 4 || nchunks * k > INT_MAX / 2)) return rw_host::kInvalid;
   if ((threads != 128 && threads != 256 && threads != 512) || (depth != 2 && depth != 4 && depth != 8))
     return rw_host::kInvalid;
+  if (nchunks > 1 && (!work || !counters)) return rw_host::kInvalid;
+  const int n = (int)nchunks;
   if (dtype == 0) {
     if (cols % 4 == 0 && rw_host::aligned16(x))
-      return launch_chunks<float, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, sa, stream);
-    return launch_chunks<float, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, sa, stream);
+      return launch_chunks<float, true>(x, values, indices, work, counters, rows, cols, chunk, n, k, sa, stream);
+    return launch_chunks<float, false>(x, values, indices, work, counters, rows, cols, chunk, n, k, sa, stream);
   }
   if (dtype == 1) {
     if (cols % 8 == 0 && (chunk % 8 == 0 || nchunks == 1) && rw_host::aligned16(x))
-      return launch_chunks<uint16_t, true>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, sa, stream);
-    return launch_chunks<uint16_t, false>(x, values, indices, work, rows, cols, chunk, (int)nchunks, k, sa, stream);
+      return launch_chunks<uint16_t, true>(x, values, indices, work, counters, rows, cols, chunk, n, k, sa, stream);
+    return launch_chunks<uint16_t, false>(x, values, indices, work, counters, rows, cols, chunk, n, k, sa, stream);
   }
   return rw_host::kInvalid;
 }
@@ -1675,8 +1685,7 @@ int launch_impl(const void* x, void* values, void* indices, void* work, long lon
 
 extern "C" int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
                       long long cols, int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream) {
-  (void)counters;
-  return launch_impl(x, values, indices, work, rows, cols, k, dtype, threads, depth, chunk,
+  return launch_impl(x, values, indices, work, counters, rows, cols, k, dtype, threads, depth, chunk,
                      SampleArgs{nullptr, nullptr, 0.0f, 0.0f}, stream);
 }
 
@@ -1689,21 +1698,21 @@ extern "C" int topk_launch_sample(const void* x, void* values, void* indices, vo
                                   long long rows, long long cols, int k, int dtype, int threads, int depth,
                                   long long chunk, const float* uniforms, void* out, float temperature, float top_p,
                                   hipStream_t stream) {
-  (void)counters;
   if (rows > 0 && k > 0 && (!uniforms || !out)) return rw_host::kInvalid;
-  return launch_impl(x, values, indices, work, rows, cols, k, dtype, threads, depth, chunk,
+  return launch_impl(x, values, indices, work, counters, rows, cols, k, dtype, threads, depth, chunk,
                      SampleArgs{uniforms, (long long*)out, temperature, top_p}, stream);
 }
 
 // No counterpart in the reference (whose counters self-reset only when a launch completes): zeroes counters[0, rows)
-// and the library's arrival counters for `stream` on `stream`, for a caller recovering from a launch that did not
-// complete.
+// on `stream` with a small kernel (no memset node, so the call may be captured into a graph), for a caller recovering
+// from a launch that did not complete.
 extern "C" int topk_reset(void* counters, long long rows, hipStream_t stream) {
   if (rows <= 0) return rw_host::kOk;
   if (!counters) return rw_host::kInvalid;
-  const int e = (int)hipMemsetAsync(counters, 0, (size_t)rows * sizeof(unsigned), stream);
-  if (e != rw_host::kOk) return e;
-  return rw_host::clear_stream_workspace(stream, kArrivalsPurpose);
+  long long grid = (rows + kThreads - 1) / kThreads;
+  if (grid > 1024) grid = 1024;
+  hipLaunchKernelGGL(topk_zero, dim3((unsigned)grid), dim3(kThreads), 0, stream, (unsigned*)counters, rows);
+  return (int)hipGetLastError();
 }
 
 // Sampling from a top-k list (no counterpart in the reference: the step after top-k in a decoder's sampler; see

@@ -1,14 +1,25 @@
-"""RMSNorm candidate wrapper: loads its kernel build, allocates y and launches the kernel.
+"""RMSNorm over the last dimension, served by this package's MI355X library through the reference's C entry point.
 
-y = x times rsqrt(the mean of x^2 over the last dim + eps) for x[rows, cols] in bf16 (1) or fp16 (2), with that rsqrt
-rounded to x's dtype before the product (the reference's rmsnorm/candidate.py:3-4 and kernel.cu:1-8); eps is 1e-6
-unless inputs["eps"] is given. With inputs["weight"] (a [cols] tensor of x's dtype) the result is weight * y, rounded
-once more to the dtype, through the library's `rmsnorm_launch_weighted`; without it, through the reference ABI's
-`launch`. x is passed contiguous. params.json (optional) may set "threads" (a multiple of 32 from 32 to 1024, default
-256), validated as the reference does. The library is $CKOPT_BUILD_DIR/libkernel.so when CKOPT_BUILD_DIR is set, else
-this package's build/rmsnorm/libkernel.so. With inputs["residual"] (x's dtype and shape) the call is the fused residual
-add (no counterpart in the reference): h = x + residual is returned as "residual" (written over the given tensor when
-inputs["inplace"] is true) and y = rmsnorm(h), times weight when given, through `rmsnorm_add_launch`.
+Contract (the reference's rmsnorm/candidate.py:25-50 and its entry point rmsnorm/kernel.cu:132): run({"x": x}) with
+x a 2-D bf16 (dtype code 1) or fp16 (code 2) GPU tensor returns {"y": y}, y = x * inv for each row, where inv is
+1 / sqrt(mean(x^2) + eps) rounded to x's dtype before the product (rmsnorm/kernel.cu:1-8). eps defaults to 1e-6;
+inputs["eps"] overrides it.
+
+Additions of this build (no counterpart in the reference):
+  - inputs["weight"], a [cols] tensor of x's dtype: y = weight * (x * inv), the product rounded to the dtype again
+    (entry point rmsnorm_launch_weighted);
+  - inputs["residual"], x's dtype and shape: the residual add fused in front of the norm. h = x + residual comes back
+    as "residual" (it overwrites the given tensor when inputs["inplace"] is true) and y = rmsnorm(h), weighted when a
+    weight is given (entry point rmsnorm_add_launch).
+
+Library: libkernel.so from the directory named by CKOPT_BUILD_DIR, or this package's build/rmsnorm/ when that variable
+is unset. A missing library is an ImportError; there is no CPU path.
+
+Tuning file: an optional params.json beside this file may hold "threads" (default 256). The C entry point validates it
+as the reference does (a multiple of 32 in [32, 1024]); the MI355X kernels choose their own launch shape.
+
+Errors: ValueError before any launch for an input the kernels do not take, RuntimeError carrying the HIP error code
+when the launch reports one.
 """
 
 import ctypes
@@ -18,34 +29,43 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_PARAMS_PATH = os.path.join(_HERE, "params.json")
-_params = {}
-if os.path.exists(_PARAMS_PATH):
-    with open(_PARAMS_PATH) as _handle:
-        _params = json.load(_handle)
-_THREADS = int(_params.get("threads", 256))
-_EPS = 1e-6
-_DTYPES = {torch.bfloat16: 1, torch.float16: 2}
+
+
+def _tuning():
+    path = os.path.join(_HERE, "params.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f)
+
+
+_TUNING = _tuning()
+_THREADS = int(_TUNING.get("threads", 256))
+_DEFAULT_EPS = 1e-6
+_CODE = {torch.bfloat16: 1, torch.float16: 2}
 
 LIB_PATH = os.path.join(os.environ.get("CKOPT_BUILD_DIR") or os.path.join(_HERE, "..", "build", "rmsnorm"),
                         "libkernel.so")
 if not os.path.exists(LIB_PATH):
-    raise ImportError(f"rmsnorm: {LIB_PATH} is missing (build it with make_libs.py)")
+    raise ImportError(f"rmsnorm: no library at {LIB_PATH}; run make_libs.py first")
 _lib = ctypes.CDLL(LIB_PATH)
+# int launch(const void* x, void* y, long long rows, int cols, int dtype, float eps, int threads, hipStream_t)
 _lib.launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
                         ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
 _lib.launch.restype = ctypes.c_int
+# int rmsnorm_launch_weighted(x, weight, y, rows, cols, dtype, eps, threads, stream)
 _lib.rmsnorm_launch_weighted.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong,
                                          ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
 _lib.rmsnorm_launch_weighted.restype = ctypes.c_int
+# int rmsnorm_add_launch(x, residual, weight, y, residual_out, rows, cols, dtype, eps, threads, stream)
 _lib.rmsnorm_add_launch.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
                                                              ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
 _lib.rmsnorm_add_launch.restype = ctypes.c_int
 
 
-def _problem(x, w):
-    """Why x (and w) are not inputs this kernel serves, or None."""
-    if x.dtype not in _DTYPES:
+def _reject(x, w, r):
+    """A short reason when x (with its optional weight w and residual r) cannot go to the kernels, else None."""
+    if x.dtype not in _CODE:
         return f"dtype {x.dtype}"
     if x.dim() != 2 or x.shape[1] < 1:
         return f"shape {tuple(x.shape)}"
@@ -53,40 +73,38 @@ def _problem(x, w):
         return f"device {x.device}"
     if w is not None and (w.dtype != x.dtype or tuple(w.shape) != (x.shape[1],) or w.device != x.device):
         return f"weight {w.dtype} {tuple(w.shape)} on {w.device}"
+    if r is not None and (r.dtype != x.dtype or r.shape != x.shape or r.device != x.device):
+        return f"residual {r.dtype} {tuple(r.shape)} on {r.device}"
     return None
 
 
+def _checked(err):
+    if err:
+        raise RuntimeError(f"kernel launch failed: HIP error {err}")
+
+
 def run(inputs):
-    x = inputs["x"]
-    w = inputs.get("weight")
-    r = inputs.get("residual")
-    eps = float(inputs.get("eps", _EPS))
-    problem = _problem(x, w)
-    if problem is None and r is not None and (r.dtype != x.dtype or r.shape != x.shape or r.device != x.device):
-        problem = f"residual {r.dtype} {tuple(r.shape)} on {r.device}"
-    if problem:
-        raise ValueError(f"rmsnorm candidate: {problem}")
+    x, w, r = inputs["x"], inputs.get("weight"), inputs.get("residual")
+    eps = float(inputs.get("eps", _DEFAULT_EPS))
+    reason = _reject(x, w, r)
+    if reason:
+        raise ValueError(f"rmsnorm candidate: {reason}")
     x = x.contiguous()
     y = torch.empty_like(x)
     rows, cols = x.shape
+    code = _CODE[x.dtype]
     stream = torch.cuda.current_stream(x.device).cuda_stream
+    w = w.contiguous() if w is not None else None  # held until the launch is queued
+    wp = w.data_ptr() if w is not None else None
     if r is not None:
-        # fused residual add: h = x + residual goes to "residual" (in place when inputs["inplace"] and the given
-        # residual is contiguous), y = rmsnorm(h) [* weight]
         r_in = r.contiguous()
+        # h goes over the caller's residual only when asked to and when that tensor is the one the kernel reads
         h = r_in if inputs.get("inplace") and r_in.data_ptr() == r.data_ptr() else torch.empty_like(x)
-        wp = w.contiguous().data_ptr() if w is not None else None
-        err = _lib.rmsnorm_add_launch(x.data_ptr(), r_in.data_ptr(), wp, y.data_ptr(), h.data_ptr(), rows, cols,
-                                      _DTYPES[x.dtype], eps, _THREADS, stream)
-        if err:
-            raise RuntimeError(f"kernel launch failed: HIP error {err}")
+        _checked(_lib.rmsnorm_add_launch(x.data_ptr(), r_in.data_ptr(), wp, y.data_ptr(), h.data_ptr(), rows, cols,
+                                         code, eps, _THREADS, stream))
         return {"y": y, "residual": h}
-    if w is None:
-        err = _lib.launch(x.data_ptr(), y.data_ptr(), rows, cols, _DTYPES[x.dtype], eps, _THREADS, stream)
+    if wp is None:
+        _checked(_lib.launch(x.data_ptr(), y.data_ptr(), rows, cols, code, eps, _THREADS, stream))
     else:
-        w = w.contiguous()
-        err = _lib.rmsnorm_launch_weighted(x.data_ptr(), w.data_ptr(), y.data_ptr(), rows, cols, _DTYPES[x.dtype], eps,
-                                           _THREADS, stream)
-    if err:
-        raise RuntimeError(f"kernel launch failed: HIP error {err}")
+        _checked(_lib.rmsnorm_launch_weighted(x.data_ptr(), wp, y.data_ptr(), rows, cols, code, eps, _THREADS, stream))
     return {"y": y}

@@ -1,11 +1,18 @@
-"""Softmax candidate wrapper: loads its kernel build, allocates y and launches the kernel.
+"""Softmax over the last dimension, served by this package's MI355X library through the reference's C entry point.
 
-y = softmax(x) over the last dim of x in fp32 (dtype 0) or bf16 (1), every value accumulated in fp32 and rounded once,
-with the run(inputs) -> {"y": y} contract of the reference's softmax/baseline.py:12-13 (the reference ships no softmax
-candidate; its ABI is softmax/kernel.cu:520). The one `launch` entry of libkernel.so serves both dtypes; x is passed
-contiguous and its leading dims are flattened into rows. params.json (optional) may set "threads" and "aux", the
-reference ABI's block-size hints, which this build accepts and does not need. The library is
-$CKOPT_BUILD_DIR/libkernel.so when CKOPT_BUILD_DIR is set, else this package's build/softmax/libkernel.so.
+Contract (the same shape as the reference's softmax/baseline.py:12-13, whose entry point is softmax/kernel.cu:520):
+run({"x": x}) returns {"y": y}, y holding softmax(x) along x's last dimension. x may be fp32 (dtype code 0) or bf16
+(code 1) and have any number of leading dimensions, which become rows. Sums and exponentials are taken in fp32 and
+each output element is rounded once.
+
+Library: libkernel.so from the directory named by CKOPT_BUILD_DIR, or this package's build/softmax/ when that variable
+is unset. A missing library is an ImportError; there is no CPU path.
+
+Tuning file: an optional params.json beside this file may hold "threads" and "aux". The C entry point checks nothing
+about them and the MI355X kernels pick their own launch shape, so they only travel through.
+
+Errors: ValueError before any launch for an input the kernels do not take, RuntimeError carrying the HIP error code
+when the launch reports one.
 """
 
 import ctypes
@@ -15,28 +22,35 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_PARAMS_PATH = os.path.join(_HERE, "params.json")
-_params = {}
-if os.path.exists(_PARAMS_PATH):
-    with open(_PARAMS_PATH) as _handle:
-        _params = json.load(_handle)
-_THREADS = int(_params.get("threads", 256))
-_AUX = int(_params.get("aux", 1024))
-_DTYPES = {torch.float32: 0, torch.bfloat16: 1}
+
+
+def _tuning():
+    path = os.path.join(_HERE, "params.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f)
+
+
+_TUNING = _tuning()
+_THREADS = int(_TUNING.get("threads", 256))
+_AUX = int(_TUNING.get("aux", 1024))
+_CODE = {torch.float32: 0, torch.bfloat16: 1}
 
 LIB_PATH = os.path.join(os.environ.get("CKOPT_BUILD_DIR") or os.path.join(_HERE, "..", "build", "softmax"),
                         "libkernel.so")
 if not os.path.exists(LIB_PATH):
-    raise ImportError(f"softmax: {LIB_PATH} is missing (build it with make_libs.py)")
+    raise ImportError(f"softmax: no library at {LIB_PATH}; run make_libs.py first")
 _lib = ctypes.CDLL(LIB_PATH)
+# int launch(const void* x, void* y, long long rows, long long cols, int dtype, int threads, int aux, hipStream_t)
 _lib.launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_longlong, ctypes.c_int,
                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
 _lib.launch.restype = ctypes.c_int
 
 
-def _problem(x):
-    """Why x is not an input this kernel serves, or None."""
-    if x.dtype not in _DTYPES:
+def _reject(x):
+    """A short reason when x cannot go to the kernels, else None."""
+    if x.dtype not in _CODE:
         return f"dtype {x.dtype}"
     if x.dim() < 1:
         return f"shape {tuple(x.shape)}"
@@ -47,14 +61,14 @@ def _problem(x):
 
 def run(inputs):
     x = inputs["x"]
-    problem = _problem(x)
-    if problem:
-        raise ValueError(f"softmax candidate: {problem}")
+    reason = _reject(x)
+    if reason:
+        raise ValueError(f"softmax candidate: {reason}")
     x = x.contiguous()
     y = torch.empty_like(x)
     cols = x.shape[-1]
     rows = x.numel() // cols if cols else 0
-    err = _lib.launch(x.data_ptr(), y.data_ptr(), rows, cols, _DTYPES[x.dtype], _THREADS, _AUX,
+    err = _lib.launch(x.data_ptr(), y.data_ptr(), rows, cols, _CODE[x.dtype], _THREADS, _AUX,
                       torch.cuda.current_stream(x.device).cuda_stream)
     if err:
         raise RuntimeError(f"kernel launch failed: HIP error {err}")

@@ -1,12 +1,10 @@
 /* topk: the k largest entries of each row of x[rows, cols] in fp32 (dtype 0) or bf16 (dtype 1), sorted descending with
  * ties broken by the lowest index (+0 above -0, +NaN above +inf, -NaN at the bottom: the composite order of the
  * reference), 1 <= k <= 1024. Library: build/topk/libkernel.so. Replaces the reference's topk/kernel.cu:520-570 (ctypes
- * binding topk/candidate.py:31-36). Device pointers; asynchronous on `stream`. The caller owns the workspace and
- * counters; a split row's chunks count their arrivals in counters of the library's own instead (one per 256 bytes,
- * so that the rows' counting atomics do not share a line, all zeros between launches; for k = 1 the row's best
- * composite so far sits beside its counter, so no list is handed over), and for k > 64 hand their
- * candidate lists over in a workspace of the library's (up to 2052 u64 per chunk); both are allocated on first use
- * per (device, stream) and grown when a launch needs more. */
+ * binding topk/candidate.py:31-36). Device pointers; asynchronous on `stream`. As in the reference, the caller owns
+ * the workspace and the counters (topk/candidate.py:38-63) and the library allocates nothing and keeps no device
+ * state: a split row's chunks hand their results over in the caller's work and count their arrivals on the caller's
+ * counters[row]. */
 #ifndef ROWKERN_TOPK_H
 #define ROWKERN_TOPK_H
 #include <hip/hip_runtime_api.h>
@@ -21,19 +19,23 @@ extern "C" {
 long long plan(long long rows, long long cols, int dtype, int threads, int depth, int min_chunk);
 
 /* topk/kernel.cu:549: values [rows, k] in x's dtype, indices [rows, k] int64; work: u64 [rows * nchunks * k]
- * (nchunks = ceil(cols / chunk); the chunk lists of split rows for k <= 64); counters: u32 [>= rows], zero on entry
- * and left zero (a split row's last chunk to arrive merges, as in the reference, counted in the library's counters; for
- * k > 64 a row is split into at most 256 chunks, longer than `chunk` when needed, as the result does not depend on
- * the chunking).
+ * (nchunks = ceil(cols / chunk)), the chunk results of split rows; counters: u32 [>= rows], zero on entry and left
+ * zero (a split row's last chunk to arrive merges, as in the reference, and zeroes counters[row]). The launch may join
+ * chunks into fewer, longer ones, which stays inside that work: for k <= 64 a last chunk too short to give each of
+ * a workgroup's four waves a 16-byte vector is folded into the previous chunk when the two fit one 16384-element
+ * register tile; for k > 64 a row is split into at most min(256, k) chunks of at least 16k columns (the result does
+ * not depend on the chunking). For k > 64 the chunks also leave their bounds in the row's indices before the merge
+ * writes them.
  * Returns 0 (rows <= 0 or k <= 0 is a no-op), -1 for k > cols, k > 1024, cols > INT_MAX / 2, rows > 65535, chunk <= 0,
- * a split row with chunk % 4 != 0 or nchunks * k > INT_MAX / 2, threads not 128/256/512, depth not 2/4/8 or an unknown
- * dtype, otherwise the hipError_t of the launch. Launches sharing work/counters must be ordered (one stream). */
+ * a split row with chunk % 4 != 0 or nchunks * k > INT_MAX / 2, threads not 128/256/512, depth not 2/4/8, an unknown
+ * dtype or (this build's addition) a split row with a null work or counters, otherwise the hipError_t of the launch.
+ * Launches sharing work/counters must be ordered (one stream). */
 int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows, long long cols,
            int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream);
 
 /* No counterpart in the reference (whose counters self-reset only when a launch completes): zeroes counters[0, rows)
- * and the library's arrival counters for `stream` on `stream`, for a caller recovering from a launch that did not
- * complete. Returns 0, -1 (NULL counters) or the hipError_t of a memset. */
+ * on `stream` with a small kernel, for a caller recovering from a launch that did not complete. Returns 0, -1 (NULL
+ * counters) or the hipError_t of the launch. */
 int topk_reset(void* counters, long long rows, hipStream_t stream);
 
 /* No counterpart in the reference (the step after top-k in a decoder's sampler): one index per row drawn

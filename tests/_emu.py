@@ -1,7 +1,8 @@
 """Builds a kernel source file from the package's csrc/ as a CPU program under the HIP emulation in tests/emu/.
 
 The source is compiled as the library builds it, except that its inline asm statements (scheduling fences and waits
-for the memory counters, which have no meaning on the CPU) become no-ops. It is linked with a driver from tests/emu/
+for the memory counters) go to the emulation's hook, where `s_waitcnt vmcnt(0)` makes the lane's pending stores
+visible in the weak mode and everything else is a no-op. It is linked with a driver from tests/emu/
 and the oracle's C restatement, which the driver compares the kernels' outputs with.
 """
 
@@ -30,11 +31,7 @@ def build(tmpdir, source, driver):
     if clang is None or shutil.which("gcc") is None:
         pytest.skip("clang++ (for the kernels' vector extensions on the host) or gcc is missing")
     stem = os.path.splitext(source)[0]
-    with open(os.path.join(CSRC, source)) as f:
-        src = f.read().replace("asm volatile(", "EMU_ASM(")
-    kern = os.path.join(str(tmpdir), stem + "_emu.cpp")
-    with open(kern, "w") as f:
-        f.write(src)
+    kern = kernel_source(tmpdir, source)
     obj = os.path.join(str(tmpdir), "oracle.o")
     if not os.path.exists(obj):
         subprocess.run(["gcc", "-O2", "-c", os.path.join(ROOT, "oracle", "oracle.c"), "-o", obj], check=True)
@@ -46,13 +43,62 @@ def build(tmpdir, source, driver):
     return exe
 
 
-def run(exe, args, env=None, timeout=600, concurrent=False):
-    """Runs the emulation with the given arguments and asserts that it reports ALL OK. concurrent: every workgroup on an
-    OS thread of its own, all at once (EMU_CONCURRENT)."""
+def kernel_source(tmpdir, source):
+    """csrc/<source> with its inline asm statements routed to the emulation's hook; returns the path of the copy."""
+    stem = os.path.splitext(source)[0]
+    with open(os.path.join(CSRC, source)) as f:
+        src = f.read().replace("asm volatile(", "EMU_ASM(")
+    kern = os.path.join(str(tmpdir), stem + "_emu.cpp")
+    with open(kern, "w") as f:
+        f.write(src)
+    return kern
+
+
+def build_shared(tmpdir, source, name):
+    """Compiles csrc/<source> alone into a shared object tmpdir/name (the emulation's runtime inside it)."""
+    clang = _clang()
+    if clang is None:
+        pytest.skip("clang++ (for the kernels' vector extensions on the host) is missing")
+    out = os.path.join(str(tmpdir), name)
+    proc = subprocess.run([clang, "-std=c++17", "-O1", "-fPIC", "-shared", "-U_FORTIFY_SOURCE", "-D_FORTIFY_SOURCE=0",
+                           "-fno-strict-aliasing", "-w", "-pthread", "-I", EMU, "-I", CSRC,
+                           kernel_source(tmpdir, source), "-o", out], capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stderr[-4000:]
+    return out
+
+
+def build_driver(tmpdir, driver, libs=("-ldl",)):
+    """Compiles tests/emu/<driver> with the oracle's C restatement (no kernel source) into an executable."""
+    clang = _clang()
+    if clang is None or shutil.which("gcc") is None:
+        pytest.skip("clang++ or gcc is missing")
+    obj = os.path.join(str(tmpdir), "oracle_pic.o")
+    if not os.path.exists(obj):
+        subprocess.run(["gcc", "-O2", "-fPIC", "-c", os.path.join(ROOT, "oracle", "oracle.c"), "-o", obj], check=True)
+    exe = os.path.join(str(tmpdir), os.path.splitext(driver)[0])
+    # -rdynamic: the emulation runtime's state (allocation count, schedules) is the driver's, shared by every library
+    # the driver opens; each library keeps its own kernels and statics
+    proc = subprocess.run([clang, "-std=c++17", "-O1", "-w", "-pthread", "-rdynamic", "-I", EMU,
+                           os.path.join(EMU, driver), obj, "-o", exe, "-lm", *libs], capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stderr[-4000:]
+    return exe
+
+
+def run(exe, args, env=None, timeout=600, concurrent=False, weak=False, expect_ok=True):
+    """Runs the emulation with the given arguments and asserts that it reports ALL OK (or, with expect_ok False, that
+    it reports a failure). concurrent: every workgroup on an OS thread of its own, all at once (EMU_CONCURRENT). weak:
+    agent-scope stores become visible late and out of order (EMU_WEAK)."""
     env = dict(os.environ if env is None else env)
-    env.pop("EMU_CONCURRENT", None)
+    for var in ("EMU_CONCURRENT", "EMU_WEAK"):
+        env.pop(var, None)
     if concurrent:
         env["EMU_CONCURRENT"] = "1"
+    if weak:
+        env["EMU_WEAK"] = "1"
     proc = subprocess.run([exe, *[str(a) for a in args]], capture_output=True, text=True, timeout=timeout, env=env)
     out = proc.stdout + proc.stderr
-    assert proc.returncode == 0 and "ALL OK" in proc.stdout, f"{args}: rc {proc.returncode}\n{out[-3000:]}"
+    if expect_ok:
+        assert proc.returncode == 0 and "ALL OK" in proc.stdout, f"{args}: rc {proc.returncode}\n{out[-3000:]}"
+    else:
+        assert proc.returncode != 0 and "FAILED" in proc.stdout, f"{args}: expected a failure\n{out[-3000:]}"
+    return out

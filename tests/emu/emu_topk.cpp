@@ -1,9 +1,9 @@
 // Runs csrc/topk.hip's plan() and launch() under the CPU emulation (hip/hip_runtime.h beside this file) and compares
 // every launch with the oracle (oracle/oracle.c: oracle_topk), bit for bit: values, int64 indices, and the caller's
-// counters left at zero. Each launch is followed by topk_launch_sample(), whose values, indices and draws must equal
+// counters left at zero; a launch must not allocate (the caller's work and counters carry the hand-off). Each launch is followed by topk_launch_sample(), whose values, indices and draws must equal
 // launch()'s and topk_sample_launch()'s on them, and the draws the oracle's (oracle_topk_sample) wherever the uniform
-// is not within its tolerance band of an interval edge. Every buffer the kernels touch (input, outputs, work, counters
-// and the library's own workspaces) lies between guard pages.
+// is not within its tolerance band of an interval edge. Every buffer the kernels touch (input, outputs, work and
+// counters) lies between guard pages.
 //
 // usage: emu_topk rows cols dtype ks chunk min_chunk reps seed [shuffle_seed [pattern]]
 //   dtype 0 fp32, 1 bf16; ks comma-separated; chunk 0 takes plan()'s (min_chunk max 16k for k > 64, as the
@@ -111,7 +111,12 @@ int main(int argc, char** argv) {
     for (int rep = 0; rep < reps; ++rep) {
       std::memset(vals, 0xA5, rows * k * esz);
       std::memset(idx, 0xA5, rows * k * 8);
+      const long long m0 = emu::mallocs();
       const int err = launch(x, vals, idx, work, cnt, rows, cols, k, dtype, 256, 4, chunk, nullptr);
+      if (emu::mallocs() != m0) {
+        std::printf("k=%d chunk=%lld: launch allocated device memory\n", k, chunk);
+        ++bad;
+      }
       if (err) {
         std::printf("k=%d chunk=%lld: launch returned %d\n", k, chunk, err);
         ++bad;

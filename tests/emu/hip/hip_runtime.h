@@ -10,7 +10,15 @@
 //    thread_local static, so each workgroup's thread has its own;
 //  - device buffers lie between PROT_NONE pages (flush against the upper one, or against the lower one with
 //    EMU_ALIGN_START set) and start filled with 0xA5, so an access outside a buffer faults at once;
-//  - the atomics are sequentially consistent operations (fibers of one workgroup switch only at barriers).
+//  - the atomics are sequentially consistent operations (fibers of one workgroup switch only at barriers), except
+//    in the weak mode (EMU_WEAK set): there an agent-scope store (__hip_atomic_store) is held in its lane's queue of
+//    pending stores and becomes visible to other workgroups late and out of order -- a pending store drains at random
+//    at the lane's later atomic operations and barriers, all of the lane's drain at `s_waitcnt vmcnt(0)` (the wait
+//    that orders them before a later arrival count), and what a lane left pending when it ended drains one store at a
+//    time, now and then, while other lanes run, and wholly when the launch completes. A lane reads its own pending stores (same-address order is
+//    kept); atomic read-modify-writes act on memory at once. With EMU_DROP_VMCNT set as well, `s_waitcnt vmcnt(0)`
+//    drains nothing: the planted mistake that the weak mode must expose.
+//  - hipMalloc calls are counted (emu::mallocs()), so a driver can show that a launch allocates nothing.
 #pragma once
 #include <sched.h>
 #include <setjmp.h>
@@ -23,8 +31,10 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <atomic>
 #include <functional>
 #include <map>
+#include <mutex>
 #include <random>
 #include <thread>
 #include <vector>
@@ -35,7 +45,7 @@
 #define __forceinline__ inline
 #define __launch_bounds__(...)
 #define __shared__ static thread_local
-#define EMU_ASM(...) ((void)0)
+#define EMU_ASM(...) emu::asm_hook(#__VA_ARGS__)
 
 typedef int hipError_t;
 enum { hipSuccess = 0, hipErrorInvalidValue = 1 };
@@ -65,7 +75,14 @@ struct Bar {
   int line = -1;
 };
 
+struct Pending {
+  void* p;
+  uint64_t v;
+  int size;
+};
+
 struct Fiber {
+  std::vector<Pending> pending;  // the weak mode's stores not yet visible
   jmp_buf jb;
   ucontext_t uc;
   char* stack = nullptr;
@@ -114,6 +131,76 @@ inline int lid() { return flat() % kW; }
   std::abort();
 }
 
+// ---- the weak mode ------------------------------------------------------------------------------------------------
+inline bool weak() {
+  static const bool w = std::getenv("EMU_WEAK") != nullptr;
+  return w;
+}
+inline bool drop_vmcnt() {
+  static const bool d = std::getenv("EMU_DROP_VMCNT") != nullptr;
+  return d;
+}
+inline std::mutex& inflight_mu() {
+  static std::mutex m;
+  return m;
+}
+inline std::vector<Pending>& inflight() {  // stores of ended lanes, not yet visible
+  static std::vector<Pending> q;
+  return q;
+}
+inline void apply(const Pending& e) {
+  if (e.size == 8) __atomic_store_n((uint64_t*)e.p, e.v, __ATOMIC_SEQ_CST);
+  else if (e.size == 4) __atomic_store_n((uint32_t*)e.p, (uint32_t)e.v, __ATOMIC_SEQ_CST);
+  else if (e.size == 2) __atomic_store_n((uint16_t*)e.p, (uint16_t)e.v, __ATOMIC_SEQ_CST);
+  else __atomic_store_n((uint8_t*)e.p, (uint8_t)e.v, __ATOMIC_SEQ_CST);
+}
+inline void drain_all(std::vector<Pending>& q) {
+  for (const Pending& e : q) apply(e);
+  q.clear();
+}
+// Lets some pending stores (the lane's own, and some of ended lanes') become visible, out of order.
+inline void maybe_drain() {
+  State& s = S();
+  if (!s.cur) return;
+  std::vector<Pending>& q = s.cur->pending;
+  for (size_t i = 0; i < q.size();) {
+    if (s.rng() % 8 == 0) {
+      apply(q[i]);
+      q[i] = q.back();  // out of order, except that a lane keeps one entry per address (see store)
+      q.pop_back();
+    } else {
+      ++i;
+    }
+  }
+  if (s.rng() % 64 == 0) {  // now and then one store of an ended lane, picked at random
+    std::lock_guard<std::mutex> lock(inflight_mu());
+    std::vector<Pending>& g = inflight();
+    if (!g.empty()) {
+      const size_t i = s.rng() % g.size();
+      apply(g[i]);
+      g[i] = g.back();
+      g.pop_back();
+    }
+  }
+}
+inline void asm_hook(const char* text) {
+  if (!weak() || !S().cur) return;
+  if (std::strstr(text, "vmcnt(0)") && !drop_vmcnt()) drain_all(S().cur->pending);
+}
+template <typename T>
+inline Pending* own_pending(const T* p) {
+  State& s = S();
+  if (!s.cur) return nullptr;
+  for (Pending& e : s.cur->pending)
+    if (e.p == (const void*)p) return &e;
+  return nullptr;
+}
+inline std::atomic<long long>& malloc_count() {
+  static std::atomic<long long> n{0};
+  return n;
+}
+inline long long mallocs() { return malloc_count().load(); }
+
 inline void yield() {
   State& s = S();
   ++s.switches;
@@ -136,7 +223,10 @@ inline void arrive(Bar& b, int active, int line) {
   yield();
 }
 inline void wave_sync(int line) { arrive(S().wbar[wid()], S().wactive[wid()], line); }
-inline void block_sync(int line) { arrive(S().bbar, S().bactive, line); }
+inline void block_sync(int line) {
+  if (weak()) maybe_drain();
+  arrive(S().bbar, S().bactive, line);
+}
 
 inline bool lane_done(int w, int l) { return S().fib[w * kW + l].done; }
 
@@ -222,6 +312,11 @@ inline void trampoline() {
   State& s = S();
   s.body();
   Fiber* f = s.cur;
+  if (!f->pending.empty()) {  // a lane that ends leaves its stores in flight
+    std::lock_guard<std::mutex> lock(inflight_mu());
+    for (const Pending& e : f->pending) inflight().push_back(e);
+    f->pending.clear();
+  }
   f->done = true;
   const int w = (int)f->tid.x / kW;
   --s.wactive[w];
@@ -319,6 +414,7 @@ inline void launch(dim3 grid, dim3 block, std::function<void()> body) {
       s.block_idx = b;
       run_block();
     }
+    drain_all(inflight());  // the launch completes: every store is visible
     return;
   }
   // every workgroup on its own thread, with a state from the pool (kept for the next launch)
@@ -340,6 +436,7 @@ inline void launch(dim3 grid, dim3 block, std::function<void()> body) {
     });
   }
   for (std::thread& t : threads) t.join();
+  drain_all(inflight());
 }
 
 // Device buffers end at a PROT_NONE page (an access past the end faults at once) and start after one; contents start
@@ -392,15 +489,56 @@ inline void guarded_free(void* p) {
 #define __shfl_up(v, d, w) emu::shfl_up((v), (unsigned)(d), (int)(w), __LINE__)
 
 #define __HIP_MEMORY_SCOPE_AGENT 0
-#define __hip_atomic_load(p, o, sc) __atomic_load_n((p), __ATOMIC_SEQ_CST)
-#define __hip_atomic_store(p, v, o, sc) __atomic_store_n((p), (v), __ATOMIC_SEQ_CST)
+template <typename T>
+inline T emu_atomic_load(const T* p) {
+  if (emu::weak()) {
+    emu::maybe_drain();
+    if (emu::Pending* e = emu::own_pending(p)) {
+      T v;
+      std::memcpy(&v, &e->v, sizeof(T));
+      return v;
+    }
+  }
+  return __atomic_load_n(p, __ATOMIC_SEQ_CST);
+}
+template <typename T, typename U>
+inline void emu_atomic_store(T* p, U v) {
+  static_assert(sizeof(T) <= 8, "");
+  const T t = (T)v;
+  if (!emu::weak() || !emu::S().cur) {
+    __atomic_store_n(p, t, __ATOMIC_SEQ_CST);
+    return;
+  }
+  emu::maybe_drain();
+  uint64_t bits = 0;
+  std::memcpy(&bits, &t, sizeof(T));
+  if (emu::Pending* e = emu::own_pending(p)) e->v = bits;  // the later store to an address replaces the earlier
+  else emu::S().cur->pending.push_back(emu::Pending{(void*)p, bits, (int)sizeof(T)});
+}
+// A read-modify-write acts on memory at once, after the lane's own pending store to the same address.
+template <typename T>
+inline void emu_rmw_prepare(T* p) {
+  if (!emu::weak()) return;
+  emu::maybe_drain();
+  std::vector<emu::Pending>& q = emu::S().cur->pending;
+  for (size_t i = 0; i < q.size(); ++i)
+    if (q[i].p == (void*)p) {
+      emu::apply(q[i]);
+      q.erase(q.begin() + (long)i);
+      break;
+    }
+}
+#define __hip_atomic_load(p, o, sc) emu_atomic_load((p))
+#define __hip_atomic_store(p, v, o, sc) emu_atomic_store((p), (v))
 template <typename T, typename U>
 inline T emu_fetch_add(T* p, U v) {
+  if (emu::S().cur) emu_rmw_prepare(p);
   return __atomic_fetch_add(p, (T)v, __ATOMIC_SEQ_CST);
 }
 #define __hip_atomic_fetch_add(p, v, o, sc) emu_fetch_add((p), (v))
 template <typename T, typename U>
 inline T emu_fetch_max(T* p, U v) {
+  if (emu::S().cur) emu_rmw_prepare(p);
   T old = __atomic_load_n(p, __ATOMIC_SEQ_CST);
   while ((T)v > old && !__atomic_compare_exchange_n(p, &old, (T)v, false, __ATOMIC_SEQ_CST, __ATOMIC_SEQ_CST)) {
   }
@@ -409,7 +547,7 @@ inline T emu_fetch_max(T* p, U v) {
 #define __hip_atomic_fetch_max(p, v, o, sc) emu_fetch_max((p), (v))
 template <typename T, typename U>
 inline T atomicAdd(T* p, U v) {
-  return emu_fetch_add(p, v);
+  return __atomic_fetch_add(p, (T)v, __ATOMIC_SEQ_CST);  // LDS atomics (workgroup-local)
 }
 
 inline int __popcll(unsigned long long v) { return __builtin_popcountll(v); }
@@ -433,6 +571,7 @@ inline hipError_t hipOccupancyMaxActiveBlocksPerMultiprocessor(int* n, F, int, s
   return hipSuccess;
 }
 inline hipError_t hipMalloc(void** p, size_t n) {
+  ++emu::malloc_count();
   *p = emu::guarded_alloc(n);
   return *p ? hipSuccess : hipErrorInvalidValue;
 }

@@ -105,3 +105,24 @@ def test_wrappers_reject_bad_inputs_before_launch(pkg):
         pkg.rope(q, q, torch.zeros(1, 2, dtype=torch.int32), cos=torch.zeros(4, 64), sin=torch.zeros(4, 64))
     with pytest.raises(ValueError):
         pkg.rope(q, q, torch.zeros(1, 2, dtype=torch.int64), cos=torch.zeros(4, 64), sin=torch.zeros(4, 64))
+
+
+def test_topk_codes_without_gpu(pkg):
+    # the argument checks run before any HIP call; the caller's work and counters are required for split rows
+    lib = ctypes.CDLL(pkg.lib_path("topk"))
+    lib.launch.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_longlong, ctypes.c_longlong] + [ctypes.c_int] * 4 + \
+        [ctypes.c_longlong, ctypes.c_void_p]
+    p = 256  # never dereferenced: every call below returns before a launch
+    assert lib.launch(p, p, p, p, p, 0, 100, 5, 0, 256, 4, 100, None) == 0       # no rows
+    assert lib.launch(p, p, p, p, p, 2, 100, 0, 0, 256, 4, 100, None) == 0       # k = 0
+    assert lib.launch(p, p, p, p, p, 2, 100, 101, 0, 256, 4, 100, None) == -1    # k > cols
+    assert lib.launch(p, p, p, p, p, 2, 5000, 1025, 0, 256, 4, 5000, None) == -1  # k > 1024
+    assert lib.launch(p, p, p, p, p, 70000, 100, 5, 0, 256, 4, 100, None) == -1  # rows > 65535
+    assert lib.launch(p, p, p, p, p, 2, 100, 5, 0, 256, 4, 50, None) == -1       # split with chunk % 4
+    assert lib.launch(p, p, p, p, p, 2, 100, 5, 0, 100, 4, 100, None) == -1      # threads
+    assert lib.launch(p, p, p, p, p, 2, 100, 5, 0, 256, 3, 100, None) == -1      # depth
+    assert lib.launch(p, p, p, p, p, 2, 100, 5, 2, 256, 4, 100, None) == -1      # dtype
+    assert lib.launch(p, p, p, None, p, 2, 100, 5, 0, 256, 4, 52, None) == -1    # split row without work
+    assert lib.launch(p, p, p, p, None, 2, 100, 5, 0, 256, 4, 52, None) == -1    # split row without counters
+    lib.topk_reset.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+    assert lib.topk_reset(None, 0, None) == 0 and lib.topk_reset(None, 4, None) == -1

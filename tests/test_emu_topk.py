@@ -2,21 +2,27 @@
 (tests/emu/hip/hip_runtime.h), every launch checked bit for bit against the oracle.
 
 Each workgroup thread is a cooperative fiber and each cross-lane operation an exchange between barriers of the wave's
-live lanes. Every buffer the kernels touch (input, outputs, work, counters and the library's own hand-off
-workspaces) lies between guard pages, so an out-of-bounds access ends the run with a fault. The cases cover
+live lanes. Every buffer the kernels touch (input, outputs, the caller's work and counters) lies between guard pages,
+so an out-of-bounds access ends the run with a fault, and a launch that allocates device memory fails the case. The cases cover
 single- and split-chunk rows, every k class (1, the lane-maxima bound up to 64, the wide path up to 1024), short last
 tiles, ties, monotone and all-negative rows, the all-ones NaN, repeated launches on the same buffers (the arrival
 counters' self-reset), and shuffled workgroup and lane schedules. The concurrent cases run every workgroup of a launch
 on an OS thread of its own, so chunks publish and count their arrivals while the row's other chunks and merger run.
-What the emulation does not model is the hardware's memory ordering between workgroups (the host's is stronger) and
-the compiler's gfx950 code.
+The weak cases make agent-scope stores visible to other workgroups late and out of order, as the memory system may:
+a store drains when its lane waits with `s_waitcnt vmcnt(0)`, at random before that, and, when its lane has ended
+without waiting, one store at a time now and then, or when the launch completes. The hand-off (result stores, the wait,
+then the arrival count) must stay exact under it, and the same cases with the wait taken out (a planted mistake, on the
+CPU) must fail. A driver also loads two copies of the library into one process and alternates launches of k = 1, 50
+and 1024 between them on shared caller buffers. What the emulation does not model is the compiler's gfx950 code.
 """
 
 import os
 
 import pytest
 
-from _emu import build, run
+import shutil
+
+from _emu import build, build_driver, build_shared, run
 
 
 @pytest.fixture(scope="module")
@@ -72,3 +78,34 @@ def test_emulated_topk_guard_below_start(emu_topk):
     env = dict(os.environ, EMU_ALIGN_START="1")
     for case in (CASES[0], CASES[4], CASES[6]):
         run(emu_topk, case[1:], env=env)
+
+
+# rows, cols, dtype, ks, chunk, min_chunk, reps, seed, shuffle seed, pattern: split rows under the weak mode
+WEAK = [
+    ("c5_rows_fp32", 8, 128256, 0, "1,50,1024", 0, 16384, 2, 41, -1, "randn"),
+    ("split_every_k", 4, 40000, 0, ALL_K, 4096, 2048, 3, 42, -1, "randn"),
+    ("split_bf16_ties", 4, 40000, 1, "1,13,64,65,300", 4096, 2048, 2, 43, 3, "ints"),
+]
+
+
+@pytest.mark.parametrize("concurrent", [False, True], ids=["one_after_another", "concurrent"])
+@pytest.mark.parametrize("case", WEAK, ids=[c[0] for c in WEAK])
+def test_emulated_topk_weak_visibility(emu_topk, case, concurrent):
+    run(emu_topk, case[1:], weak=True, concurrent=concurrent)
+
+
+@pytest.mark.parametrize("concurrent", [False, True], ids=["one_after_another", "concurrent"])
+def test_weak_mode_exposes_a_missing_wait(emu_topk, concurrent):
+    # the planted mistake: the chunks count their arrival without waiting for their result stores, so the row's last
+    # arrival can read stale slots (k = 1), lists (k <= 64) or lists and bound headers (k > 64)
+    env = dict(os.environ, EMU_DROP_VMCNT="1")
+    run(emu_topk, WEAK[1][1:], env=env, weak=True, concurrent=concurrent, expect_ok=False)
+
+
+def test_emulated_two_library_copies(tmp_path):
+    a = build_shared(tmp_path, "topk.hip", "libtopk_a.so")
+    b = str(tmp_path / "libtopk_b.so")
+    shutil.copy(a, b)
+    exe = build_driver(tmp_path, "emu_two_copies.cpp")
+    run(exe, [a, b, 8, 128256, 1, 3, 5])
+    run(exe, [a, b, 4, 128256, 0, 2, 6], weak=True)

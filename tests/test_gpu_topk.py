@@ -1,11 +1,12 @@
 """GPU parity of top-k (build/topk/libkernel.so: `plan`, `launch`, `topk_reset`) against the oracle, bit for bit:
 values (the element bits) and int64 indices, sorted descending with ties by the lowest index.
 
-Covers single- and multi-chunk rows (the merge by the row's last workgroup to arrive, counted in the library's
-arrival counters), every k class (1, the lane-maxima bound up to 64, the general path up to 1024), ties and special
-values, negative rows and the all-ones NaN (the value the k <= 64 kernel pads tiles with), bf16, unaligned and ragged
-rows, short last tiles, workspace reuse, the arrival counters' growth, reset and self-reset, adversarial orders that
-force many prunes, the top-k workload at k = 1, 50 and 1024, and the draw fused into the launch.
+Covers single- and multi-chunk rows (the merge by the row's last workgroup to arrive, counted on the caller's
+counters and handed over in the caller's work), every k class (1, the lane-maxima bound up to 64, the general path up
+to 1024), ties and special values, negative rows and the all-ones NaN (the value the k <= 64 kernel pads tiles with),
+bf16, unaligned and ragged rows, short last tiles, workspace reuse across shapes, work and outputs holding stale
+bytes on entry, the counters' reset and self-reset, adversarial orders that force many prunes, the top-k workload at
+k = 1, 50 and 1024, and the draw fused into the launch.
 """
 
 import numpy as np
@@ -21,8 +22,9 @@ def lib(pkg):
     return pkg.candidate("topk")._lib
 
 
-def run_abi(pkg, x, k, chunk=None):
-    """Launch through the C-ABI with an explicit chunk (None: plan's)."""
+def run_abi(pkg, x, k, chunk=None, poison=False):
+    """Launch through the C-ABI with an explicit chunk (None: plan's). poison: work, values and indices start as all
+    ones (the kernels must not depend on what the caller's buffers held)."""
     cand = pkg.candidate("topk")
     L = lib(pkg)
     rows, cols = x.shape
@@ -34,6 +36,9 @@ def run_abi(pkg, x, k, chunk=None):
     counters = torch.zeros(max(rows, 1), dtype=torch.int32, device=x.device)
     vals = torch.empty(rows, k, dtype=x.dtype, device=x.device)
     idx = torch.empty(rows, k, dtype=torch.int64, device=x.device)
+    if poison:
+        for t in (work, vals, idx):
+            t.view(torch.uint8).fill_(0xFF)
     err = L.launch(x.data_ptr(), vals.data_ptr(), idx.data_ptr(), work.data_ptr(), counters.data_ptr(), rows, cols, k,
                    dtype, 256, 4, chunk, torch.cuda.current_stream().cuda_stream)
     assert err == 0
@@ -48,9 +53,9 @@ def expect(oracle, x, k):
     return oracle.topk(bits16(x), k, "bf16")
 
 
-def check(pkg, oracle, x_cpu, k, dev, chunk=None, what=""):
+def check(pkg, oracle, x_cpu, k, dev, chunk=None, what="", poison=False):
     print(f"[topk] {what} {tuple(x_cpu.shape)} {x_cpu.dtype} k={k} chunk={chunk}", flush=True)
-    vals, idx, nchunks = run_abi(pkg, x_cpu.to(dev), k, chunk)
+    vals, idx, nchunks = run_abi(pkg, x_cpu.to(dev), k, chunk, poison)
     rv, ri = expect(oracle, x_cpu, k)
     got_i = idx.cpu().numpy()
     got_v = vals.cpu().numpy() if x_cpu.dtype == torch.float32 else bits16(vals)
@@ -140,8 +145,8 @@ def test_negative_rows_and_all_ones_nan(pkg, oracle, dev):
 
 
 def test_handoff_workspace_across_shapes(pkg, oracle, dev):
-    # back-to-back split launches on one stream, growing (a reallocation of the arrival counters) and shrinking:
-    # every launch must leave the counters all zeros for the next; topk_reset clears them as well
+    # back-to-back split launches of growing and shrinking shapes on one stream, each with fresh caller buffers: every
+    # launch must leave the counters all zeros; topk_reset clears them as well
     g = torch.Generator().manual_seed(7)
     shapes = [(2, 9000, 7, 2048), (512, 32000, 64, 1024), (3, 20000, 64, 1024), (64, 40000, 50, 4096),
               (2, 9000, 7, 2048)]
@@ -155,12 +160,15 @@ def test_handoff_workspace_across_shapes(pkg, oracle, dev):
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("k", [1, 13, 50, 64, 100, 1024])
 def test_short_last_tiles(pkg, oracle, dev, dt, k):
-    # chunks whose last register tile leaves whole waves without data (the bound is split over the waves holding data)
-    # or holds fewer lanes or groups than k (no bound: the tile is pushed exactly over its vectors holding data); the
-    # k > 64 kernel picks its own chunk, so its tails come from the column counts
+    # chunks whose last register tile leaves whole waves without data, or holds fewer lanes or groups than k: such a
+    # tile has no admission bound and is pushed again, exactly, over its vectors (the re-push path). For k <= 64 the
+    # launch folds a last chunk shorter than one vector per lane into the previous one when both fit one tile, so the
+    # 2048-column cases reach that path only inside the fold; a multi-tile chunk plus a short tail (2 x 16384 + 640:
+    # 160 fp32 or 80 bf16 vectors, so waves 2 and 3 hold none) still reaches it for both dtypes. The k > 64 kernel
+    # picks its own chunk, so its tails come from the column counts.
     g = torch.Generator().manual_seed(900 + k)
     for cols, chunk in [(62 * 2048 + 1280, 2048), (3 * 2048 + 40, 2048), (2 * 17664, 17664), (2 * 16384 + 1280, 16384),
-                        (16384 + 136, None), (1000, None)]:
+                        (2 * 16384 + 640, 16384), (16384 + 136, None), (1000, None)]:
         if k <= cols:
             x = (torch.randn(3, cols, generator=g) * 2).to(dt)
             check(pkg, oracle, x, k, dev, chunk=chunk, what="short last tile")
@@ -202,9 +210,20 @@ def test_workspace_reuse_and_wrapper(pkg, oracle, dev):
         v, ix = pkg.topk(x.to(dev), 50)
         rv, ri = oracle.topk(x.numpy(), 50)
         assert np.array_equal(ix.cpu().numpy(), ri) and np.array_equal(v.cpu().numpy(), rv)
-    counters = pkg.candidate("topk")._counters[dev]
+    counters = pkg.candidate("topk")._buffers.counters[dev]
     assert (counters == 0).all()
     assert lib(pkg).topk_reset(counters.data_ptr(), counters.numel(), torch.cuda.current_stream().cuda_stream) == 0
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_stale_caller_buffers(pkg, oracle, dev, dt):
+    # the caller's work, values and indices hold all-ones bytes on entry (stale composites, a stale header in the row's
+    # indices): every k class, split and unsplit, must still be exact
+    g = torch.Generator().manual_seed(41)
+    x = (torch.randn(6, 40000, generator=g) * 2).to(dt)
+    for k in (1, 13, 64, 65, 300, 1024):
+        for chunk in (None, 4096, 40000):
+            check(pkg, oracle, x, k, dev, chunk=chunk, what="stale buffers", poison=True)
 
 
 def test_invalid_arguments(pkg, dev):
@@ -221,6 +240,8 @@ def test_invalid_arguments(pkg, dev):
     assert L.launch(p, p, p, p, p, 2, 100, 5, 0, 100, 4, 100, s) == -1    # threads
     assert L.launch(p, p, p, p, p, 2, 100, 5, 0, 256, 3, 100, s) == -1    # depth
     assert L.launch(p, p, p, p, p, 2, 100, 5, 2, 256, 4, 100, s) == -1    # dtype
+    assert L.launch(p, p, p, None, p, 2, 100, 5, 0, 256, 4, 52, s) == -1   # a split row without work
+    assert L.launch(p, p, p, p, None, 2, 100, 5, 0, 256, 4, 52, s) == -1   # a split row without counters
 
 
 @pytest.mark.parametrize("k", [1, 50, 1024])
