@@ -44,6 +44,8 @@ struct Smem {
   int bin;       // narrowing: the bin holding the wanted rank
   int above;     // narrowing: composites in the bins above it
   int last;      // the row's last arrival (split rows of the 64 < k kernel)
+  int members;   // bucketed selection: the wanted bucket's members gathered so far
+  u64 pick;      // bucketed selection: the k-th largest
 };
 
 __device__ __forceinline__ u64 composite(uint32_t u, uint32_t index) {
@@ -1346,6 +1348,97 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   }
 }
 
+// Keeps exactly the k largest of the m candidates s.buf[0, m) (k < m <= kWideList) and raises s.thr to the k-th: one
+// pass of bucket counts, (max - c) >> sh into kRankBuckets 16-bit LDS counters as write_ranked does, and a scan find
+// the bucket holding the k-th; its members (about m / kRankBuckets on spread-out values) are gathered and ranked among
+// themselves. A bucket of more than kThreads members (values clustered far below an outlier) takes the general prune
+// (histogram narrowing). Every thread calls it; the block is synchronized on return.
+template <typename S>
+__device__ void prune_bucketed(S& s, int m, int k) {
+  constexpr int P = kWideList / kThreads;
+  constexpr int BPT = kRankBuckets / kThreads;
+  const int t = (int)threadIdx.x;
+  __syncthreads();
+  u64 c[P];
+  u64 mx = 0, mn = ~0ull;
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    const int i = r * kThreads + t;
+    c[r] = i < m ? s.buf[i] : 0ull;
+    if (i < m) {
+      mx = c[r] > mx ? c[r] : mx;
+      mn = c[r] < mn ? c[r] : mn;
+    }
+  }
+  mx = block_ext64<true>(mx, s);
+  mn = block_ext64<false>(mn, s);
+  const u64 range = mx - mn;
+  const int bits = range ? 64 - __clzll(range) : 0;
+  const int sh = bits > 12 ? bits - 12 : 0;  // (mx - mn) >> sh < kRankBuckets
+  unsigned* cnt2 = reinterpret_cast<unsigned*>(s.buf + kWideList);  // bucket b: half b & 1 of word b >> 1
+  u64* members = s.buf + kWideList + kRankBuckets / 4;                // after the counters (kRankBuckets * 2 bytes)
+  for (int w = t; w < kRankBuckets / 2; w += kThreads) cnt2[w] = 0;
+  if (t == 0) s.members = 0;
+  __syncthreads();
+  int bk[P];
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    const u64 d = (mx - c[r]) >> sh;
+    bk[r] = d < (u64)kRankBuckets ? (int)d : kRankBuckets - 1;
+    if (r * kThreads + t < m) atomicAdd(&cnt2[bk[r] >> 1], 1u << (16 * (bk[r] & 1)));
+  }
+  __syncthreads();
+  // the bucket holding position k - 1 (bucket 0 holds the largest candidates)
+  unsigned own[BPT], sum = 0;
+#pragma unroll
+  for (int i = 0; i < BPT; i += 2) {
+    const unsigned w = cnt2[(t * BPT + i) >> 1];
+    own[i] = w & 0xffffu;
+    own[i + 1] = w >> 16;
+    sum += own[i] + own[i + 1];
+  }
+  unsigned incl = sum;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const unsigned o = __shfl_up(incl, d, kWave);
+    if (lane_id() >= d) incl += o;
+  }
+  if (lane_id() == kWave - 1) s.wsum[wave_id()] = incl;
+  __syncthreads();
+  unsigned run = incl - sum;
+  for (int w = 0; w < wave_id(); ++w) run += s.wsum[w];
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    if (run < (unsigned)k && (unsigned)k <= run + own[i]) {
+      s.bin = t * BPT + i;
+      s.above = (int)run;
+      s.hist[0] = own[i];
+    }
+    run += own[i];
+  }
+  __syncthreads();
+  const int B = s.bin, r = k - s.above, pop = (int)s.hist[0];  // the k-th is the r-th largest of bucket B's pop
+  if (pop > kThreads) {
+    prune(s, k);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < P; ++i)
+    if (i * kThreads + t < m && bk[i] == B) members[atomicAdd(&s.members, 1)] = c[i];
+  __syncthreads();
+  if (t < pop) {
+    const u64 mine = members[t];
+    int above = 0;
+    for (int j = 0; j < pop; ++j) above += members[j] > mine;
+    if (above == r - 1) s.pick = mine;
+  }
+  __syncthreads();
+  const u64 kth = s.pick;
+  keep_at_least(s, m, kth);
+  if (t == 0 && kth > s.thr) s.thr = kth;
+  __syncthreads();
+}
+
 // A lower bound of the k-th largest of the wave's values v[i] (N per lane; 0 marks no value and is never counted) with
 // at least k values at or above it; 0 when the wave holds fewer than k values. The bitwise search of wave_kth32 over N
 // values per lane, over [max(lo, smallest value), largest value]: `lo` (wave-uniform) must not exceed the k-th largest,
@@ -1476,7 +1569,9 @@ __global__ void __launch_bounds__(kThreads)
     sample_list<T>(sa, u, values, indices, row, k);
     return;
   }
-  if (s.count > k) prune(s, k);  // the chunk's k largest (its k-th raises s.thr)
+  // the chunk's k largest (its k-th raises s.thr)
+  if (s.count > kWideList) prune(s, k);
+  else if (s.count > k) prune_bucketed(s, s.count, k);
   const int n = s.count;
   // publish: the list, zero-padded to k, and the header (k-bound key << 32 | q-bound key) in the row's output
   u64* wr = work + row * (long long)nchunks * k;
