@@ -18,9 +18,9 @@ read once and every output element written once (workloads.algorithmic_bytes).
 latency of an isolated launch (a few microseconds) to every figure.
 
 The JSON line is printed for the headline workload (RMSNorm bf16 [16384, 4096] with weight); `per_workload` carries
-every named workload measured the same way. The CPU baseline times the reference's PyTorch path for the headline on
-this host's cores (oracle/torch_paths, test infrastructure used here only as the timed baseline) on a bounded sample of
-rows.
+every named workload measured the same way. Beside each GPU figure, "cpu" times the reference's PyTorch path for that
+workload on this host's cores (oracle/torch_paths, test infrastructure used here only as the timed baseline) over the
+whole workload (--cpu-seconds of host time shared by all); the headline's is also `cpu_baseline`.
 """
 
 import argparse
@@ -59,7 +59,8 @@ def parse():
     p.add_argument("--k", type=int, default=None, help="top-k: measure only this k (default: 1, 50 and 1024)")
     p.add_argument("--no-cold", action="store_true", help="skip the flushed single-launch timing")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-seconds", type=float, default=20.0,
+                   help="host time shared by the CPU legs of the measured workloads")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only launch a 256 MiB read-only and a 256 MiB write-only kernel --steps times (for the "
                         "counter scaling)")
@@ -249,30 +250,88 @@ def time_cold(case, steps, flush):
             "cold_us_p90": us[(9 * len(us)) // 10]}
 
 
-def cpu_baseline(pkg, seconds):
-    """The reference's PyTorch path for the headline (x * rsqrt(mean(x^2) + eps).to(bf16), then weight *) on this
-    host's cores, on a bounded sample of rows, reported in the metric's unit."""
+def cpu_paths(pkg, name, k):
+    """(description, a callable running the reference's torch path once over the whole workload) for the CPU leg of a
+    workload. The paths (oracle/torch_paths, test infrastructure used here only as the timed baseline):
+    softmax/baseline.py:13 for softmax, the rmsnorm/kernel.cu:1-8 expression (times the weight) for RMSNorm, HF-style
+    cos/sin construction for the tokens' positions and the rope/kernel.cu:1-11 rotation for RoPE, torch.topk for
+    top-k. Every call runs over the whole workload (each takes at most tens of milliseconds on a server's cores), so
+    the figure is not one of a sample that the host's caches hold."""
     import torch
     from oracle import torch_paths
+    inp = pkg.workloads.WORKLOADS[name]()
+    if name.startswith("softmax"):
+        x = inp["x"]
+        return f"torch.softmax over x{list(x.shape)} fp32", lambda: torch_paths.softmax(x)
+    if name == "rmsnorm_16384x4096":
+        x, w, eps = inp["x"], inp["weight"], inp["eps"]
+        return "rmsnorm expression over x[16384, 4096] bf16 + weight", lambda: torch_paths.rmsnorm(x, w, eps)
+    if name == "rmsnorm_add_16384x4096":
+        x, r, w, eps = inp["x"], inp["residual"], inp["weight"], inp["eps"]
+        return "h = x + residual, rmsnorm(h) * weight over [16384, 4096] bf16", \
+            lambda: torch_paths.rmsnorm_add(x, r, w, eps)
+    if name.startswith("rope"):
+        q, kk, pos, inv = inp["q"], inp["k"], inp["position_ids"], inp["inv_freq"]
+
+        def rope():
+            # HF-style cos/sin for the positions, then the rotation of q and k in fp32, one rounding
+            freqs = torch.outer(pos[0].float(), inv)
+            emb = torch.cat((freqs, freqs), dim=-1)
+            cos, sin = emb.cos(), emb.sin()
+            return torch_paths.rope(q, cos, sin, pos), torch_paths.rope(kk, cos, sin, pos)
+        if name.startswith("rope_kv"):
+            v, slots = inp["v"], inp["slot_mapping"].reshape(-1)
+            kc, vc = inp["k_cache"], inp["v_cache"]
+            tokens = slots.numel()
+
+            def rope_kv():
+                qo, ko = rope()
+                kc.index_copy_(0, slots, ko.reshape(tokens, 8, 128))
+                vc.index_copy_(0, slots, v.reshape(tokens, 8, 128))
+                return qo
+            return "cos/sin, rotation of q and k, cache scatter of k and v over 16384 tokens", rope_kv
+        return "cos/sin and the rotation of q[4, 4096, 32, 128] and k[4, 4096, 8, 128] bf16", rope
+    if name == "topk_sample_128x128256":
+        x, u = inp["x"], inp["uniforms"]
+        kk, temp, top_p = inp["k"], inp["temperature"], inp["top_p"]
+
+        def topk_sample():
+            v, i = torch.topk(x, kk, dim=-1, sorted=True)
+            p = torch.softmax(v / temp, dim=-1)
+            c = torch.cumsum(p, dim=-1)
+            keep = (c - p) < top_p * c[:, -1:]
+            p = p * keep
+            c = torch.cumsum(p, dim=-1)
+            pick = torch.searchsorted(c, (u * c[:, -1]).unsqueeze(-1)).clamp_(max=kk - 1)
+            return i.gather(-1, pick)
+        return "torch.topk (k = 50) over x[128, 128256] fp32, softmax, nucleus cut, draw", topk_sample
+    if name == "topk_128x128256":
+        x = inp["x"]
+        return f"torch.topk k = {k} over x[128, 128256] fp32", lambda: torch.topk(x, k, dim=-1, sorted=True)
+    raise KeyError(name)
+
+
+def cpu_leg(pkg, name, k, seconds):
+    """The reference's CPU path for one workload on this host's cores (cpu_paths), in the metric's unit: the workload's
+    algorithmic bytes / the median time of a call, over `seconds` of calls (at least 10, after 2 warm-ups)."""
+    import torch
     torch.set_num_threads(os.cpu_count() or 1)
-    inp = pkg.workloads.rmsnorm_16384x4096()
-    rows = 2048
-    x, w, eps = inp["x"][:rows].contiguous(), inp["weight"], inp["eps"]
-    nbytes = 2 * x.numel() * 2 + w.numel() * 2
+    what, fn = cpu_paths(pkg, name, k)
+    nbytes = pkg.workloads.algorithmic_bytes(name, k or 50)
     for _ in range(2):
-        torch_paths.rmsnorm(x, w, eps)
+        fn()
     times = []
     t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end or len(times) < 10:
         t = time.perf_counter()
-        torch_paths.rmsnorm(x, w, eps)
+        fn()
         times.append(time.perf_counter() - t)
     times.sort()
     med = times[len(times) // 2]
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{rows} of 16384 rows (x[{rows}, 4096] bf16 + weight), median of {len(times)} calls of the "
-                      f"torch path after 2 warm-ups, {med * 1e3:.2f} ms/call; cpu_count={os.cpu_count()}, "
-                      f"cpu={cpu_model()}"}
+            "us_per_call": round(med * 1e6, 1),
+            "sample": f"the whole workload: {what}; median of {len(times)} calls after 2 warm-ups, "
+                      f"{med * 1e3:.3f} ms/call; cpu_count={os.cpu_count()}, cpu={cpu_model()}"}
 
 
 def cpu_model():
@@ -482,9 +541,16 @@ def main():
                                if key not in ("wall_s", "bytes")}
                          for lab, r in results.items()},
     }
-    if not args.no_cpu and head == HEADLINE:
-        print("[bench] CPU baseline (torch path on the host cores)", file=sys.stderr, flush=True)
-        line["cpu_baseline"] = cpu_baseline(pkg, args.cpu_seconds)
+    if not args.no_cpu:
+        # the reference's CPU path beside every GPU figure, sharing one bounded budget of host time
+        each = args.cpu_seconds / max(1, len(cases))
+        for name, k in cases:
+            label = name if k is None else f"{name}_k{k}"
+            print(f"[bench] CPU baseline {label} (torch path on the host cores)", file=sys.stderr, flush=True)
+            cpu = cpu_leg(pkg, name, k, each)
+            line["per_workload"][label]["cpu"] = cpu
+            if label == head:
+                line["cpu_baseline"] = {key: cpu[key] for key in ("value", "unit", "cores", "kind", "sample")}
     print(json.dumps(line))
 
 

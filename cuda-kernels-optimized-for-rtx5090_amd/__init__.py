@@ -1,9 +1,11 @@
 """MI355X-native row-wise LLM-inference kernels: softmax, RMSNorm, RoPE and top-k, hand-written in HIP for gfx950.
 
 The product is one C-ABI library per op, build/<op>/libkernel.so (make_libs.py), exporting the reference's entry
-points (`launch`, and `plan` for top-k; declared in include/<op>.h) plus a few extensions. <op>/candidate.py mirrors
-the reference harness's `run(inputs)` wrapper for the op and loads that library with ctypes; the functions below are
-conveniences over those wrappers. Inputs must be GPU tensors; there is no CPU fallback.
+points (`launch`, and `plan` for top-k; declared in include/<op>.h) plus a few extensions. Two bindings sit above
+them: <op>/candidate.py mirrors the reference harness's `run(inputs)` wrapper for the op and loads that library with
+ctypes (the functions below are conveniences over those wrappers), and torch_ops.py registers the PyTorch-ROCm
+operators torch.ops.ckopt.* (build/torch/libckopt_torch.so) over the same entry points. Inputs must be GPU tensors;
+there is no CPU fallback.
 """
 
 import importlib.util
@@ -15,6 +17,7 @@ from . import workloads  # noqa: F401  (named workloads: shapes, seeds, byte cou
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 OPS = ("softmax", "rmsnorm", "rope", "topk")
 PROBES = ("probe",)  # the bandwidth probes of the measurement (bench.py --ceiling), not an op
+TORCH = ("torch",)   # the torch operators over the op libraries
 
 
 def lib_path(op):
@@ -22,8 +25,8 @@ def lib_path(op):
     return os.path.join(PKG_DIR, "build", op, "libkernel.so")
 
 
-def build(ops=OPS + PROBES):
-    """Compiles the libraries of the given ops (and the probes) for gfx950; returns {op: path}."""
+def build(ops=OPS + PROBES + TORCH):
+    """Compiles the libraries of the given ops (and the probes and the torch operators); returns {op: path}."""
     from . import make_libs
     return make_libs.build(ops)
 
@@ -39,6 +42,12 @@ def candidate(op):
         spec.loader.exec_module(mod)
         sys.modules[name] = mod
     return mod
+
+
+def ops():
+    """torch.ops.ckopt, with the operators registered (torch_ops.py)."""
+    from . import torch_ops
+    return torch_ops.load()
 
 
 def softmax(x):

@@ -1,10 +1,11 @@
-"""Builds one `libkernel.so` per op from csrc/<op>.hip for gfx950 with hipcc, into build/<op>/.
+"""Builds one `libkernel.so` per op from csrc/<op>.hip for gfx950 with hipcc, into build/<op>/, and the PyTorch-ROCm
+operators over them (csrc/torch_ops.cpp, torch.ops.ckopt.*) into build/torch/libckopt_torch.so.
 
-Each library exports the reference's C-ABI for its op (`launch`, and `plan` for top-k) plus the extensions declared in
-include/<op>.h, so a harness that loads `$CKOPT_BUILD_DIR/libkernel.so` can point CKOPT_BUILD_DIR at build/<op>.
+Each op library exports the reference's C-ABI for its op (`launch`, and `plan` for top-k) plus the extensions declared
+in include/<op>.h, so a harness that loads `$CKOPT_BUILD_DIR/libkernel.so` can point CKOPT_BUILD_DIR at build/<op>.
 
-    python make_libs.py            # build every op
-    python make_libs.py softmax    # build some
+    python make_libs.py            # build every op and the torch operators
+    python make_libs.py softmax    # build some (torch: the operators)
 """
 
 import concurrent.futures
@@ -15,6 +16,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIBS = ("softmax", "rmsnorm", "rope", "topk", "probe")  # the four ops and the bandwidth probes of bench.py --ceiling
+TORCH = "torch"  # the torch operators over the op libraries
 ARCH = os.environ.get("ROWKERN_ARCH", "gfx950")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 (some of their forms are unreliable on this part); hipcc's host pass
@@ -43,7 +45,34 @@ def lib_path(op):
     return os.path.join(HERE, "build", op, "libkernel.so")
 
 
+def torch_lib_path():
+    return os.path.join(HERE, "build", TORCH, "libckopt_torch.so")
+
+
+def build_torch_ops():
+    """csrc/torch_ops.cpp against the installed PyTorch-ROCm (its headers and libraries), with the host compiler: the
+    operators hold no device code of their own, they call the op libraries."""
+    import torch
+    from torch.utils import cpp_extension
+    out = torch_lib_path()
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__=1",
+           "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           *[f"-I{p}" for p in cpp_extension.include_paths(device_type="cuda")], "-I", os.path.join(HERE, "..", "include"),
+           os.path.join(CSRC, "torch_ops.cpp"), f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+           "-ltorch_hip", f"-Wl,-rpath,{torch_lib}", "-ldl", "-o", tmp]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"the torch operators failed to build ({proc.returncode}):\n" + proc.stderr[-6000:])
+    os.replace(tmp, out)
+    return TORCH, out, ""
+
+
 def build_one(op):
+    if op == TORCH:
+        return build_torch_ops()
     src = os.path.join(CSRC, op + ".hip")
     out = lib_path(op)
     os.makedirs(os.path.dirname(out), exist_ok=True)
@@ -57,7 +86,7 @@ def build_one(op):
     return op, out, "\n".join(lines)
 
 
-def build(ops=LIBS, jobs=4):
+def build(ops=LIBS + (TORCH,), jobs=4):
     """Compiles the given ops; returns {op: path}. Raises RuntimeError on a compiler error."""
     results = {}
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
@@ -69,6 +98,6 @@ def build(ops=LIBS, jobs=4):
 
 
 if __name__ == "__main__":
-    ops = sys.argv[1:] or LIBS
+    ops = sys.argv[1:] or LIBS + (TORCH,)
     for op, path in build(ops).items():
         print(op, path)
