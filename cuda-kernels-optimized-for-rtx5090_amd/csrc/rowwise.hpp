@@ -96,6 +96,19 @@ template <> __device__ __forceinline__ u32x4 pack<F16>(const float* f) {
   return r;
 }
 
+// e^d for a value that is rounded to bf16 or fp16 afterwards: 2^(d log2 e) by the hardware's exp2 (v_exp_f32),
+// evaluated 64 binades up and scaled back, so that results below the fp32 normal range are not flushed to zero (the
+// instruction flushes them). The relative error, about 1e-5 (the roundings of d log2 e + 64 and the instruction's own),
+// is far below the 2^-9 half ulp of bf16; four instructions where the correctly rounded expf takes about fourteen, which
+// keeps the 16-bit softmax paths (twice the elements per byte of fp32) memory-bound. d = -inf gives 0, NaN stays NaN.
+__device__ __forceinline__ float exp_narrow(float d) {
+  return __builtin_amdgcn_exp2f(d * 1.44269504088896341f + 64.0f) * 0x1p-64f;
+}
+// The exponential of a path whose outputs have format T: expf for fp32 (within the 1e-5 relative bar of its results),
+// exp_narrow for the 16-bit formats.
+template <typename T> __device__ __forceinline__ float exp_to(float d) { return exp_narrow(d); }
+template <> __device__ __forceinline__ float exp_to<F32>(float d) { return expf(d); }
+
 // Scalar element access (unaligned / ragged paths).
 template <typename T> __device__ __forceinline__ float load_elem(const void* p, long long i);
 template <> __device__ __forceinline__ float load_elem<F32>(const void* p, long long i) {

@@ -9,16 +9,17 @@
 //    group (DPP inside each wave, one LDS slot per wave across waves) and y = exp(x - max) / sum is written from the
 //    registers: one HBM read and one write per element. Workgroups are persistent: each walks the rows with a stride
 //    of the grid and loads its next row while it reduces and stores the current one.
-//  - co-resident tier (longer rows, when all of their chunks fit on the GPU at once): one pass; see softmax_coop.
-//  - split tier (longer rows otherwise): a row is split into chunks of WAVES x 64 x NV vectors, one workgroup each.
-//    Pass 1 reduces each chunk to its online-softmax pair (m, s = sum of exp(x - m)) in a workspace; pass 2 merges the
-//    row's pairs (M = max m, S = sum of s * exp(m - M)) in every wave and writes exp(x - M) / S for its chunk,
-//    re-reading the chunk (2R + 1W).
+//  - co-resident tier (longer rows, up to 64 chunks of 16384 elements): one pass over x for any number of rows; see
+//    softmax_coop.
+//  - stream tier (longer rows still): one workgroup per row, two passes, no workspace; see softmax_stream.
 //  - generic tier (any length or alignment): one workgroup per row, three scalar passes (max, sum, write).
+// The library allocates no device memory: the co-resident tier exchanges its chunk pairs through a static device
+// table whose entries carry a per-launch tag, so nothing has to be cleared between launches.
 // The normalisation multiplies by the fp32 reciprocal of the row sum (the reference divides, softmax/kernel.cu:240;
 // the two differ by at most 1.5 ulp in fp32 and are within the 1e-5 relative tolerance of the fp64 oracle).
 #include <climits>
 #include <cmath>
+#include <mutex>
 
 #include "host.hpp"
 #include "rowwise.hpp"
@@ -57,7 +58,7 @@ __device__ __forceinline__ float exp_and_sum(float (&f)[NV][T::V], float m, long
     const bool ok = FULL || (long long)k * G + t < count;
 #pragma unroll
     for (int i = 0; i < T::V; ++i) {
-      f[k][i] = expf(f[k][i] - m);
+      f[k][i] = exp_to<T>(f[k][i] - m);
       s += ok ? f[k][i] : 0.0f;
     }
   }
@@ -142,244 +143,251 @@ __global__ void __launch_bounds__((WAVES < 4 ? 4 : WAVES) * 64)
   }
 }
 
-// Split tier, pass 1: block b = row * chunks + c reduces vectors [c * CH, min((c + 1) * CH, nvec)) of its row to
-// (m, s) and writes them to ws[b].
-template <typename T, int WAVES, int NV, bool NTL>
+// Stream tier (aligned rows too long for the co-resident tier, or when it is declined): one workgroup of WAVES waves
+// per row, persistent over rows, two passes and no workspace. Pass 1 keeps each lane's online (max, sum of exp(x -
+// max)) over its vectors, U of them in flight per lane, merged over the workgroup (M = max m, S = sum s * exp(m - M));
+// pass 2 reads the row again and writes exp(x - M) * (1 / S): 2R + 1W, the second read mostly from the caches.
+template <typename T, int WAVES, bool NTS>
 __global__ void __launch_bounds__(WAVES * 64)
-    softmax_split_stats(const void* __restrict__ x, float2* __restrict__ ws, long long nvec, long long chunks) {
+    softmax_stream(const void* __restrict__ x, void* __restrict__ y, long long rows, long long nvec) {
   constexpr int G = WAVES * kWave;
-  constexpr long long CH = (long long)G * NV;
+  constexpr int U = 4;
   __shared__ float slots[2][WAVES];
-  const long long b = blockIdx.x;
-  const long long row = b / chunks, c = b - row * chunks;
-  const long long first = c * CH;
-  const long long count = nvec - first < CH ? nvec - first : CH;
   const int t = (int)threadIdx.x;
-  Regs<NV> r;
-  load_vectors<G, NV, false, NTL>(r, x, row * nvec + first, count, t);
-  float f[NV][T::V];
-  float m = lane_max<T, G, NV, false>(r, f, count, t);
-  m = group_reduce<WAVES>(m, OpMax{}, slots[0], wave_id(), 0);
-  float s = exp_and_sum<T, G, NV, false>(f, m, count, t);
-  s = group_reduce<WAVES>(s, OpSum{}, slots[1], wave_id(), 0);
-  // An all -inf chunk contributes nothing to the merge (its NaN sum must not reach it).
-  if (t == 0) ws[b] = make_float2(m, m == -INFINITY ? 0.0f : s);
-}
-
-// Merge of a row's chunk pairs, computed identically (same lanes, same order) by every wave that needs it.
-__device__ __forceinline__ void merge_pairs(const float2* __restrict__ p, long long chunks, float& M, float& S) {
-  const int lane = lane_id();
-  float m = -INFINITY, s = 0.0f;
-  for (long long i = lane; i < chunks; i += kWave) {
-    const float2 q = p[i];
-    const float mm = fmaxf(m, q.x);
-    if (mm != -INFINITY) {
-      s = s * expf(m - mm) + q.y * expf(q.x - mm);
-      m = mm;
+  for (long long row = blockIdx.x; row < rows; row += gridDim.x) {
+    const long long base = row * nvec;
+    float m = -INFINITY, s = 0.0f;
+    for (long long i0 = 0; i0 < nvec; i0 += (long long)G * U) {
+      u32x4 r[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const long long i = i0 + (long long)u * G + t;
+        r[u] = load16<false>(x, base + (i < nvec ? i : nvec - 1));  // clamped: issued unconditionally
+      }
+      float f[U][T::V];
+      float cm = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        unpack<T>(r[u], f[u]);
+        const bool ok = i0 + (long long)u * G + t < nvec;
+#pragma unroll
+        for (int e = 0; e < T::V; ++e) cm = ok ? fmaxf(cm, f[u][e]) : cm;
+      }
+      if (cm > m) {  // rescale the running sum to the new maximum (-inf elements never raise it)
+        s = m == -INFINITY ? 0.0f : s * expf(m - cm);
+        m = cm;
+      }
+      if (m != -INFINITY) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const bool ok = i0 + (long long)u * G + t < nvec;
+#pragma unroll
+          for (int e = 0; e < T::V; ++e) s += ok ? exp_to<T>(f[u][e] - m) : 0.0f;
+        }
+      }
     }
-  }
-  M = wave_max(m);
-  S = wave_sum(M == -INFINITY ? s : s * expf(m - M));
-}
-
-// Split tier, pass 2: re-reads the chunk and writes exp(x - M) / S.
-template <typename T, int WAVES, int NV, bool NTL, bool NTS>
-__global__ void __launch_bounds__(WAVES * 64)
-    softmax_split_apply(const void* __restrict__ x, void* __restrict__ y, const float2* __restrict__ ws,
-                        long long nvec, long long chunks) {
-  constexpr int G = WAVES * kWave;
-  constexpr long long CH = (long long)G * NV;
-  const long long b = blockIdx.x;
-  const long long row = b / chunks, c = b - row * chunks;
-  const long long first = c * CH;
-  const long long count = nvec - first < CH ? nvec - first : CH;
-  const int t = (int)threadIdx.x;
-  Regs<NV> r;
-  load_vectors<G, NV, false, NTL>(r, x, row * nvec + first, count, t);
-  float M, S;
-  merge_pairs(ws + row * chunks, chunks, M, S);
-  float f[NV][T::V];
+    const float M = group_reduce<WAVES>(m, OpMax{}, slots[0], wave_id(), 0);
+    const float S = group_reduce<WAVES>(m == -INFINITY ? 0.0f : s * expf(m - M), OpSum{}, slots[1], wave_id(), 0);
+    const float inv = 1.0f / S;  // an all -inf row: M = -inf, S = 0, and every output NaN (as the fp64 reference)
+    for (long long i = t; i < nvec; i += G) {
+      float f[T::V];
+      unpack<T>(load16<false>(x, base + i), f);
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    unpack<T>(r.v[k], f[k]);
-#pragma unroll
-    for (int e = 0; e < T::V; ++e) f[k][e] = expf(f[k][e] - M);
+      for (int e = 0; e < T::V; ++e) f[e] = exp_to<T>(f[e] - M) * inv;
+      store16<NTS>(y, base + i, pack<T>(f));
+    }
+    __syncthreads();  // the slots are written again by the next row's reductions
   }
-  scale_store<T, G, NV, false, NTS>(f, S, y, row * nvec + first, count, t, true);
 }
 
-// Co-resident tier, for long rows whose chunks all fit on the GPU at once: the split tier's chunks, each held in its
-// workgroup's registers across the exchange of the row's chunk pairs, so x is read once (1R + 1W). For fp32 the
-// registers hold exp(x - m) after the first pass and the output is exp(x - m) * (exp(m - M) / S), within 3 ulp of
-// the once-rounded value (outputs in the fp32 subnormal range, below 2^-126, are within a few 2^-149). The grid never
-// exceeds what the GPU holds at once, so every workgroup of a row is resident (or waits only for other kernels to
-// drain). A workgroup publishes its pair (m, s) as one device-coherent 64-bit store into the row's slot for it; a slot
-// holding 0 is unpublished (no pair is 0: a chunk's s is >= 1 for a finite max, an all -inf chunk stores (-inf, 0)
-// and a NaN chunk NaNs). Wave 0 polls the row's slots with device-coherent loads until all are published, merges them
-// (the same lanes and order in every workgroup of the row, so all agree bit for bit) and hands M and S to the other
-// waves; the chunk is then written from the registers. Last, a departure counter finds the row's last workgroup, which
-// zeroes the row's slots and the counter for the next launch (the workspace starts zeroed). The wait is bounded
-// (spin_limit polls): it always ends, even if a row's workgroups could not all run at once (other kernels holding
-// CUs, or two such launches on two streams). A workgroup whose wait ends before every pair is published takes the
-// row's M and S from x itself (every thread an online max and sum over a share of the whole row), so the result
-// stays within the tolerance either way; only the time suffers.
-constexpr unsigned kSpinLimit = 1u << 22;
-constexpr int kCoopMaxChunks = 64;  // slots a row may have (one per lane of the polling wave)
+// Co-resident tier: long rows in chunks of WAVES x 64 x NV vectors, one workgroup per chunk, every workgroup of a launch
+// resident at once (the grid never exceeds the GPU's resident slots of this kernel): x is read once (1R + 1W). The
+// grid is `groups` row groups of `chunks` workgroups; group g handles rows g, g + groups, ..., one row per iteration,
+// so any number of rows keeps one pass over x. Per iteration, each workgroup holds its chunk in registers as
+// e = exp(x - m) in fp32 (one exp per element), reduces it to its online-softmax pair (m, s = sum of e), and publishes
+// the pair into its slot of the device-scope pair table; wave 0 polls the group's slots until every chunk's pair of
+// this row is there, merges them in a fixed order (the online-softmax merge, the same lanes and order in every
+// workgroup of the row, so all agree bit for bit; softmax/kernel.cu:121-152 is the reference's form of it), and the
+// chunk is written as e * (exp(m - M) / S), within 3 fp32 ulp of the once-rounded value before the output's rounding.
+//
+// The pair table needs no clearing: each pair is two 64-bit words, (tag << 32 | m bits) and (tag << 32 | s bits),
+// stored with device-coherent stores, and a word counts only when its tag is this launch's tag for the iteration (the
+// host hands every launch a fresh range of tags; tag 0, the table's load-time contents, is never handed out). The
+// table is double-buffered by iteration parity: a chunk writes its slot of parity p again two iterations later, by
+// which time every workgroup of its group has published the iteration in between, and so has read parity p. A launch
+// on another stream that uses the same slots at the same time can only make a wait fail (its tags differ), never pass.
+//
+// The wait is bounded by time: after wait_ticks of the 100 MHz s_memrealtime clock with pairs still missing (other
+// kernels holding CUs, so that the row's workgroups are not all resident) the workgroup takes the row's M and S from x
+// itself (every thread an online max and sum over a share of the whole row), so the result stays within the tolerance
+// either way; only the time suffers, by about one read of the row per waiting workgroup.
+constexpr int kCoopMaxChunks = 64;   // a row's chunks: one slot each, polled by one lane each of one wave
+constexpr int kCoopSlots = 4096;     // pair slots per parity: the most workgroups one launch may have
+__device__ __align__(256) unsigned long long g_coop_pairs[2][kCoopSlots][2];
 
-__device__ __forceinline__ unsigned long long pair_bits(float m, float s) {
-  return ((unsigned long long)__float_as_uint(s) << 32) | __float_as_uint(m);
-}
-
-template <typename T, int WAVES, int NV, bool NTL, bool NTS>
+// LOOP: some row group has more than one row (groups < rows); without it every workgroup takes one row, and the
+// kernel is compiled without the loop (which costs registers: fewer resident workgroups).
+template <typename T, int WAVES, int NV, bool NTL, bool NTS, bool LOOP>
 __global__ void __launch_bounds__(WAVES * 64)
-    softmax_coop(const void* __restrict__ x, void* __restrict__ y, unsigned long long* __restrict__ pairs,
-                 unsigned* __restrict__ departs, long long nvec, long long chunks, unsigned spin_limit) {
+    softmax_coop(const void* __restrict__ x, void* __restrict__ y, long long rows, long long nvec, int chunks,
+                 int groups, unsigned tag0, unsigned wait_ticks) {
   constexpr int G = WAVES * kWave;
   constexpr long long CH = (long long)G * NV;
   constexpr int PER = kCoopMaxChunks / kWave;
   __shared__ float slots[2][WAVES];
   __shared__ float ms[2];
   __shared__ int partial;  // the wait ended before every pair of the row was published
-  const long long b = blockIdx.x;
-  const long long row = b / chunks, c = b - row * chunks;
-  const long long first = c * CH;
-  const long long count = nvec - first < CH ? nvec - first : CH;
-  const int t = (int)threadIdx.x;
-  Regs<NV> r;
-  load_vectors<G, NV, false, NTL>(r, x, row * nvec + first, count, t);
-  // the chunk's pair; exp(x - m) is not kept (the registers keep x for the second use)
-  float m = -INFINITY;
+  const int c = (int)(blockIdx.x % (unsigned)chunks), group = (int)(blockIdx.x / (unsigned)chunks);
+  const int first = c * (int)CH;  // < 2^31: at most kCoopMaxChunks chunks of CH vectors
+  const int count = nvec - first < CH ? (int)(nvec - first) : (int)CH;
+  const int t0 = (int)threadIdx.x;
+  const int iters = (int)((rows - group + groups - 1) / groups);
+  constexpr bool PREFETCH = LOOP && T::V == 8;
+  Regs<NV> next;  // PREFETCH: the next row's raw chunk, loaded during the wait
+  if constexpr (PREFETCH) load_vectors<G, NV, false, NTL>(next, x, group * nvec + first, count, t0);
+  for (int it = 0; it < iters; ++it) {
+    const long long row = group + (long long)it * groups;
+    // the lane's offsets are formed anew each iteration (hoisted out of the loop they would hold NV 64-bit offsets in
+    // registers for its whole length)
+    int t = t0;
+    if constexpr (LOOP) asm volatile("" : "+v"(t));
+    const unsigned long long tag = (unsigned long long)(tag0 + (unsigned)it) << 32;
+    unsigned long long(*table)[2] = g_coop_pairs[it & 1] + (long long)group * chunks;
+    Regs<NV> r;
+    if constexpr (PREFETCH) r = next;
+    else load_vectors<G, NV, false, NTL>(r, x, row * nvec + first, count, t);
+    float m = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    float f[T::V];
-    unpack<T>(r.v[k], f);
-    const bool ok = (long long)k * G + t < count;
+    for (int k = 0; k < NV; ++k) {
+      float f[T::V];
+      unpack<T>(r.v[k], f);
+      const bool ok = k * G + t < count;
 #pragma unroll
-    for (int i = 0; i < T::V; ++i) m = ok ? fmaxf(m, f[i]) : m;
-  }
-  m = group_reduce<WAVES>(m, OpMax{}, slots[0], wave_id(), 0);
-  // fp32: the registers now take e = exp(x - m) (0 for an all -inf chunk) in place of x, and the output is e * (exp(m -
-  // M) / S): one exp per element. bf16 (twice the elements per register) keeps x and evaluates exp(x - M) again.
-  constexpr bool KEEP = T::V == 4;
-  float s = 0.0f;
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    float f[T::V];
-    unpack<T>(r.v[k], f);
-    const bool ok = (long long)k * G + t < count;
-#pragma unroll
-    for (int i = 0; i < T::V; ++i) {
-      const float e = ok && m != -INFINITY ? expf(f[i] - m) : 0.0f;
-      s += e;
-      if constexpr (KEEP) r.v[k][i] = __float_as_uint(e);
+      for (int i = 0; i < T::V; ++i) m = ok ? fmaxf(m, f[i]) : m;
     }
-  }
-  s = group_reduce<WAVES>(s, OpSum{}, slots[1], wave_id(), 0);
-  unsigned long long* row_pairs = pairs + row * chunks;
-  if (t == 0)  // an all -inf chunk has s = 0 and contributes nothing to the merge
-    __hip_atomic_store(row_pairs + c, pair_bits(m, s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (wave_id() == 0) {
-    const int lane = lane_id();
-    unsigned long long v[PER];
+    m = group_reduce<WAVES>(m, OpMax{}, slots[0], wave_id(), 0);
+    // the registers take e = exp(x - m) (0 for an all -inf chunk) in place of x: one exp per element
+    float e[NV][T::V];
+    float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) v[i] = 0;
-    for (unsigned n = 0; n < spin_limit; ++n) {
-      bool ready = true;
+    for (int k = 0; k < NV; ++k) {
+      float f[T::V];
+      unpack<T>(r.v[k], f);
+      const bool ok = k * G + t < count;
+#pragma unroll
+      for (int i = 0; i < T::V; ++i) {
+        e[k][i] = ok && m != -INFINITY ? exp_to<T>(f[i] - m) : 0.0f;
+        s += e[k][i];
+      }
+    }
+    s = group_reduce<WAVES>(s, OpSum{}, slots[1], wave_id(), 0);
+    // x is now held as e: the next row's loads go out before the wait and the stores, into the freed registers (bf16,
+    // whose raw chunk is half the size of e; for fp32 the two together would halve the resident workgroups)
+    if constexpr (PREFETCH)
+      if (it + 1 < iters) load_vectors<G, NV, false, NTL>(next, x, (row + groups) * nvec + first, count, t);
+    if (t == 0) {  // an all -inf chunk publishes (-inf, 0) and contributes nothing to the merge
+      __hip_atomic_store(&table[c][0], tag | __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&table[c][1], tag | __float_as_uint(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (wave_id() == 0) {
+      const int lane = lane_id();
+      unsigned long long wm[PER], ws[PER];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) wm[i] = ws[i] = 0;
+      const unsigned long long start = __builtin_amdgcn_s_memrealtime();
+      bool complete = false;
+      while (true) {
+        bool have = true;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int at = i * kWave + lane;
+          if (at < chunks) {
+            if ((wm[i] >> 32) != (tag >> 32))
+              wm[i] = __hip_atomic_load(&table[at][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((ws[i] >> 32) != (tag >> 32))
+              ws[i] = __hip_atomic_load(&table[at][1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            have = have && (wm[i] >> 32) == (tag >> 32) && (ws[i] >> 32) == (tag >> 32);
+          }
+        }
+        if (__ballot(!have) == 0) {
+          complete = true;
+          break;
+        }
+        // (the clock is a scalar read, so the decision is the wave's; readfirstlane states it)
+        if (__builtin_amdgcn_readfirstlane((int)(__builtin_amdgcn_s_memrealtime() - start > wait_ticks))) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      float pm = -INFINITY, ps = 0.0f;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
-        const long long at = (long long)i * kWave + lane;
-        if (at < chunks && v[i] == 0)
-          v[i] = __hip_atomic_load(row_pairs + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ready = ready && (at >= chunks || v[i] != 0);
-      }
-      if (__ballot(!ready) == 0) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    bool have = true;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) have = have && ((long long)i * kWave + lane >= chunks || v[i] != 0);
-    const bool complete = __ballot(!have) == 0;
-    float pm = -INFINITY, ps = 0.0f;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      if ((long long)i * kWave + lane < chunks) {
-        const float qm = __uint_as_float((unsigned)v[i]), qs = __uint_as_float((unsigned)(v[i] >> 32));
-        const float mm = fmaxf(pm, qm);
-        if (mm != -INFINITY) {
-          ps = ps * expf(pm - mm) + qs * expf(qm - mm);
-          pm = mm;
+        if (i * kWave + lane < chunks) {
+          const float qm = __uint_as_float((unsigned)wm[i]), qs = __uint_as_float((unsigned)ws[i]);
+          const float mm = fmaxf(pm, qm);
+          if (mm != -INFINITY) {
+            ps = ps * expf(pm - mm) + qs * expf(qm - mm);
+            pm = mm;
+          }
         }
       }
-    }
-    const float M = wave_max(pm);
-    const float S = wave_sum(M == -INFINITY ? ps : ps * expf(pm - M));
-    if (lane == 0) {
-      ms[0] = M;
-      ms[1] = S;
-      partial = complete ? 0 : 1;
-    }
-  }
-  __syncthreads();
-  if (partial) {
-    // the row's M and S from x: an online max and sum per thread over its share of the row, merged over the block
-    // (-inf elements add nothing; a NaN makes the sum NaN, as in the pairs)
-    float tm = -INFINITY, ts = 0.0f;
-    for (long long i = t; i < nvec; i += G) {
-      float f[T::V];
-      unpack<T>(load16<false>(x, row * nvec + i), f);
-#pragma unroll
-      for (int e = 0; e < T::V; ++e) {
-        if (f[e] == -INFINITY) continue;
-        if (f[e] > tm) {
-          ts = ts * expf(tm - f[e]) + 1.0f;
-          tm = f[e];
-        } else {
-          ts += expf(f[e] - tm);
-        }
+      const float M = wave_max(pm);
+      const float S = wave_sum(M == -INFINITY ? ps : ps * expf(pm - M));
+      if (lane == 0) {
+        ms[0] = M;
+        ms[1] = S;
+        partial = complete ? 0 : 1;
       }
-    }
-    const float RM = group_reduce<WAVES>(tm, OpMax{}, slots[0], wave_id(), 0);
-    const float RS = group_reduce<WAVES>(tm == -INFINITY ? 0.0f : ts * expf(tm - RM), OpSum{}, slots[1], wave_id(), 0);
-    __syncthreads();  // every wave has read ms and the slots before they are written
-    if (t == 0) {
-      ms[0] = RM;
-      ms[1] = RS;
     }
     __syncthreads();
-  }
-  const float M = ms[0], S = ms[1];
-  if constexpr (KEEP) {
+    if (partial) {
+      // the row's M and S from x: an online max and sum per thread over its share of the row, merged over the block
+      // (-inf elements add nothing; a NaN makes the sum NaN, as in the pairs)
+      float tm = -INFINITY, ts = 0.0f;
+      for (long long i = t; i < nvec; i += G) {
+        float f[T::V];
+        unpack<T>(load16<false>(x, row * nvec + i), f);
+#pragma unroll
+        for (int e = 0; e < T::V; ++e) {
+          if (f[e] == -INFINITY) continue;
+          if (f[e] > tm) {
+            ts = ts * expf(tm - f[e]) + 1.0f;
+            tm = f[e];
+          } else {
+            ts += expf(f[e] - tm);
+          }
+        }
+      }
+      const float RM = group_reduce<WAVES>(tm, OpMax{}, slots[0], wave_id(), 0);
+      const float RS =
+          group_reduce<WAVES>(tm == -INFINITY ? 0.0f : ts * expf(tm - RM), OpSum{}, slots[1], wave_id(), 0);
+      __syncthreads();  // every wave has read ms and the slots before they are written
+      if (t == 0) {
+        ms[0] = RM;
+        ms[1] = RS;
+      }
+      __syncthreads();
+    }
+    const float M = ms[0], S = ms[1];
     // y = e * exp(m - M) / S; an all -inf chunk (e = 0) gives 0, or NaN when the whole row is -inf (M = -inf)
     const float scale = m == -INFINITY ? (M == -INFINITY ? NAN : 0.0f) : expf(m - M) / S;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const long long i = (long long)k * G + t;
+      const int i = k * G + t;
       if (i < count) {
         float f[T::V];
 #pragma unroll
-        for (int e = 0; e < T::V; ++e) f[e] = __uint_as_float(r.v[k][e]) * scale;
+        for (int j = 0; j < T::V; ++j) f[j] = e[k][j] * scale;
         store16<NTS>(y, row * nvec + first + i, pack<T>(f));
       }
     }
-  } else {
-    float f[NV][T::V];
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      unpack<T>(r.v[k], f[k]);
-#pragma unroll
-      for (int e = 0; e < T::V; ++e) f[k][e] = expf(f[k][e] - M);
-    }
-    scale_store<T, G, NV, false, NTS>(f, S, y, row * nvec + first, count, t, true);
+    if constexpr (!LOOP) break;
+    __syncthreads();  // ms, partial and the reduction slots are written again by the next row
   }
-  if (wave_id() == 0) {
-    unsigned old = 0;
-    if (lane_id() == 0) old = __hip_atomic_fetch_add(departs + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (__builtin_amdgcn_readfirstlane(old) == (unsigned)chunks - 1) {  // the row's last workgroup: clear for reuse
-      for (long long at = lane_id(); at < chunks; at += kWave)
-        __hip_atomic_store(row_pairs + at, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (lane_id() == 0) __hip_atomic_store(departs + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+}
+
+// Clears the pair table (before a launch whose tags restart after the tag counter wrapped).
+__global__ void __launch_bounds__(256) softmax_coop_clear() {
+  unsigned long long* p = &g_coop_pairs[0][0][0];
+  for (int i = (int)(blockIdx.x * 256 + threadIdx.x); i < 2 * kCoopSlots * 2; i += (int)(gridDim.x * 256)) p[i] = 0;
 }
 
 // Generic tier: any row length and alignment; one 256-thread block per row (grid-strided), three scalar passes.
@@ -403,11 +411,14 @@ __global__ void __launch_bounds__(256)
 
 // ---- host side ------------------------------------------------------------------------------------------------------
 
-// Tuning slots (0 = automatic): row-tier waves per row, row-tier vectors per lane, row-tier resident blocks per CU,
-// split-tier waves, split-tier vectors per lane, forced tier (1 row, 2 split, 3 generic, 4 co-resident), non-temporal
-// loads (1 on, 2 off), the co-resident tier's bound on its polls (tests force its fallback with a small one).
-enum { kTuneWaves = 0, kTuneNv = 1, kTuneBlocksPerCu = 2, kTuneSplitWaves = 3, kTuneSplitNv = 4, kTuneTier = 5,
-       kTuneNtLoads = 6, kTuneSpinLimit = 7 };
+// Tuning slots (0 = automatic), for sweeps and tests: row-tier waves per row, row-tier vectors per lane, row-tier
+// resident blocks per CU, stream-tier waves, co-resident row groups (fewer forces more rows per workgroup), preferred
+// tier (1 row, 2 stream, 3 generic, 4 co-resident; a tier that cannot take the rows is passed over for the automatic
+// choice), non-temporal loads (1 on, 2 off), the co-resident tier's wait budget in 100 MHz ticks (tests force its
+// fallback with 1).
+enum { kTuneWaves = 0, kTuneNv = 1, kTuneBlocksPerCu = 2, kTuneStreamWaves = 3, kTuneCoopGroups = 4, kTuneTier = 5,
+       kTuneNtLoads = 6, kTuneWaitTicks = 7 };
+constexpr unsigned kCoopWaitTicks = 10000;  // 100 us: tens of times a row's arrival skew, a few launch lengths
 
 int pow2_at_least(long long v) {
   int p = 1;
@@ -473,67 +484,82 @@ int launch_rows(int waves, int nv, const void* x, void* y, long long rows, long 
   }
 }
 
-template <typename T, int WAVES, int NV, bool NTL>
-int launch_split_k(const void* x, void* y, long long rows, long long nvec, hipStream_t stream) {
-  constexpr long long CH = (long long)WAVES * kWave * NV;
-  const long long chunks = (nvec + CH - 1) / CH;
-  const long long blocks = rows * chunks;
-  if (blocks > (long long)UINT_MAX) return rw_host::kInvalid;
-  int err = 0;
-  float2* ws = (float2*)rw_host::stream_workspace(stream, (size_t)blocks * sizeof(float2), &err);
-  if (!ws) return err;
-  hipLaunchKernelGGL((softmax_split_stats<T, WAVES, NV, NTL>), dim3((unsigned)blocks), dim3(WAVES * kWave), 0, stream,
-                     x, ws, nvec, chunks);
-  hipLaunchKernelGGL((softmax_split_apply<T, WAVES, NV, NTL, true>), dim3((unsigned)blocks), dim3(WAVES * kWave), 0,
-                     stream, x, y, ws, nvec, chunks);
+template <typename T, int WAVES>
+int launch_stream_w(const void* x, void* y, long long rows, long long nvec, hipStream_t stream) {
+  long long grid = (long long)rw_host::device_cus() * (16 / WAVES > 1 ? 16 / WAVES : 1);
+  if (grid > rows) grid = rows;
+  hipLaunchKernelGGL((softmax_stream<T, WAVES, true>), dim3((unsigned)grid), dim3(WAVES * kWave), 0, stream, x, y,
+                     rows, nvec);
   return (int)hipGetLastError();
 }
 
-template <typename T, int WAVES, bool NTL>
-int launch_split_w(int nv, const void* x, void* y, long long rows, long long nvec, hipStream_t stream) {
-  switch (nv) {
-    case 2: return launch_split_k<T, WAVES, 2, NTL>(x, y, rows, nvec, stream);
-    case 4: return launch_split_k<T, WAVES, 4, NTL>(x, y, rows, nvec, stream);
-    case 8: return launch_split_k<T, WAVES, 8, NTL>(x, y, rows, nvec, stream);
-    default: return rw_host::kInvalid;
+template <typename T>
+int launch_stream(const void* x, void* y, long long rows, long long nvec, hipStream_t stream) {
+  switch (rw_host::tune_get(kTuneStreamWaves)) {
+    case 4: return launch_stream_w<T, 4>(x, y, rows, nvec, stream);
+    case 8: return launch_stream_w<T, 8>(x, y, rows, nvec, stream);
+    default: return launch_stream_w<T, 16>(x, y, rows, nvec, stream);
   }
 }
 
-template <typename T, bool NTL>
-int launch_split(int waves, int nv, const void* x, void* y, long long rows, long long nvec, hipStream_t stream) {
-  switch (waves) {
-    case 4: return launch_split_w<T, 4, NTL>(nv, x, y, rows, nvec, stream);
-    case 8: return launch_split_w<T, 8, NTL>(nv, x, y, rows, nvec, stream);
-    case 16: return launch_split_w<T, 16, NTL>(nv, x, y, rows, nvec, stream);
-    default: return rw_host::kInvalid;
+// The co-resident tier's tags: per device, the next unused one (0 is never handed out: it is the pair table's contents
+// at load). A launch takes one per iteration; when the 32-bit counter would wrap, the table is cleared on the launch's
+// stream and the tags start again at 1.
+unsigned coop_tags(int dev, unsigned n, hipStream_t stream, int* err) {
+  static std::mutex mu;
+  static unsigned next[64];
+  std::lock_guard<std::mutex> lock(mu);
+  unsigned& nx = next[dev & 63];
+  *err = rw_host::kOk;
+  if (nx == 0 || nx + n < nx) {
+    hipLaunchKernelGGL(softmax_coop_clear, dim3(16), dim3(256), 0, stream);
+    *err = (int)hipGetLastError();
+    nx = 1;
   }
+  const unsigned t = nx;
+  nx += n;
+  return t;
 }
 
-// Co-resident tier: chunks of 4 waves x 64 lanes x 16 vectors (16384 fp32 / 32768 bf16 elements), up to kCoopRows
-// rows of up to kCoopMaxChunks chunks. Returns 1, launching nothing, when the rows' chunks do not all fit on the GPU
-// at once. Workspace: the departure counters (a fixed region, so that launches of any shape agree on it), then the
-// pair slots.
-constexpr long long kCoopRows = 4096;
-constexpr size_t kCoopCounterBytes = (size_t)kCoopRows * sizeof(unsigned);
-
+// Co-resident tier: chunks of 4 waves x 64 lanes x 64 elements (16 fp32 or 8 bf16 vectors per lane), at most
+// kCoopMaxChunks per row; one row per workgroup when every row's chunks fit on the GPU at once, else row groups
+// walking several rows (a second instantiation: the loop costs registers). Returns 1, launching nothing, when one
+// row's chunks do not fit on the GPU at once.
 template <typename T, bool NTL>
 int launch_coop(const void* x, void* y, long long rows, long long nvec, hipStream_t stream) {
-  constexpr int WAVES = 4, NV = 16;
-  constexpr long long CH = (long long)WAVES * kWave * NV;
-  long long chunks = (nvec + CH - 1) / CH;
-  auto kern = softmax_coop<T, WAVES, NV, NTL, true>;
-  static int occ = 0;  // resident blocks per CU of this instantiation (idempotent cache)
-  if (occ <= 0) occ = blocks_per_cu(kern, WAVES * kWave);
-  const long long blocks = rows * chunks;
-  if (rows > kCoopRows || chunks > kCoopMaxChunks || blocks > (long long)rw_host::device_cus() * occ) return 1;
-  int err = 0;
-  char* ws = (char*)rw_host::stream_workspace(stream, kCoopCounterBytes + (size_t)blocks * 8, &err, 1, true);
-  if (!ws) return err;
-  unsigned* departs = (unsigned*)ws;
-  unsigned long long* pairs = (unsigned long long*)(ws + kCoopCounterBytes);
-  const int limit = rw_host::tune_get(kTuneSpinLimit);
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(WAVES * kWave), 0, stream, x, y, pairs, departs, nvec, chunks,
-                     limit > 0 ? (unsigned)limit : kSpinLimit);
+  constexpr int WAVES = 4, NV1 = 64 / T::V, NVL = T::V == 4 ? 16 : 8;
+  constexpr long long CH1 = (long long)WAVES * kWave * NV1, CHL = (long long)WAVES * kWave * NVL;
+  auto one = softmax_coop<T, WAVES, NV1, NTL, true, false>;
+  auto loop = softmax_coop<T, WAVES, NVL, NTL, true, true>;
+  static int occ_one = 0, occ_loop = 0;  // resident blocks per CU of each instantiation (idempotent caches)
+  if (occ_one <= 0) occ_one = blocks_per_cu(one, WAVES * kWave);
+  if (occ_loop <= 0) occ_loop = blocks_per_cu(loop, WAVES * kWave);
+  const int want = rw_host::tune_get(kTuneCoopGroups);
+  const long long cus = rw_host::device_cus();
+  long long chunks = (nvec + CH1 - 1) / CH1;
+  long long slots = cus * occ_one;
+  if (slots > kCoopSlots) slots = kCoopSlots;
+  const bool single = chunks <= kCoopMaxChunks && rows * chunks <= slots && (want <= 0 || want >= rows);
+  if (!single) {
+    chunks = (nvec + CHL - 1) / CHL;
+    slots = cus * occ_loop;
+    if (slots > kCoopSlots) slots = kCoopSlots;
+    if (chunks > kCoopMaxChunks || chunks > slots) return 1;
+  }
+  long long groups = single ? rows : slots / chunks;
+  if (want > 0 && want < groups) groups = want;
+  if (groups > rows) groups = rows;
+  const long long iters = (rows + groups - 1) / groups;
+  if (iters > 0x40000000LL) return 1;
+  int dev = 0, err = (int)hipGetDevice(&dev);
+  if (err != rw_host::kOk) return err;
+  const unsigned tag0 = coop_tags(dev, (unsigned)iters, stream, &err);
+  if (err != rw_host::kOk) return err;
+  const int budget = rw_host::tune_get(kTuneWaitTicks);
+  const unsigned ticks = budget > 0 ? (unsigned)budget : kCoopWaitTicks;
+  const dim3 grid((unsigned)(groups * chunks)), block(WAVES * kWave);
+  if (single) hipLaunchKernelGGL(one, grid, block, 0, stream, x, y, rows, nvec, (int)chunks, (int)groups, tag0, ticks);
+  else hipLaunchKernelGGL(loop, grid, block, 0, stream, x, y, rows, nvec, (int)chunks, (int)groups, tag0, ticks);
   return (int)hipGetLastError();
 }
 
@@ -551,8 +577,9 @@ int launch_typed(const void* x, void* y, long long rows, long long cols, hipStre
   const int tier = rw_host::tune_get(kTuneTier);
   if (!vec || tier == 3) return launch_generic<T>(x, y, rows, cols, stream);
   const long long nvec = cols / T::V;
+  if (tier == 2) return launch_stream<T>(x, y, rows, nvec, stream);
   const bool ntl = rw_host::tune_get(kTuneNtLoads) == 1;
-  if (tier != 2 && nvec <= (long long)kMaxWaves * kWave * kMaxNv) {
+  if (tier != 4 && nvec <= (long long)kMaxWaves * kWave * kMaxNv) {
     // Row tier: 4 vectors per lane as long as 16 waves suffice, then up to 8.
     int waves = rw_host::tune_get(kTuneWaves), nv = rw_host::tune_get(kTuneNv);
     if (waves <= 0) {
@@ -565,19 +592,11 @@ int launch_typed(const void* x, void* y, long long rows, long long cols, hipStre
       return ntl ? launch_rows<T, true>(waves, nv, x, y, rows, nvec, stream)
                  : launch_rows<T, false>(waves, nv, x, y, rows, nvec, stream);
     }
-    if (tier == 1) return rw_host::kInvalid;
   }
-  if (tier == 0 || tier == 4) {
-    const int rc =
-        ntl ? launch_coop<T, true>(x, y, rows, nvec, stream) : launch_coop<T, false>(x, y, rows, nvec, stream);
-    if (rc != 1) return rc;
-    if (tier == 4) return rw_host::kInvalid;
-  }
-  int waves = rw_host::tune_get(kTuneSplitWaves), nv = rw_host::tune_get(kTuneSplitNv);
-  if (waves <= 0) waves = 4;
-  if (nv <= 0) nv = 8;
-  return ntl ? launch_split<T, true>(waves, nv, x, y, rows, nvec, stream)
-             : launch_split<T, false>(waves, nv, x, y, rows, nvec, stream);
+  const int rc =
+      ntl ? launch_coop<T, true>(x, y, rows, nvec, stream) : launch_coop<T, false>(x, y, rows, nvec, stream);
+  if (rc != 1) return rc;
+  return launch_stream<T>(x, y, rows, nvec, stream);
 }
 
 }  // namespace

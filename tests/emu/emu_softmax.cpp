@@ -4,13 +4,14 @@
 // NaN). Every device buffer lies between guard pages. The co-resident tier (4) needs EMU_CONCURRENT: its workgroups
 // wait for one another.
 //
-// usage: emu_softmax rows cols dtype(0 fp32, 1 bf16) tier seed [waves nv [offset [pattern [reps [spin_limit]]]]]
-//   tier: 1 row, 2 split, 3 generic, 4 co-resident (forced through softmax_tune); waves / nv: the row tier's (tier 1)
-//   or the split tier's (tier 2) shape, 0 automatic; offset shifts x and y by that many elements from a 16-byte
-//   boundary (a misaligned row takes the generic tier); pattern: randn (N(0, 4)) or special (-inf elements, an all
-//   -inf row, a row of one huge value); reps: launches on the same buffers, each checked (the co-resident tier's
-//   hand-off slots must be clear again for the next); spin_limit bounds the co-resident tier's polls (a small one
-//   makes its workgroups stop waiting and take the row's statistics from x).
+// usage: emu_softmax rows cols dtype(0 fp32, 1 bf16) tier seed [waves nv [offset [pattern [reps [wait_ticks]]]]]
+//   tier: 1 row, 2 stream, 3 generic, 4 co-resident (preferred through softmax_tune); waves / nv: the row tier's
+//   shape (tier 1), the stream tier's waves (tier 2), the co-resident tier's row groups in nv (tier 4; fewer groups
+//   than rows make each workgroup walk several rows), 0 automatic; offset shifts x and y by that many elements from a
+//   16-byte boundary (a misaligned row takes the generic tier); pattern: randn (N(0, 4)) or special (-inf elements,
+//   an all -inf row, a row of one huge value); reps: launches on the same buffers, each checked (the co-resident
+//   tier's pair table is reused by the next launch, under fresh tags); wait_ticks bounds the co-resident tier's wait
+//   (1 makes its workgroups stop waiting and take the row's statistics from x).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -50,8 +51,14 @@ int main(int argc, char** argv) {
   const int reps = argc > 10 ? atoi(argv[10]) : 1;
   if (argc > 11) softmax_tune(7, atoi(argv[11]));
   softmax_tune(5, tier);
-  softmax_tune(tier == 2 ? 3 : 0, waves);
-  softmax_tune(tier == 2 ? 4 : 1, nv);
+  if (tier == 2) {
+    softmax_tune(3, waves);
+  } else if (tier == 4) {
+    softmax_tune(4, nv);
+  } else {
+    softmax_tune(0, waves);
+    softmax_tune(1, nv);
+  }
   const size_t esz = dtype == 0 ? 4 : 2, n = (size_t)rows * cols;
   std::mt19937_64 g(seed);
   std::normal_distribution<float> nd(0.0f, 4.0f);

@@ -13,7 +13,8 @@
 //  - the atomics are sequentially consistent operations (fibers of one workgroup switch only at barriers), except
 //    in the weak mode (EMU_WEAK set): there an agent-scope store (__hip_atomic_store) is held in its lane's queue of
 //    pending stores and becomes visible to other workgroups late and out of order -- a pending store drains at random
-//    at the lane's later atomic operations and barriers, all of the lane's drain at `s_waitcnt vmcnt(0)` (the wait
+//    at the lane's later atomic operations, ballots, sleeps and barriers (so a lane that keeps running sees its
+//    stores complete in the end, as the hardware's do), all of the lane's drain at `s_waitcnt vmcnt(0)` (the wait
 //    that orders them before a later arrival count), and what a lane left pending when it ended drains one store at a
 //    time, now and then, while other lanes run, and wholly when the launch completes. A lane reads its own pending stores (same-address order is
 //    kept); atomic read-modify-writes act on memory at once. With EMU_DROP_VMCNT set as well, `s_waitcnt vmcnt(0)`
@@ -32,6 +33,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <atomic>
+#include <chrono>
 #include <functional>
 #include <map>
 #include <mutex>
@@ -45,6 +47,7 @@
 #define __forceinline__ inline
 #define __launch_bounds__(...)
 #define __shared__ static thread_local
+#define __align__(n) alignas(n)
 #define EMU_ASM(...) emu::asm_hook(#__VA_ARGS__)
 
 typedef int hipError_t;
@@ -231,6 +234,7 @@ inline void block_sync(int line) {
 inline bool lane_done(int w, int l) { return S().fib[w * kW + l].done; }
 
 inline uint64_t ballot(bool p, int line) {
+  if (weak()) maybe_drain();  // a lane's stores complete while it runs, whatever it runs
   State& s = S();
   const int w = wid();
   s.slots[w][lid()] = p;
@@ -396,6 +400,17 @@ inline void run_block() {
 }
 
 inline bool concurrent() { return std::getenv("EMU_CONCURRENT") != nullptr; }
+inline void sleep_a_while() {
+  if (weak()) maybe_drain();
+  if (concurrent()) sched_yield();
+}
+inline unsigned long long realtime_ticks() {
+  // EMU_CLOCK_STOPPED: time never advances, so a bounded wait can only end by what it waits for
+  static const bool stopped = std::getenv("EMU_CLOCK_STOPPED") != nullptr;
+  if (stopped) return 0;
+  return (unsigned long long)std::chrono::duration_cast<std::chrono::microseconds>(
+             std::chrono::steady_clock::now().time_since_epoch()).count() / 10;
+}
 
 inline void launch(dim3 grid, dim3 block, std::function<void()> body) {
   State& s = S();
@@ -485,7 +500,10 @@ inline void guarded_free(void* p) {
 #define __builtin_amdgcn_mbcnt_lo(m, c) emu::mbcnt_lo((unsigned)(m), (unsigned)(c))
 #define __builtin_amdgcn_mbcnt_hi(m, c) emu::mbcnt_hi((unsigned)(m), (unsigned)(c))
 #define __builtin_amdgcn_wave_barrier() emu::wave_sync(__LINE__)
-#define __builtin_amdgcn_s_sleep(n) (emu::concurrent() ? (void)sched_yield() : (void)0)
+#define __builtin_amdgcn_s_sleep(n) emu::sleep_a_while()
+// the 100 MHz real-time counter, slowed 1000-fold: fibers and OS threads advance far more slowly than waves, so a
+// wait budget in ticks keeps its proportion to the work around it
+#define __builtin_amdgcn_s_memrealtime() emu::realtime_ticks()
 #define __shfl_up(v, d, w) emu::shfl_up((v), (unsigned)(d), (int)(w), __LINE__)
 
 #define __HIP_MEMORY_SCOPE_AGENT 0
@@ -551,6 +569,7 @@ inline T atomicAdd(T* p, U v) {
 }
 
 inline int __popcll(unsigned long long v) { return __builtin_popcountll(v); }
+#define __builtin_amdgcn_exp2f(x) exp2f(x)
 inline int __clzll(long long v) { return v ? __builtin_clzll((unsigned long long)v) : 64; }
 inline int __clz(int v) { return v ? __builtin_clz((unsigned)v) : 32; }
 inline float __uint_as_float(unsigned u) { return __builtin_bit_cast(float, u); }

@@ -7,9 +7,13 @@ Every device buffer lies between guard pages, so a read or write past either end
 the run with a fault. The cases force each tier and register shape through the libraries' tuning slots, and cover
 ragged rows and tails, misaligned buffers (the scalar paths), in-place forms, -inf and all -inf rows, RoPE's head
 sizes down to 24 and its fused KV-cache write with skipped (-1) slots. The softmax co-resident tier, whose
-workgroups wait for one another, runs with every workgroup on an OS thread of its own, over repeated launches (its
-hand-off slots must be clear again for the next).
+workgroups wait for one another, runs with every workgroup on an OS thread of its own, over repeated launches (the
+pair table is reused under fresh tags), with one row per workgroup and with row groups walking several rows; also
+under the weak mode (its pairs become visible late and out of order) with the wait's clock stopped, so that every wait
+must end by its pairs, never by its time budget.
 """
+
+import os
 
 import pytest
 
@@ -36,7 +40,7 @@ def emu_rope(emu_dir):
     return build(emu_dir, "rope.hip", "emu_rope.cpp")
 
 
-# rows, cols, dtype (0 fp32, 1 bf16), tier (1 row, 2 split, 3 generic), seed, waves, nv, offset, pattern
+# rows, cols, dtype (0 fp32, 1 bf16), tier (1 row, 2 stream, 3 generic), seed, waves, nv, offset, pattern
 SOFTMAX = [
     ("row_fp32", 37, 4096, 0, 1, 1, 0, 0, 0, "randn"),
     ("row_bf16", 37, 4096, 1, 1, 2, 0, 0, 0, "randn"),
@@ -45,9 +49,9 @@ SOFTMAX = [
     ("row_one_wave", 40, 256, 0, 1, 13, 1, 1, 0, "randn"),
     ("row_long_bf16", 3, 65536, 1, 1, 15, 0, 0, 0, "randn"),
     ("row_special_bf16", 8, 4096, 1, 1, 10, 0, 0, 0, "special"),
-    ("split_fp32", 5, 20000, 0, 2, 5, 4, 2, 0, "randn"),
-    ("split_bf16", 5, 20000, 1, 2, 6, 4, 2, 0, "randn"),
-    ("split_special", 8, 5000, 0, 2, 11, 4, 2, 0, "special"),
+    ("stream_fp32", 5, 20000, 0, 2, 5, 4, 0, 0, "randn"),
+    ("stream_bf16", 5, 20000, 1, 2, 6, 16, 0, 0, "randn"),
+    ("stream_special", 8, 5000, 0, 2, 11, 8, 0, 0, "special"),
     ("generic_fp32", 7, 3000, 0, 3, 7, 0, 0, 0, "randn"),
     ("generic_odd_bf16", 7, 3001, 1, 3, 8, 0, 0, 0, "randn"),
     ("misaligned_fp32", 8, 4096, 0, 1, 9, 0, 0, 1, "randn"),
@@ -55,12 +59,14 @@ SOFTMAX = [
 ]
 
 # the co-resident tier (its workgroups wait for one another: run concurrently), with repeated launches on the same
-# buffers: rows, cols, dtype, seed, pattern, reps
+# buffers: rows, cols, dtype, seed, pattern, reps, row groups (0: one row per workgroup)
 COOP = [
-    ("coop_fp32", 2, 70000, 0, 3, "randn", 3),
-    ("coop_bf16", 3, 100000, 1, 4, "randn", 2),
-    ("coop_special", 4, 40000, 0, 5, "special", 2),
-    ("coop_one_chunk_bf16", 2, 16384, 1, 6, "randn", 2),
+    ("coop_fp32", 2, 70000, 0, 3, "randn", 3, 0),
+    ("coop_bf16", 3, 100000, 1, 4, "randn", 2, 0),
+    ("coop_special", 4, 40000, 0, 5, "special", 2, 0),
+    ("coop_one_chunk_bf16", 2, 16384, 1, 6, "randn", 2, 0),
+    ("coop_groups_fp32", 7, 70000, 0, 7, "randn", 3, 2),
+    ("coop_groups_special_bf16", 5, 40000, 1, 8, "special", 2, 3),
 ]
 
 # rows, cols, dtype (1 bf16, 2 fp16), mode (0 launch, 1 weighted, 2 add, 3 add in place), seed, waves, nv,
@@ -103,17 +109,26 @@ def test_emulated_softmax_matches_oracle(emu_softmax, case):
 
 @pytest.mark.parametrize("case", COOP, ids=[c[0] for c in COOP])
 def test_emulated_softmax_coresident_tier(emu_softmax, case):
-    rows, cols, dtype, seed, pattern, reps = case[1:]
-    run(emu_softmax, [rows, cols, dtype, 4, seed, 0, 0, 0, pattern, reps], concurrent=True)
+    rows, cols, dtype, seed, pattern, reps, groups = case[1:]
+    run(emu_softmax, [rows, cols, dtype, 4, seed, 0, groups, 0, pattern, reps], concurrent=True)
+
+
+@pytest.mark.parametrize("case", COOP, ids=[c[0] for c in COOP])
+def test_emulated_softmax_coresident_weak_stopped_clock(emu_softmax, case):
+    # pairs visible late and out of order, and a wait that cannot end by its time budget: every wait ends by its pairs
+    rows, cols, dtype, seed, pattern, reps, groups = case[1:]
+    env = dict(os.environ, EMU_CLOCK_STOPPED="1")
+    run(emu_softmax, [rows, cols, dtype, 4, seed, 0, groups, 0, pattern, reps], env=env, concurrent=True, weak=True,
+        timeout=300)
 
 
 @pytest.mark.parametrize("concurrent", [False, True], ids=["one_after_another", "concurrent"])
 @pytest.mark.parametrize("case", COOP, ids=[c[0] for c in COOP])
 def test_emulated_softmax_coresident_fallback(emu_softmax, case, concurrent):
-    # the wait bounded to one poll: workgroups that find their row incomplete (all but the row's last when they run one
+    # the wait bounded to one tick: workgroups that find their row incomplete (all but the row's last when they run one
     # after another) take the row's statistics from x
-    rows, cols, dtype, seed, pattern, reps = case[1:]
-    run(emu_softmax, [rows, cols, dtype, 4, seed, 0, 0, 0, pattern, reps, 1], concurrent=concurrent)
+    rows, cols, dtype, seed, pattern, reps, groups = case[1:]
+    run(emu_softmax, [rows, cols, dtype, 4, seed, 0, groups, 0, pattern, reps, 1], concurrent=concurrent)
 
 
 @pytest.mark.parametrize("case", RMSNORM, ids=[c[0] for c in RMSNORM])

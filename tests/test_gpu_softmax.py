@@ -2,8 +2,9 @@
 
 fp32: |y - oracle| <= 1e-5 |oracle| elementwise (the oracle is the fp64 softmax rounded once); bf16: within 1 ulp.
 Shapes cover every tier: wave-per-row and workgroup-per-row rows (full and ragged), the single-pass co-resident tier
-and the two-pass split tier for long rows, and the generic tier for lengths that are not a multiple of the vector width
-and for misaligned pointers.
+for long rows (one row per workgroup, and row groups walking several rows when the rows' chunks do not all fit at
+once), the two-pass stream tier for rows beyond it, and the generic tier for lengths that are not a multiple of the
+vector width and for misaligned pointers.
 """
 
 import ctypes
@@ -82,8 +83,8 @@ def test_long_rows_with_infinite_chunks(pkg, oracle, dev):
 
 @pytest.mark.parametrize("rows,cols,dtype", [(64, 262144, "fp32"), (3, 70000, "fp32"), (1, 1 << 20, "fp32"),
                                              (100, 40000, "fp32"), (8, 131072, "bf16"), (2, 300000, "bf16")])
-def test_long_rows_single_pass_and_split(pkg, oracle, dev, rows, cols, dtype):
-    """Long rows through the co-resident single-pass tier (4) and the two-pass split tier (2), forced in turn."""
+def test_long_rows_single_pass_and_stream(pkg, oracle, dev, rows, cols, dtype):
+    """Long rows through the co-resident single-pass tier (4) and the two-pass stream tier (2), preferred in turn."""
     lib = pkg.candidate("softmax")._lib
     g = torch.Generator().manual_seed(rows + cols)
     x = torch.randn(rows, cols, generator=g) * 4
@@ -109,9 +110,9 @@ def test_long_rows_single_pass_and_split(pkg, oracle, dev, rows, cols, dtype):
 
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])
 def test_single_pass_fallback_when_the_wait_ends(pkg, oracle, dev, dtype):
-    """The co-resident tier with its wait bounded to one poll (forced from the host): workgroups that find their row's
-    pairs incomplete take the row's statistics from x, the rest merge the pairs; every output stays within the
-    tolerance, over repeated launches (the row's slots are cleared for the next either way)."""
+    """The co-resident tier with its wait bounded to one tick of its clock (forced from the host): workgroups that find
+    their row's pairs incomplete take the row's statistics from x, the rest merge the pairs; every output stays within
+    the tolerance, over repeated launches, with one row per workgroup and with row groups walking several rows."""
     lib = pkg.candidate("softmax")._lib
     g = torch.Generator().manual_seed(21)
     x = torch.randn(6, 262144 + 4096, generator=g) * 4
@@ -126,8 +127,9 @@ def test_single_pass_fallback_when_the_wait_ends(pkg, oracle, dev, dtype):
     try:
         lib.softmax_tune(5, 4)
         lib.softmax_tune(7, 1)
-        for rep in range(3):
-            print(f"[softmax fallback] {dtype} launch {rep}", flush=True)
+        for rep, groups in enumerate((0, 0, 2, 4)):
+            lib.softmax_tune(4, groups)
+            print(f"[softmax fallback] {dtype} launch {rep} groups={groups}", flush=True)
             y = pkg.softmax(xd)
             if dtype == "bf16":
                 assert_ulp(bits16(y), ref, 1, f"launch {rep}")
@@ -136,6 +138,7 @@ def test_single_pass_fallback_when_the_wait_ends(pkg, oracle, dev, dtype):
     finally:
         lib.softmax_tune(7, 0)
         lib.softmax_tune(5, 0)
+        lib.softmax_tune(4, 0)
     y = pkg.softmax(xd)  # the default wait again, on the slots the fallback launches left
     if dtype == "bf16":
         assert_ulp(bits16(y), ref, 1, "after")
@@ -143,8 +146,53 @@ def test_single_pass_fallback_when_the_wait_ends(pkg, oracle, dev, dtype):
         assert_rel(y.cpu().numpy(), ref, FP32_TOL, "after")
 
 
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_single_pass_rows_beyond_one_wave(pkg, oracle, dev, dtype):
+    """More long rows than the GPU holds chunks of at once (the reference's 256 x 262144 README shape): row groups walk
+    several rows each, still one read of x; and row groups forced down to 1, 3 and 5 (many rows per workgroup, the
+    pair table's two parities in turn, the last iteration of some groups shorter)."""
+    lib = pkg.candidate("softmax")._lib
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(256, 262144, generator=g) * 5
+    x[3, :100000] = float("-inf")
+    if dtype == "bf16":
+        x = x.bfloat16()
+        ref = oracle.softmax(bits16(x), "bf16")
+    else:
+        ref = oracle.softmax(x.numpy(), "fp32")
+    print(f"[softmax groups] 256x262144 {dtype}", flush=True)
+    y = pkg.softmax(x.to(dev))
+    if dtype == "bf16":
+        assert_ulp(bits16(y), ref, 1, "256x262144")
+    else:
+        assert_rel(y.cpu().numpy(), ref, FP32_TOL, "256x262144")
+    xs = x[:13, :70000].contiguous()
+    refs = oracle.softmax(bits16(xs), "bf16") if dtype == "bf16" else oracle.softmax(xs.numpy(), "fp32")
+    xd = xs.to(dev)
+    try:
+        lib.softmax_tune(5, 4)
+        for groups in (1, 3, 5):
+            lib.softmax_tune(4, groups)
+            print(f"[softmax groups] 13x70000 {dtype} groups={groups}", flush=True)
+            for _ in range(2):
+                y = pkg.softmax(xd)
+                if dtype == "bf16":
+                    assert_ulp(bits16(y), refs, 1, f"groups {groups}")
+                else:
+                    assert_rel(y.cpu().numpy(), refs, FP32_TOL, f"groups {groups}")
+    finally:
+        lib.softmax_tune(4, 0)
+        lib.softmax_tune(5, 0)
+
+
+def test_rows_beyond_the_single_pass_tier(pkg, oracle, dev):
+    """A row of more than 64 chunks (16384 fp32 each) takes the two-pass stream tier."""
+    g = torch.Generator().manual_seed(23)
+    run_fp32(pkg, oracle, dev, torch.randn(2, (1 << 20) + 4096, generator=g) * 3, "2x(2^20+4096)")
+
+
 def test_single_pass_back_to_back_shapes(pkg, oracle, dev):
-    """Consecutive single-pass launches of different shapes on one stream: each leaves its row counters at zero."""
+    """Consecutive single-pass launches of different shapes on one stream: each takes fresh tags in the pair table."""
     g = torch.Generator().manual_seed(9)
     xs = [torch.randn(64, 262144, generator=g), torch.randn(5, 50000, generator=g),
           torch.randn(16, 1 << 18, generator=g), torch.randn(5, 50000, generator=g)]
@@ -199,5 +247,5 @@ def test_tuning_overrides_keep_results(pkg, oracle, dev):
             print(f"[softmax tune] tier={tier}", flush=True)
             assert_rel(pkg.softmax(xd).cpu().numpy(), ref, FP32_TOL, f"tier {tier}")
     finally:
-        for slot in range(7):
+        for slot in range(8):
             lib.softmax_tune(slot, 0)
