@@ -16,6 +16,7 @@
 // published bounds, and the output row is ordered by bucketing and ranking in LDS.
 #include <climits>
 #include <cstdint>
+#include <mutex>
 #include <type_traits>
 
 #include "host.hpp"
@@ -1796,6 +1797,76 @@ extern "C" int topk_launch_sample(const void* x, void* values, void* indices, vo
   if (rows > 0 && k > 0 && (!uniforms || !out)) return rw_host::kInvalid;
   return launch_impl(x, values, indices, work, counters, rows, cols, k, dtype, threads, depth, chunk,
                      SampleArgs{uniforms, (long long*)out, temperature, top_p}, stream);
+}
+
+// ---- the allocation-free entry point ---------------------------------------------------------------------------------
+
+// Scratch of topk_launch_noalloc, one copy per GPU the library runs on, held until the process ends: the per-row
+// arrival counters (kNoAllocRows u32) and then the chunk results (up to kNoAllocWork bytes of u64 slots). In host code
+// `scratch` names a host-side stand-in, not device memory: the launcher asks for its device address once per device
+// (hipGetSymbolAddress) and passes that address to the kernels.
+constexpr size_t kNoAllocRows = 65536;                     // rows > 65535 are rejected by launch() anyway
+constexpr size_t kNoAllocCounterBytes = kNoAllocRows * 4;  // 256 KiB
+constexpr size_t kNoAllocWork = (size_t)16 << 20;          // 16 MiB of chunk results: rows * nchunks * k * 8 bytes
+static __device__ __align__(256) unsigned char scratch[kNoAllocCounterBytes + kNoAllocWork];
+
+namespace {
+constexpr int kMaxDevices = 64;
+
+// The device address of `scratch` on the current device, looked up once per device; nullptr with *err set on failure.
+unsigned char* scratch_address(int* err) {
+  static std::mutex mu;
+  static unsigned char* addr[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *err = e != hipSuccess ? (int)e : rw_host::kInvalid;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *err = e != hipSuccess ? (int)e : rw_host::kInvalid;
+      return nullptr;
+    }
+    addr[dev] = static_cast<unsigned char*>(p);
+  }
+  *err = rw_host::kOk;
+  return addr[dev];
+}
+
+}  // namespace
+
+// No counterpart in the reference: launch() for callers that cannot allocate device memory (code under HIP graph
+// capture, tight serving loops, harnesses that forbid hipMalloc). The same arguments without work and counters: the
+// library's static per-GPU scratch holds them, and the call allocates nothing. Each call first zeroes the scratch's
+// counters for its rows with a small kernel (no memset node, so the call may be captured into a graph), then runs
+// launch()'s kernels. -1 as launch(), and also when a split row's results would not fit the scratch (rows * nchunks *
+// k * 8 bytes above 16 MiB, nchunks = ceil(cols / chunk)). Every call on one GPU uses that GPU's one scratch: calls that
+// overlap on one GPU (two streams, or two host threads) race and must be ordered by the caller.
+extern "C" int topk_launch_noalloc(const void* x, void* values, void* indices, long long rows, long long cols, int k,
+                                   int dtype, int threads, int depth, long long chunk, hipStream_t stream) {
+  if (rows <= 0 || k <= 0) return rw_host::kOk;
+  if (k > cols || k > kMaxK || cols > INT_MAX / 2 || rows > 65535 || chunk <= 0) return rw_host::kInvalid;
+  const long long nchunks = (cols + chunk - 1) / chunk;
+  if (nchunks > 1 && (unsigned long long)rows * (unsigned long long)nchunks * (unsigned long long)k * 8ull >
+                         (unsigned long long)kNoAllocWork)
+    return rw_host::kInvalid;
+  int err = rw_host::kOk;
+  unsigned char* base = scratch_address(&err);
+  if (!base) return err;
+  unsigned* counters = reinterpret_cast<unsigned*>(base);
+  u64* work = reinterpret_cast<u64*>(base + kNoAllocCounterBytes);
+  if (nchunks > 1) {
+    long long grid = (rows + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(topk_zero, dim3((unsigned)grid), dim3(kThreads), 0, stream, counters, rows);
+    err = (int)hipGetLastError();
+    if (err != rw_host::kOk) return err;
+  }
+  return launch_impl(x, values, indices, work, counters, rows, cols, k, dtype, threads, depth, chunk,
+                     SampleArgs{nullptr, nullptr, 0.0f, 0.0f}, stream);
 }
 
 // No counterpart in the reference (whose counters self-reset only when a launch completes): zeroes counters[0, rows)

@@ -33,6 +33,16 @@ long long plan(long long rows, long long cols, int dtype, int threads, int depth
 int launch(const void* x, void* values, void* indices, void* work, void* counters, long long rows, long long cols,
            int k, int dtype, int threads, int depth, long long chunk, hipStream_t stream);
 
+/* No counterpart in the reference: launch() for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The same arguments and checks without work and
+ * counters, which live in a static scratch of the library, one per GPU, held until the process ends: 256 KiB of row
+ * counters and 16 MiB of chunk results. Each call zeroes its counters with a small kernel first (no memset node) and
+ * allocates nothing. -1 also when a split row's results would not fit (rows * nchunks * k * 8 bytes above 16 MiB,
+ * nchunks = ceil(cols / chunk)). All calls on one GPU share that GPU's scratch: calls that overlap on one GPU (two
+ * streams, two host threads) race and must be ordered by the caller. */
+int topk_launch_noalloc(const void* x, void* values, void* indices, long long rows, long long cols, int k, int dtype,
+                        int threads, int depth, long long chunk, hipStream_t stream);
+
 /* No counterpart in the reference (whose counters self-reset only when a launch completes): zeroes counters[0, rows)
  * on `stream` with a small kernel, for a caller recovering from a launch that did not complete. Returns 0, -1 (NULL
  * counters) or the hipError_t of the launch. */
