@@ -40,6 +40,7 @@ def lib():
         L.oracle_rmsnorm.argtypes = [vp, vp, vp, ll, ll, i, f, vp]
         L.oracle_rmsnorm_add.argtypes = [vp, vp, vp, vp, vp, ll, ll, i, f]
         L.oracle_topk_sample.argtypes = [vp, vp, vp, vp, ll, i, i, f, f, vp]
+        L.oracle_topk_sample_band.argtypes = [vp, vp, vp, vp, ll, i, i, f, f]
         L.oracle_rope_cache.argtypes = [vp, vp, vp, vp, vp, vp, vp, ll, i, i, i, i, i]
         L.oracle_rope_freq.argtypes = [vp, vp, vp, vp, vp, vp, ll, i, i, i, i]
         L.oracle_rope_table.argtypes = [vp, ll, i, vp, vp]
@@ -49,7 +50,7 @@ def lib():
         L.oracle_f32_to_f16.argtypes = [f]
         L.oracle_f32_to_f16.restype = ctypes.c_uint16
         for fn in ("oracle_softmax", "oracle_rmsnorm", "oracle_rope_cache", "oracle_rope_freq", "oracle_rope_table",
-                   "oracle_topk"):
+                   "oracle_topk", "oracle_topk_sample", "oracle_topk_sample_band"):
             getattr(L, fn).restype = None
         _lib = L
     return _lib
@@ -184,3 +185,25 @@ def topk_sample(values, indices, u, temperature=1.0, top_p=1.0, dtype="fp32"):
     lib().oracle_topk_sample(_ptr(vals), _ptr(idx), _ptr(uu), _ptr(out), rows, k, 0 if dtype == "fp32" else 1,
                              ctypes.c_float(temperature), ctypes.c_float(top_p), _ptr(amb))
     return out, amb.astype(bool)
+
+
+def topk_sample_band(values, indices, u, temperature=1.0, top_p=1.0, dtype="fp32"):
+    """The admissible draws of topk_sample for every row: (lo, hi) int arrays of list positions, the draws that the
+    rule gives when its sums, cut and target each move by up to 1e-5 of the row's total (fp32 evaluation in any order).
+    A draw is correct when it is one of indices[r, lo[r]..hi[r]]."""
+    vals = _c(values, np.float32 if dtype == "fp32" else np.uint16)
+    uu = _c(u, np.float32)
+    rows, k = np.asarray(indices).shape
+    lo = np.empty(rows, dtype=np.int32)
+    hi = np.empty(rows, dtype=np.int32)
+    lib().oracle_topk_sample_band(_ptr(vals), _ptr(uu), _ptr(lo), _ptr(hi), rows, k, 0 if dtype == "fp32" else 1,
+                                  ctypes.c_float(temperature), ctypes.c_float(top_p))
+    return lo, hi
+
+
+def draw_admissible(drawn, indices, lo, hi):
+    """Whether each row's drawn index is one of indices[r, lo[r]..hi[r]]."""
+    idx = np.asarray(indices)
+    pos = np.arange(idx.shape[1])[None, :]
+    window = (pos >= np.asarray(lo)[:, None]) & (pos <= np.asarray(hi)[:, None])
+    return ((idx == np.asarray(drawn)[:, None]) & window).any(axis=1)

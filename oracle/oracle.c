@@ -329,3 +329,64 @@ void oracle_topk_sample(const void* values, const int64_t* indices, const float*
   }
   free(S);
 }
+
+/* The admissible draws of oracle_topk_sample for every row, as a range of list positions [lo[r], hi[r]]: the positions
+ * that the draw rule picks when the prefix sums S_i, the cut top_p * S_(k-1) and the target u * S_(kept-1) each move by
+ * up to tol = 1e-5 of the total (what fp32 evaluation of the same rule, in any order of summation over k <= 1024 terms,
+ * stays within). A row whose u and cut lie away from every boundary gets lo = hi = the exact draw's position; a row near
+ * one gets the two (rarely more) positions either side; the exact draw is always in the band. temperature <= 0:
+ * [0, 0]. */
+void oracle_topk_sample_band(const void* values, const float* u, int* lo, int* hi, long long rows, int k, int dtype,
+                             float temperature, float top_p) {
+  double* S = (double*)malloc(sizeof(double) * (size_t)k);
+  for (long long r = 0; r < rows; ++r) {
+    if (temperature <= 0.0f) {
+      lo[r] = hi[r] = 0;
+      continue;
+    }
+    double m = -INFINITY;
+    for (int i = 0; i < k; ++i) {
+      const double x = (double)load_fmt(values, r * k + i, dtype == 1 ? 1 : 0) / (double)temperature;
+      if (x > m) m = x;
+    }
+    double run = 0.0;
+    for (int i = 0; i < k; ++i) {
+      const double x = (double)load_fmt(values, r * k + i, dtype == 1 ? 1 : 0) / (double)temperature;
+      run += exp(x - m);
+      S[i] = run;
+    }
+    const double total = S[k - 1], tol = 1e-5 * total, cut = (double)top_p * total;
+    /* the kept counts the cut allows: 1 + the positions i >= 1 whose S_(i-1) is below the cut, +- the tolerance */
+    int kmin = top_p >= 1.0f ? k : 1, kmax = kmin;
+    for (int i = 1; i < k && top_p < 1.0f; ++i) {
+      if (S[i - 1] < cut - 2.0 * tol) kmin = i + 1;
+      if (S[i - 1] < cut + 2.0 * tol) kmax = i + 1;
+    }
+    /* the exact draw (oracle_topk_sample's rule) is always admissible; it is also the whole band of a row whose sums
+     * are not finite, where no comparison holds (values must be finite when temperature > 0) */
+    int kept0 = top_p >= 1.0f ? k : 1;
+    for (int i = 1; i < k && top_p < 1.0f; ++i)
+      if (S[i - 1] < cut) kept0 = i + 1;
+    const double target0 = (double)u[r] * S[kept0 - 1];
+    int l = kept0 - 1;
+    for (int i = 0; i < kept0; ++i)
+      if (S[i] > target0 && i < l) l = i;
+    int h = l;
+    for (int kept = kmin; kept <= kmax; ++kept) {
+      const double target = (double)u[r] * S[kept - 1];
+      /* position i can be the first kept one above the target; and the last kept one when none may be above it */
+      for (int i = 0; i < kept; ++i) {
+        const int above = S[i] > target - 2.0 * tol;
+        const int first = i == 0 || S[i - 1] <= target + 2.0 * tol;
+        const int last = i == kept - 1 && S[i] <= target + 2.0 * tol;
+        if ((above && first) || last) {
+          if (i < l) l = i;
+          if (i > h) h = i;
+        }
+      }
+    }
+    lo[r] = l;
+    hi[r] = h;
+  }
+  free(S);
+}

@@ -33,8 +33,9 @@ def build(tmpdir, source, driver):
     stem = os.path.splitext(source)[0]
     kern = kernel_source(tmpdir, source)
     obj = os.path.join(str(tmpdir), "oracle.o")
-    if not os.path.exists(obj):
-        subprocess.run(["gcc", "-O2", "-c", os.path.join(ROOT, "oracle", "oracle.c"), "-o", obj], check=True)
+    src = os.path.join(ROOT, "oracle", "oracle.c")
+    if not os.path.exists(obj) or os.path.getmtime(obj) < os.path.getmtime(src):
+        subprocess.run(["gcc", "-O2", "-c", src, "-o", obj], check=True)
     exe = os.path.join(str(tmpdir), "emu_" + stem)
     proc = subprocess.run([clang, "-std=c++17", "-O1", "-U_FORTIFY_SOURCE", "-D_FORTIFY_SOURCE=0",
                            "-fno-strict-aliasing", "-w", "-pthread", "-I", EMU, "-I", CSRC, kern,
@@ -73,8 +74,9 @@ def build_driver(tmpdir, driver, libs=("-ldl",)):
     if clang is None or shutil.which("gcc") is None:
         pytest.skip("clang++ or gcc is missing")
     obj = os.path.join(str(tmpdir), "oracle_pic.o")
-    if not os.path.exists(obj):
-        subprocess.run(["gcc", "-O2", "-fPIC", "-c", os.path.join(ROOT, "oracle", "oracle.c"), "-o", obj], check=True)
+    src = os.path.join(ROOT, "oracle", "oracle.c")
+    if not os.path.exists(obj) or os.path.getmtime(obj) < os.path.getmtime(src):
+        subprocess.run(["gcc", "-O2", "-fPIC", "-c", src, "-o", obj], check=True)
     exe = os.path.join(str(tmpdir), os.path.splitext(driver)[0])
     # -rdynamic: the emulation runtime's state (allocation count, schedules) is the driver's, shared by every library
     # the driver opens; each library keeps its own kernels and statics

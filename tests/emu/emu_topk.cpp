@@ -1,9 +1,10 @@
 // Runs csrc/topk.hip's plan() and launch() under the CPU emulation (hip/hip_runtime.h beside this file) and compares
 // every launch with the oracle (oracle/oracle.c: oracle_topk), bit for bit: values, int64 indices, and the caller's
-// counters left at zero; a launch must not allocate (the caller's work and counters carry the hand-off). Each launch is followed by topk_launch_sample(), whose values, indices and draws must equal
-// launch()'s and topk_sample_launch()'s on them, and the draws the oracle's (oracle_topk_sample) wherever the uniform
-// is not within its tolerance band of an interval edge. Every buffer the kernels touch (input, outputs, work and
-// counters) lies between guard pages.
+// counters left at zero; a launch must not allocate (the caller's work and counters carry the hand-off). Each launch
+// is followed by topk_launch_sample(), whose values, indices and draws must equal launch()'s and
+// topk_sample_launch()'s on them, with every draw one of the oracle's admissible draws (oracle_topk_sample_band: the
+// exact draw's position, and its neighbour where the uniform or the nucleus cut lies within rounding of a boundary).
+// Every buffer the kernels touch (input, outputs, work and counters) lies between guard pages.
 //
 // usage: emu_topk rows cols dtype ks chunk min_chunk reps seed [shuffle_seed [pattern]]
 //   dtype 0 fp32, 1 bf16; ks comma-separated; chunk 0 takes plan()'s (min_chunk max 16k for k > 64, as the
@@ -32,6 +33,8 @@ extern "C" int topk_sample_launch(const void* values, const void* indices, const
                                   hipStream_t stream);
 extern "C" void oracle_topk(const void* x, void* values, int64_t* indices, long long rows, long long cols, int k,
                             int dtype);
+extern "C" void oracle_topk_sample_band(const void* values, const float* u, int* lo, int* hi, long long rows, int k,
+                                        int dtype, float temperature, float top_p);
 extern "C" void oracle_topk_sample(const void* values, const int64_t* indices, const float* u, int64_t* out,
                                    long long rows, int k, int dtype, float temperature, float top_p, int* ambiguous);
 
@@ -138,11 +141,14 @@ int main(int argc, char** argv) {
       const int err3 = topk_sample_launch(vals, idx, uni, drawn1, rows, k, dtype, temperature, top_p, nullptr);
       bool fused_ok = !err2 && !err3 && std::memcmp(vals2, vals, rows * k * esz) == 0 &&
                       std::memcmp(idx2, idx, rows * k * 8) == 0 && std::memcmp(drawn1, drawn2, rows * 8) == 0;
-      // and the oracle's draw, on rows whose uniform is not within the tolerance band of an interval edge
-      std::vector<int64_t> rd(rows);
-      std::vector<int> amb(rows);
-      oracle_topk_sample(rv.data(), ri.data(), uni, rd.data(), rows, k, dtype, temperature, top_p, amb.data());
-      for (long long r = 0; r < rows; ++r) fused_ok &= amb[r] || ((int64_t*)drawn2)[r] == rd[r];
+      // and the oracle's admissible draws, every row
+      std::vector<int> lo(rows), hi(rows);
+      oracle_topk_sample_band(rv.data(), uni, lo.data(), hi.data(), rows, k, dtype, temperature, top_p);
+      for (long long r = 0; r < rows; ++r) {
+        bool in = false;
+        for (int p = lo[r]; p <= hi[r] && p < k; ++p) in |= ((int64_t*)drawn2)[r] == ri[r * k + p];
+        fused_ok &= in;
+      }
       hipFree(vals2);
       hipFree(idx2);
       hipFree(drawn1);

@@ -47,7 +47,7 @@
 #define __forceinline__ inline
 #define __launch_bounds__(...)
 #define __shared__ static thread_local
-#define __align__(n) alignas(n)
+#define __align__(n) __attribute__((aligned(n)))
 #define EMU_ASM(...) emu::asm_hook(#__VA_ARGS__)
 
 typedef int hipError_t;
@@ -580,6 +580,12 @@ inline hipError_t hipGetDevice(int* d) {
   return hipSuccess;
 }
 inline hipError_t hipGetLastError() { return hipSuccess; }
+// a device variable's address: on the host of this emulation the variable itself
+#define HIP_SYMBOL(x) (&(x))
+inline hipError_t hipGetSymbolAddress(void** p, const void* symbol) {
+  *p = const_cast<void*>(symbol);
+  return hipSuccess;
+}
 inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {
   *v = 256;
   return hipSuccess;

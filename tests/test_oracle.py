@@ -421,3 +421,60 @@ def test_topk_sample_frequencies(oracle):
     q = p[:kept] / c[kept - 1]
     freq = np.array([(got == i[0, j]).mean() for j in range(kept)])
     assert np.abs(freq - q).max() < 2.0 / n and set(got) <= set(i[0, :kept])
+
+
+def _fp32_draws(v, i, u, T, top_p, order):
+    """The draw rule evaluated in fp32 with a given association of the prefix sums: 'seq' (left to right), 'blocks'
+    (sums inside blocks of 16, then across blocks, as a wave of lanes holding 16 each would), 'rev' (each prefix sum
+    accumulated from its last term back to its first)."""
+    x = (v.astype(np.float32) / np.float32(T)).astype(np.float32)
+    e = np.exp((x - x.max(axis=1, keepdims=True)).astype(np.float32)).astype(np.float32)
+    rows, k = e.shape
+    S = np.empty_like(e)
+    for r in range(rows):
+        if order == "seq":
+            S[r] = np.cumsum(e[r], dtype=np.float32)
+        elif order == "blocks":
+            acc = np.float32(0)
+            for b in range(0, k, 16):
+                part = np.cumsum(e[r, b:b + 16], dtype=np.float32)
+                S[r, b:b + 16] = (part + acc).astype(np.float32)
+                acc = np.float32(acc + part[-1])
+        else:
+            S[r] = [np.sum(e[r, :j + 1][::-1], dtype=np.float32) for j in range(k)]
+    out = np.empty(rows, dtype=np.int64)
+    for r in range(rows):
+        tot = S[r, -1]
+        kept = k if top_p >= 1 else 1 + int(np.sum(S[r, :-1] < np.float32(top_p) * tot))
+        target = np.float32(u[r]) * S[r, kept - 1]
+        above = np.nonzero(S[r, :kept] > target)[0]
+        out[r] = i[r, above[0] if len(above) else kept - 1]
+    return out
+
+
+def test_topk_sample_band_holds_every_fp32_evaluation(oracle):
+    """The admissible band contains the exact (fp64) draw and the draws of the rule evaluated in fp32 under three
+    associations of the prefix sums; it is one position wide on most rows (wider only where u or the nucleus cut lies
+    within rounding of a boundary), and never more than three."""
+    for k, seed in ((50, 51), (300, 52), (1024, 53)):
+        v, i = _sorted_list(48, k, seed)
+        u = np.random.default_rng(seed).random(48, dtype=np.float32)
+        for T, top_p in ((0.8, 0.9), (1.0, 1.0), (0.5, 0.3)):
+            exact, amb = oracle.topk_sample(v, i, u, T, top_p)
+            lo, hi = oracle.topk_sample_band(v, i, u, T, top_p)
+            assert oracle.draw_admissible(exact, i, lo, hi).all()
+            assert (hi - lo).max() <= 2 and (hi > lo).mean() <= max(0.1, amb.mean())
+            for order in ("seq", "blocks", "rev"):
+                d = _fp32_draws(v, i, u, T, top_p, order)
+                assert oracle.draw_admissible(d, i, lo, hi).all(), (k, T, top_p, order)
+
+
+def test_topk_sample_band_rejects_a_wrong_draw(oracle):
+    # a draw one position off (the planted mistake of an off-by-one search) falls outside the band on most rows
+    v, i = _sorted_list(200, 64, 54)
+    u = np.random.default_rng(3).random(200, dtype=np.float32)
+    exact, _ = oracle.topk_sample(v, i, u, 1.0, 1.0)
+    lo, hi = oracle.topk_sample_band(v, i, u, 1.0, 1.0)
+    pos = np.argmax(i == exact[:, None], axis=1)
+    shifted = i[np.arange(200), np.minimum(pos + 1, 63)]
+    assert oracle.draw_admissible(shifted, i, lo, hi).mean() < 0.1
