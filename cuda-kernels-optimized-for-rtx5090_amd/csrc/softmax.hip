@@ -468,6 +468,9 @@ int launch_rows_w(int nv, const void* x, void* y, long long rows, long long nvec
     case 2: return launch_rows_nv<T, WAVES, 2, NTL>(x, y, rows, nvec, stream);
     case 4: return launch_rows_nv<T, WAVES, 4, NTL>(x, y, rows, nvec, stream);
     case 8: return launch_rows_nv<T, WAVES, 8, NTL>(x, y, rows, nvec, stream);
+    case 16:  // (through the tuning slots: one or two waves holding a row of up to 8192 fp32 / 16384 bf16 elements)
+      if constexpr (WAVES <= 2) return launch_rows_nv<T, WAVES, 16, NTL>(x, y, rows, nvec, stream);
+      else return rw_host::kInvalid;
     default: return rw_host::kInvalid;
   }
 }
