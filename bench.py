@@ -67,6 +67,8 @@ def parse():
     p.add_argument("--ceiling", action="store_true",
                    help="only time the bandwidth probes (build/probe): a 1R + 1W copy moving each workload's "
                         "algorithmic bytes, and a read of the top-k input")
+    p.add_argument("--profile-summary", default=None,
+                   help="directory of one profiling lease (bench.json, stats/, traffic/, occ/): writes profiles/")
     p.add_argument("--traffic-from", default=None,
                    help="directory with rocprofv3 counter CSVs (fetch/ and write/ runs of this script and of "
                         "--copy-calibration); writes profiles/traffic.json")
@@ -476,10 +478,130 @@ def traffic_from(run_dir):
     print(json.dumps(out))
 
 
+def kernel_stats(db_path):
+    """Per-kernel call count and average duration (us) from a rocprofv3 --kernel-trace --stats database."""
+    import sqlite3
+    con = sqlite3.connect(db_path)
+    rows = con.execute("select name, total_calls, average from top_kernels").fetchall()
+    con.close()
+    return [(name, int(calls), float(avg)) for name, calls, avg in rows]
+
+
+def short_kernel(name):
+    """A kernel's symbol without the return type, namespaces and argument list, template arguments kept."""
+    return name.replace("void ", "").replace("(anonymous namespace)::", "").replace("at::native::", "").split("(")[0]
+
+
+def occupancy(run_dir, cus=256, xcds=8):
+    """Per-kernel means per dispatch of the occupancy and instruction counters in run_dir's counter CSVs: resident
+    waves per CU (4 * SQ_WAVE_CYCLES, which counts in units of four cycles, over the busy cycles of one XCD,
+    GRBM_GUI_ACTIVE / xcds as read summed over the XCDs, over the CUs), the occupancy as a % of the 32 waves a CU holds
+    (rocprofv3's OccupancyPercent formula for gfx950), and the instructions issued per wave."""
+    out = {}
+    for name in ("SQ_WAVES", "SQ_WAVE_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS"):
+        for kernel, v in counter_means(run_dir, name).items():
+            out.setdefault(kernel, {})[name] = v
+    res = {}
+    for kernel, c in out.items():
+        if len(c) < 6 or c["SQ_WAVES"] <= 64:
+            continue
+        busy = c["GRBM_GUI_ACTIVE"] / xcds
+        waves = 4 * c["SQ_WAVE_CYCLES"] / busy / cus
+        res[kernel] = {"waves": int(c["SQ_WAVES"]), "resident_waves_per_cu": round(waves, 2),
+                       "occupancy_pct": round(100 * waves / 32, 1),
+                       "valu_per_wave": round(c["SQ_INSTS_VALU"] / c["SQ_WAVES"]),
+                       "salu_per_wave": round(c["SQ_INSTS_SALU"] / c["SQ_WAVES"]),
+                       "lds_per_wave": round(c["SQ_INSTS_LDS"] / c["SQ_WAVES"])}
+    return res
+
+
+def profile_summary(run_dir):
+    """Writes profiles/ from one profiling lease (run_dir as the profiling script leaves it: bench.json and
+    bench.err of the bench line, stats/ of the kernel trace, traffic/ of the FETCH_SIZE / WRITE_SIZE runs, occ/ of the
+    occupancy runs): kernel_trace_bench_workloads.txt, traffic.json and traffic_counters.txt, and
+    occupancy_bench_workloads.txt."""
+    prof = os.path.join(ROOT, "profiles")
+    with open(os.path.join(run_dir, "bench.json")) as f:
+        line = json.loads(f.read().strip().splitlines()[-1])
+    dbs = glob.glob(os.path.join(run_dir, "stats", "**", "*results.db"), recursive=True)
+    stats = kernel_stats(dbs[0]) if dbs else []
+    lines = ["# Kernel durations on MI355X: rocprofv3 kernel trace of bench.py, with bench.py's own figures from the same",
+             "# lease (one fresh box, the same binaries)", "",
+             "Commands (from /tmp, TMPDIR=/tmp):",
+             "    python3 bench.py                                                        -> the bench line",
+             "    rocprofv3 --kernel-trace --stats -d <dir>/stats -o s -- python3 bench.py --no-cold --no-cpu",
+             "    python3 bench.py --profile-summary <dir>                                -> this file", "",
+             f"{'kernel':<76} {'calls':>6} {'avg us':>9}"]
+    for name, calls, avg in sorted(stats, key=lambda r: -r[1] * r[2]):
+        lines.append(f"{short_kernel(name)[:76]:<76} {calls:>6} {avg:>9.2f}")
+    lines += ["", "bench.py (back-to-back launches over rotating copies; single flushed launch median):",
+              f"{'workload':<34} {'us/launch':>10} {'GB/s':>8} {'% of 8 TB/s':>12} {'flushed us':>11}"]
+    for lab, r in line["per_workload"].items():
+        lines.append(f"{lab:<34} {r['us_mean']:>10.2f} {r['gbs']:>8.0f} {r['pct_peak']:>12.1f} "
+                     f"{r.get('cold_us_median', float('nan')):>11.2f}")
+    with open(os.path.join(prof, "kernel_trace_bench_workloads.txt"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    traffic_from(os.path.join(run_dir, "traffic"))
+    with open(TRAFFIC_PATH) as f:
+        tr = json.load(f)
+    from __graft_entry__ import load_package
+    pkg = load_package()
+    t_lines = ["# HBM traffic per launch from rocprofv3 counters", "",
+               "Commands (from /tmp, TMPDIR=/tmp, one counter per run; W in the workloads below):",
+               "    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir>/traffic/W_fetch -o p -- python3 bench.py "
+               "--workload W --steps 5 --warmup 1 --no-cold --no-cpu",
+               "    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir>/traffic/W_write -o p -- python3 bench.py "
+               "--workload W --steps 5 --warmup 1 --no-cold --no-cpu",
+               "    (top-k: --workload topk_128x128256 --k 50, and --k 1024)",
+               "    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir>/traffic/copy_fetch -o p -- python3 bench.py "
+               "--copy-calibration --steps 5   (and WRITE_SIZE into copy_write)",
+               "    python3 bench.py --profile-summary <dir>   -> profiles/traffic.json and this file", "",
+               f"Calibration: a 256 MiB torch sum counts FETCH_SIZE {tr['calibration_fetch_kib']} KiB -> fetch scale "
+               f"{tr['fetch_scale']};",
+               f"             a 256 MiB torch fill counts WRITE_SIZE {tr['calibration_write_kib']} KiB -> write scale "
+               f"{tr['write_scale']}.", "",
+               f"{'workload':<28} {'kernels':<14} {'FETCH KiB':>10} {'WRITE KiB':>10} {'bytes/launch':>13} "
+               f"{'algorithmic':>12} {'ratio':>6}"]
+    for label, r in tr.items():
+        if label.startswith("_") or not isinstance(r, dict):
+            continue
+        name, _, kk = label.partition("_k")
+        k = int(kk) if kk.isdigit() else None
+        if k is None:
+            name = label
+        algo = pkg.workloads.algorithmic_bytes(name, k or 50)
+        t_lines.append(f"{label:<28} {r['kernel']:<14} {r['fetch_kib']:>10.1f} {r['write_kib']:>10.1f} "
+                       f"{r['bytes_per_launch']:>13} {algo:>12} {r['bytes_per_launch'] / algo:>6.3f}")
+    with open(os.path.join(prof, "traffic_counters.txt"), "w") as f:
+        f.write("\n".join(t_lines) + "\n")
+    occ_lines = ["# Occupancy and instructions per wave on MI355X (rocprofv3 counters, per dispatch, mean over the "
+                 "dispatches of each kernel)", "",
+                 "Command (from /tmp, TMPDIR=/tmp, one run per workload W):",
+                 "    rocprofv3 --pmc SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_INSTS_SALU SQ_INSTS_LDS "
+                 "GRBM_GUI_ACTIVE --output-format csv -d <dir>/occ/W -o p -- python3 bench.py --workload W --steps 5 "
+                 "--warmup 1 --no-cold --no-cpu",
+                 "resident waves per CU = 4 * SQ_WAVE_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs) / 256 CUs; occupancy = that "
+                 "/ 32 waves per CU (rocprofv3's OccupancyPercent for gfx950); over the whole dispatch, ramp and tail "
+                 "included", "",
+                 f"{'workload':<26} {'kernel':<52} {'waves':>6} {'waves/CU':>9} {'occ %':>6} {'VALU/w':>7} "
+                 f"{'SALU/w':>7} {'LDS/w':>6}"]
+    for w in sorted(os.listdir(os.path.join(run_dir, "occ"))):
+        for kernel, r in occupancy(os.path.join(run_dir, "occ", w)).items():
+            occ_lines.append(f"{w:<26} {short_kernel(kernel)[:52]:<52} {r['waves']:>6} {r['resident_waves_per_cu']:>9} "
+                             f"{r['occupancy_pct']:>6} {r['valu_per_wave']:>7} {r['salu_per_wave']:>7} "
+                             f"{r['lds_per_wave']:>6}")
+    with open(os.path.join(prof, "occupancy_bench_workloads.txt"), "w") as f:
+        f.write("\n".join(occ_lines) + "\n")
+    print("\n".join(lines + [""] + t_lines + [""] + occ_lines))
+
+
 def main():
     args = parse()
     if args.traffic_from:
         traffic_from(args.traffic_from)
+        return
+    if args.profile_summary:
+        profile_summary(args.profile_summary)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
