@@ -3,6 +3,9 @@
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cold] [--no-cpu]
     python bench.py --copy-calibration          # plain kernels of known traffic, for the counter scaling
     python bench.py --ceiling                   # the practical HBM ceiling at each workload's size (probe kernels)
+    python bench.py --probes                    # every probe structure and cache policy at each workload's size
+    python bench.py --build-probes              # compile the probes (bench_probes.hip) into _build/
+    python bench.py --profile-summary DIR       # turn one profiling lease's outputs into profiles/
     python bench.py --traffic-from DIR          # turn FETCH_SIZE / WRITE_SIZE counter runs into profiles/traffic.json
 
 A step is one launch of the op over its whole workload with the inputs already resident in HBM. Each workload is
@@ -65,8 +68,16 @@ def parse():
                    help="only launch a 256 MiB read-only and a 256 MiB write-only kernel --steps times (for the "
                         "counter scaling)")
     p.add_argument("--ceiling", action="store_true",
-                   help="only time the bandwidth probes (build/probe): a 1R + 1W copy moving each workload's "
-                        "algorithmic bytes, and a read of the top-k input")
+                   help="only time the bandwidth probes (bench_probes.hip): the best of the copy structures moving "
+                        "each workload's algorithmic bytes, and a read of the top-k input")
+    p.add_argument("--probes", action="store_true",
+                   help="only time every probe structure and cache-policy pair at each workload's size")
+    p.add_argument("--probe-summary", default=None,
+                   help="directory of one probe lease (sweep.json, ceiling.json, pmc_*/, occ/): writes profiles/")
+    p.add_argument("--summary-bench", default=None, help="a bench line (JSON file) whose workloads --probe-summary "
+                                                         "sets beside the probes")
+    p.add_argument("--build-probes", action="store_true",
+                   help="compile bench_probes.hip into _build/libbench_probes.so (on a host with hipcc)")
     p.add_argument("--profile-summary", default=None,
                    help="directory of one profiling lease (bench.json, stats/, traffic/, occ/): writes profiles/")
     p.add_argument("--traffic-from", default=None,
@@ -372,56 +383,132 @@ def copy_calibration(steps):
     print(json.dumps({"calibration_bytes": COPY_BYTES, "launches": steps}))
 
 
-class ProbeCase:
-    """A bandwidth probe bound to R device copies, timed as the workloads are: a copy (probe_copy) of `bytes` / 2
-    bytes read and as many written, or a read (probe_read) of `bytes` bytes."""
+PROBES_SRC = os.path.join(ROOT, "bench_probes.hip")
+PROBES_LIB = os.path.join(ROOT, "_build", "libbench_probes.so")
+PROBE_FAMILIES = {"stride": 0, "xcd": 1, "oneshot": 2, "slab": 3, "lds": 4, "row": 5, "read": 6, "write": 7}
+POLICIES = {"none": 0, "nt": 2, "sc0sc1": 17, "ntsc1": 18, "ntsc0sc1": 19}
+# The probes --ceiling takes the best of at each size: one of each structure, with the row kernels' cache policy.
+CEILING_PROBES = ("stride_u4_b8_nt_nt", "stride_u16_b8_nt_nt", "xcd_u4_b8_nt_nt", "oneshot_u8_b8_nt_nt",
+                  "slab_u4_b8_nt_nt", "lds_u4_b8_nt_nt", "row_u4_b8_nt_nt")
 
-    def __init__(self, pkg, label, nbytes, kind, dev):
-        import ctypes
+
+def build_probes():
+    """Compiles bench_probes.hip for gfx950 with the op libraries' hipcc flags into _build/libbench_probes.so."""
+    import subprocess
+    from __graft_entry__ import load_package
+    load_package()
+    from ck5090_amd import make_libs
+    os.makedirs(os.path.dirname(PROBES_LIB), exist_ok=True)
+    tmp = PROBES_LIB + ".tmp"
+    proc = subprocess.run([make_libs.hipcc(), *make_libs.HIPCC_FLAGS, PROBES_SRC, "-o", tmp], capture_output=True,
+                          text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for bench_probes.hip ({proc.returncode}):\n" + proc.stderr[-6000:])
+    os.replace(tmp, PROBES_LIB)
+    return PROBES_LIB
+
+
+def probe_lib():
+    import ctypes
+    if not os.path.exists(PROBES_LIB):
+        raise RuntimeError(f"no probe library at {PROBES_LIB}: build it first (python bench.py --build-probes)")
+    lib = ctypes.CDLL(PROBES_LIB)
+    lib.probe_run.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p] * 3 + [ctypes.c_longlong, ctypes.c_void_p]
+    lib.probe_run.restype = ctypes.c_int
+    return lib
+
+
+def parse_probe(spec):
+    """'family_u<unroll>_b<blocks per CU>_<load policy>_<store policy>' -> the arguments of probe_run."""
+    fam, u, b, lp, sp = spec.split("_")
+    return PROBE_FAMILIES[fam], int(u[1:]), int(b[1:]), POLICIES[lp], POLICIES[sp]
+
+
+class ProbeCase:
+    """A bandwidth probe (bench_probes.hip) bound to R device copies, timed as the workloads are. `nbytes` is the total
+    HBM traffic of one launch: a copy reads nbytes / 2 and writes as many, a read or a write moves nbytes."""
+
+    def __init__(self, lib, spec, nbytes, dev):
         import torch
-        lib = ctypes.CDLL(pkg.lib_path("probe"))
-        lib.probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
-        lib.probe_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_void_p]
-        self.label, self.k = label, None
-        moved = (nbytes // 2 if kind == "copy" else nbytes) // 16 * 16
+        family, unroll, bpc, lp, sp = parse_probe(spec)
+        copy = family not in (PROBE_FAMILIES["read"], PROBE_FAMILIES["write"])
+        self.label, self.k = spec, None
+        moved = (nbytes // 2 if copy else nbytes) // 16 * 16
         stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
         sink = torch.zeros(1, dtype=torch.int32, device=dev)
 
+        self.buffers = []  # the copies' tensors, held for as long as their pointers are launched on
+
         def make():
-            x = torch.ones(moved // 4, dtype=torch.float32, device=dev)
-            if kind == "copy":
-                y = torch.empty_like(x)
-                return lambda: lib.probe_copy(x.data_ptr(), y.data_ptr(), moved, stream())
-            return lambda: lib.probe_read(x.data_ptr(), moved, sink.data_ptr(), stream())
-        footprint = 2 * moved if kind == "copy" else moved
+            reads, writes = family != PROBE_FAMILIES["write"], family != PROBE_FAMILIES["read"]
+            x = torch.ones(moved // 4, dtype=torch.float32, device=dev) if reads else None
+            y = torch.empty(moved // 4, dtype=torch.float32, device=dev) if writes else None
+            self.buffers.append((x, y, sink))
+            xp, yp = x.data_ptr() if reads else None, y.data_ptr() if writes else None
+            return lambda: lib.probe_run(family, unroll, bpc, lp, sp, xp, yp, sink.data_ptr(), moved, stream())
+        footprint = 2 * moved if copy else moved
         self.copies = max(4, -(-ROTATE_BYTES // footprint))
         self.launchers = [make() for _ in range(self.copies)]
-        self.bytes = 2 * moved if kind == "copy" else moved
+        self.bytes = 2 * moved if copy else moved
 
     def launch(self, i=0):
         return self.launchers[i % self.copies]()
 
 
-def ceiling(pkg, steps, warmup):
-    """The practical HBM ceiling at each workload's size: the copy probe moving the workload's algorithmic bytes (half
-    read, half written: the 1R + 1W pattern of the row kernels) and the read probe over the top-k input. One JSON line
-    {label: {us_mean, bytes, gbs, pct_peak}}."""
+def time_probes(specs, sizes, steps, warmup):
+    """{(spec, size label): timing} for every probe at every (label, total bytes) size."""
     import torch
     dev = torch.device("cuda:0")
-    w = pkg.workloads
-    plan = [(f"copy_like_{n}", w.algorithmic_bytes(n), "copy")
-            for n in ("softmax_4096x4096", "rmsnorm_16384x4096", "rope_4x4096_32q_8kv_128", "rmsnorm_add_16384x4096",
-                      "rope_kv_4x4096_32q_8kv_128")]
-    plan.append(("read_like_topk_128x128256", 128 * 128256 * 4, "read"))
+    lib = probe_lib()
     out = {}
-    for label, nbytes, kind in plan:
-        case = ProbeCase(pkg, label, nbytes, kind, dev)
-        res = time_rotating(case, steps, warmup)
-        print(f"[ceiling] {label}: {res['us_mean']:.2f} us/call  {res['gbs']:.0f} GB/s  "
-              f"{res['pct_peak']:.1f}% of peak", file=sys.stderr, flush=True)
-        out[label] = {key: round(res[key], 3) for key in ("us_mean", "bytes", "gbs", "pct_peak")}
-        del case
-        torch.cuda.empty_cache()
+    for label, nbytes in sizes:
+        for spec in specs:
+            case = ProbeCase(lib, spec, nbytes, dev)
+            res = time_rotating(case, steps, warmup)
+            print(f"[probe] {label} {spec}: {res['us_mean']:.2f} us/call  {res['gbs']:.0f} GB/s  "
+                  f"{res['pct_peak']:.1f}% of peak", file=sys.stderr, flush=True)
+            out[(spec, label)] = {key: round(res[key], 3) for key in ("us_mean", "bytes", "gbs", "pct_peak")}
+            del case
+            torch.cuda.empty_cache()
+    return out
+
+
+def ceiling_sizes(pkg):
+    w = pkg.workloads
+    return [(n, w.algorithmic_bytes(n)) for n in ("softmax_4096x4096", "rmsnorm_16384x4096", "rope_4x4096_32q_8kv_128",
+                                                  "rmsnorm_add_16384x4096", "rope_kv_4x4096_32q_8kv_128")]
+
+
+def ceiling(pkg, steps, warmup):
+    """The practical HBM ceiling at each workload's size: the best of the copy probes (one of each structure) moving
+    the workload's algorithmic bytes, half read and half written (the 1R + 1W pattern of the row kernels), and the read
+    probe over the top-k input. One JSON line {workload: {best, us_mean, gbs, pct_peak, probes: {spec: us_mean}}}."""
+    res = time_probes(CEILING_PROBES, ceiling_sizes(pkg), steps, warmup)
+    res.update(time_probes(("read_u8_b8_nt_nt",), [("topk_128x128256", 128 * 128256 * 4)], steps, warmup))
+    out = {}
+    for (spec, label), r in res.items():
+        e = out.setdefault(label, {"probes": {}})
+        e["probes"][spec] = r["us_mean"]
+        if "us_mean" not in e or r["us_mean"] < e["us_mean"]:
+            e.update({"best": spec, **{k: r[k] for k in ("us_mean", "bytes", "gbs", "pct_peak")}})
+    print(json.dumps(out))
+
+
+def probe_sweep(pkg, steps, warmup):
+    """Every probe structure and every cache-policy pair of the stride probe at each workload's size, plus the read and
+    the write probes at the same sizes. One JSON line {size: {spec: us_mean}}."""
+    specs = [f"stride_u{u}_b{b}_nt_nt" for u in (2, 4, 8, 16) for b in (4, 8, 16)]
+    specs += [f"stride_u4_b8_{lp}_{sp}" for lp in POLICIES for sp in POLICIES if (lp, sp) != ("nt", "nt")]
+    specs += [f"{f}_u{u}_b8_nt_nt" for f, us in (("xcd", (4, 8)), ("oneshot", (4, 8, 16)), ("slab", (4, 8)),
+                                                  ("lds", (2, 4, 8)), ("row", (4, 8))) for u in us]
+    sizes = ceiling_sizes(pkg)
+    res = time_probes(specs, sizes, steps, warmup)
+    half = [(f"{label}_each_way", nbytes // 2) for label, nbytes in sizes]
+    res.update(time_probes(("read_u8_b8_nt_nt", "read_u4_b8_nt_nt", "write_u4_b8_nt_nt", "write_u8_b8_nt_nt"), half,
+                           steps, warmup))
+    out = {}
+    for (spec, label), r in res.items():
+        out.setdefault(label, {})[spec] = [r["us_mean"], r["pct_peak"]]
     print(json.dumps(out))
 
 
@@ -595,6 +682,91 @@ def profile_summary(run_dir):
     print("\n".join(lines + [""] + t_lines + [""] + occ_lines))
 
 
+def probe_summary(run_dir, bench_json=None):
+    """Writes profiles/probe_ceiling_and_structures.txt from one probe lease (run_dir as the probe script leaves it:
+    sweep.json of --probes, ceiling.json of --ceiling, pmc_FETCH_SIZE/ and pmc_WRITE_SIZE/ of the counter runs of
+    --ceiling --steps 5 --warmup 1, occ/ of its occupancy run), set beside the workloads of a bench line (bench_json,
+    from the same lease when it has one)."""
+    def last_json(path):
+        with open(path) as f:
+            return json.loads(f.read().strip().splitlines()[-1])
+    sweep = last_json(os.path.join(run_dir, "sweep.json"))
+    ceil = last_json(os.path.join(run_dir, "ceiling.json"))
+    work = last_json(bench_json)["per_workload"] if bench_json else {}
+    sizes = [s for s in sweep if not s.endswith("_each_way")]
+    lines = ["# Bandwidth probes: what a plain copy, read or write reaches on MI355X at each workload's size", "",
+             "Commands (one MI355X; the rocprofv3 runs from /tmp, TMPDIR=/tmp):",
+             "    python3 bench.py --probes          -> every structure and cache-policy pair below",
+             "    python3 bench.py --ceiling         -> the best structure at each size (the ceiling table)",
+             "    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir>/pmc_FETCH_SIZE -o p -- python3 bench.py "
+             "--ceiling --steps 5 --warmup 1   (and WRITE_SIZE; and SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES "
+             "SQ_INSTS_VALU SQ_INSTS_SALU SQ_INSTS_LDS GRBM_GUI_ACTIVE into <dir>/occ)",
+             "    python3 bench.py --probe-summary <dir> [--summary-bench <bench line>]   -> this file", "",
+             "Probes (bench_probes.hip): stride = persistent grid-stride copy, u = 16-byte vectors per lane in flight, "
+             "b = workgroups",
+             "of 256 threads per CU; xcd = stride with each XCD walking one contiguous eighth; oneshot = one workgroup "
+             "per tile, no loop;",
+             "slab = one contiguous slab per workgroup, register double-buffered; lds = loads straight to LDS "
+             "(global_load_lds_dwordx4);",
+             "row = the row kernels' structure (a row per workgroup, next row loaded during a barrier exchange); "
+             "read / write = one",
+             "direction only. Cache policies (load_store): none, nt, sc0sc1, ntsc1, ntsc0sc1. Sizes are the workloads' "
+             "algorithmic bytes,",
+             "half read and half written; each probe timed as the workloads are (20 warm-up + 100 launches over "
+             "rotating copies, >= 1.25 GiB).", "",
+             "## us per launch (% of 8 TB/s)", "",
+             "| probe | " + " | ".join(sizes) + " |", "|---|" + "---|" * len(sizes)]
+    for spec in sweep[sizes[0]]:
+        lines.append(f"| {spec} | " + " | ".join(f"{sweep[s][spec][0]:.2f} ({sweep[s][spec][1]:.1f})"
+                                                   for s in sizes) + " |")
+    each = [s for s in sweep if s.endswith("_each_way")]
+    lines += ["", "## One direction only, at half of each size (the bytes one direction of the copy moves)", "",
+              "| probe | " + " | ".join(each) + " |", "|---|" + "---|" * len(each)]
+    for spec in sweep[each[0]]:
+        lines.append(f"| {spec} | " + " | ".join(f"{sweep[s][spec][0]:.2f} ({sweep[s][spec][1]:.1f})"
+                                                   for s in each) + " |")
+    lines += ["", "## Ceiling (bench.py --ceiling: the best of one probe per structure, nt loads and stores) and the "
+              "workloads", "",
+              "| size | best probe | us | % of 8 TB/s | best of the sweep (any policy) | workload us | workload % of "
+              "8 TB/s | workload / best probe |", "|---|---|---|---|---|---|---|---|"]
+    for label, e in ceil.items():
+        best_any = min(sweep.get(label, {}).items(), key=lambda kv: kv[1][0], default=(None, [float("nan")]))
+        wl = work.get(label) or work.get(f"{label}_k1")
+        wl_us = wl["us_mean"] if wl else None
+        lines.append(f"| {label} | {e['best']} | {e['us_mean']:.2f} | {e['pct_peak']:.1f} | "
+                     f"{best_any[0]} {best_any[1][0]:.2f} | " +
+                     (f"{wl_us:.2f} | {wl['pct_peak']:.1f} | {100 * min(e['us_mean'], best_any[1][0]) / wl_us:.1f}%"
+                      if wl else "- | - | -") + " |")
+    # counters: every probe ran the same sizes the same number of times, so the means per dispatch compare directly
+    fetch = counter_means(os.path.join(run_dir, "pmc_FETCH_SIZE"), "FETCH_SIZE")
+    write = counter_means(os.path.join(run_dir, "pmc_WRITE_SIZE"), "WRITE_SIZE")
+    occ = occupancy(os.path.join(run_dir, "occ"))
+    with open(TRAFFIC_PATH) as f:
+        tr = json.load(f)
+    sizes_b = [e["bytes"] for lab, e in ceil.items() if lab != "topk_128x128256"]
+    copy_half = sum(sizes_b) / len(sizes_b) / 2 / 1024
+    lines += ["", "## Counters of the ceiling probes (means per dispatch over the five copy sizes; the read probe over "
+              "the top-k input)", "",
+              f"FETCH_SIZE scaled by {tr['fetch_scale']} and WRITE_SIZE by {tr['write_scale']} (profiles/traffic.json"
+              f" calibration); the copy probes' mean algorithmic bytes each way: {copy_half:.0f} KiB.", "",
+              "| kernel | FETCH KiB (scaled) | WRITE KiB | read / algorithmic | resident waves per CU | occupancy % | "
+              "VALU per wave | SALU per wave |", "|---|---|---|---|---|---|---|---|"]
+    for kernel, f_kib in fetch.items():
+        if "probe" in kernel or not any(t in kernel for t in ("copy_", "read_", "write_")):
+            continue
+        sk = short_kernel(kernel)
+        f_scaled = f_kib * tr["fetch_scale"]
+        algo = copy_half if sk.startswith("copy_") else 128 * 128256 * 4 / 1024
+        o = occ.get(kernel, {})
+        lines.append(f"| {sk} | {f_scaled:.0f} | {write.get(kernel, 0):.0f} | {f_scaled / algo:.3f} | "
+                     f"{o.get('resident_waves_per_cu', '-')} | {o.get('occupancy_pct', '-')} | "
+                     f"{o.get('valu_per_wave', '-')} | {o.get('salu_per_wave', '-')} |")
+    path = os.path.join(ROOT, "profiles", "probe_ceiling_and_structures.txt")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main():
     args = parse()
     if args.traffic_from:
@@ -602,6 +774,12 @@ def main():
         return
     if args.profile_summary:
         profile_summary(args.profile_summary)
+        return
+    if args.build_probes:
+        print(build_probes())
+        return
+    if args.probe_summary:
+        probe_summary(args.probe_summary, args.summary_bench)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -615,6 +793,9 @@ def main():
     pkg = load_package()
     if args.ceiling:
         ceiling(pkg, args.steps, args.warmup)
+        return
+    if args.probes:
+        probe_sweep(pkg, args.steps, args.warmup)
         return
     dev = torch.device("cuda:0")
     flush_buf = None if args.no_cold else torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)

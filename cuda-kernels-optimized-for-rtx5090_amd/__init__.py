@@ -16,7 +16,6 @@ from . import workloads  # noqa: F401  (named workloads: shapes, seeds, byte cou
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 OPS = ("softmax", "rmsnorm", "rope", "topk")
-PROBES = ("probe",)  # the bandwidth probes of the measurement (bench.py --ceiling), not an op
 TORCH = ("torch",)   # the torch operators over the op libraries
 
 
@@ -25,8 +24,8 @@ def lib_path(op):
     return os.path.join(PKG_DIR, "build", op, "libkernel.so")
 
 
-def build(ops=OPS + PROBES + TORCH):
-    """Compiles the libraries of the given ops (and the probes and the torch operators); returns {op: path}."""
+def build(ops=OPS + TORCH):
+    """Compiles the libraries of the given ops (and the torch operators); returns {op: path}."""
     from . import make_libs
     return make_libs.build(ops)
 

@@ -15,7 +15,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
-LIBS = ("softmax", "rmsnorm", "rope", "topk", "probe")  # the four ops and the bandwidth probes of bench.py --ceiling
+LIBS = ("softmax", "rmsnorm", "rope", "topk")
 TORCH = "torch"  # the torch operators over the op libraries
 ARCH = os.environ.get("ROWKERN_ARCH", "gfx950")
 

@@ -40,18 +40,28 @@ def test_library_exports_the_header(pkg, op):
     assert c_symbols == set(names), f"{op}: exported {sorted(c_symbols)} vs declared {sorted(names)}"
 
 
-def test_probe_library_exports_and_codes_without_gpu(pkg):
-    # the measurement's bandwidth probes (bench.py --ceiling): a library of their own, outside the op boundary
-    path = pkg.lib_path("probe")
+def test_probe_library_exports_and_codes_without_gpu():
+    # the measurement's bandwidth probes (bench_probes.hip, bench.py --ceiling / --probes): a library of their own,
+    # outside the package and the op boundary; argument checks answer before any launch
+    import bench
+    path = bench.PROBES_LIB
     assert os.path.exists(path), f"{path} not built"
     c_symbols = {s for s in exported(path) if not s.startswith("_Z") and not s.startswith("_")}
-    assert c_symbols == {"probe_copy", "probe_read"}
-    lib = ctypes.CDLL(path)
-    lib.probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
-    lib.probe_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_void_p]
-    assert lib.probe_copy(None, None, 0, None) == 0
-    assert lib.probe_copy(16, 16, 24, None) == -1  # not whole 16-byte vectors
-    assert lib.probe_read(16, 32, None, None) == -1  # no sink
+    assert c_symbols == {"probe_run"}
+    lib = bench.probe_lib()
+    stride, read, write = (bench.PROBE_FAMILIES[f] for f in ("stride", "read", "write"))
+    assert lib.probe_run(stride, 4, 8, 2, 2, None, None, None, 0, None) == 0  # nothing to move
+    assert lib.probe_run(stride, 4, 8, 2, 2, 16, 16, None, 24, None) == -1  # not whole 16-byte vectors
+    assert lib.probe_run(stride, 4, 8, 2, 2, 16, 16, None, (1 << 30) + 16, None) == -1  # beyond 1 GiB
+    assert lib.probe_run(stride, 3, 8, 2, 2, 16, 16, None, 32, None) == -1  # no such unroll
+    assert lib.probe_run(stride, 4, 8, 1, 2, 16, 16, None, 32, None) == -1  # no such policy pair
+    assert lib.probe_run(stride, 4, 0, 2, 2, 16, 16, None, 32, None) == -1  # blocks per CU out of range
+    assert lib.probe_run(bench.PROBE_FAMILIES["row"], 4, 8, 0, 2, 16, 16, None, 32, None) == -1  # nt only
+    assert lib.probe_run(read, 8, 8, 2, 2, 16, None, None, 32, None) == -1  # no sink
+    assert lib.probe_run(write, 4, 8, 2, 2, None, None, None, 32, None) == -1  # nothing to write to
+    assert lib.probe_run(99, 4, 8, 2, 2, 16, 16, 16, 32, None) == -1
+    for spec in bench.CEILING_PROBES:
+        bench.parse_probe(spec)
 
 
 def test_softmax_codes_without_gpu(pkg):
