@@ -60,6 +60,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default=None, help="measure only this workload (default: all)")
     p.add_argument("--k", type=int, default=None, help="top-k: measure only this k (default: 1, 50 and 1024)")
+    p.add_argument("--tune", action="append", default=[],
+                   help="op:slot=value, set before measuring through the op library's tuning hook (e.g. topk:1=1 "
+                        "for the last-arrival merge of k > 64); may be repeated")
     p.add_argument("--no-cold", action="store_true", help="skip the flushed single-launch timing")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=20.0,
@@ -791,6 +794,13 @@ def main():
     import torch
     from __graft_entry__ import load_package
     pkg = load_package()
+    for spec in args.tune:  # op:slot=value, through the op library's tuning hook (sweeps and A/B runs)
+        op, _, rest = spec.partition(":")
+        slot, _, value = rest.partition("=")
+        rc = getattr(pkg.candidate(op)._lib, f"{op}_tune")(int(slot), int(value))
+        if rc != 0:
+            raise SystemExit(f"--tune {spec}: the {op} library refused slot {slot}")
+        print(f"[tune] {op} slot {slot} = {value}", file=sys.stderr, flush=True)
     if args.ceiling:
         ceiling(pkg, args.steps, args.warmup)
         return

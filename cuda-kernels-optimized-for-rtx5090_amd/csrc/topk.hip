@@ -264,6 +264,16 @@ __device__ void prune(S& s, int k) {
   __syncthreads();
 }
 
+// Whether the buffer holds more than `limit` composites, uniform over the workgroup: every wave reads the count before
+// any wave goes on (to append, in the loops that call this), so that no wave reads a count another wave has already
+// raised and the waves cannot disagree on a prune (whose barriers they would then pair with different barriers).
+template <typename S>
+__device__ __forceinline__ bool prune_due(S& s, int limit) {
+  const bool due = s.count > limit;
+  __syncthreads();
+  return due;
+}
+
 template <typename T> struct Fmt;
 template <> struct Fmt<float> { static constexpr int W = 4; };      // elements per 16-byte vector
 template <> struct Fmt<uint16_t> { static constexpr int W = 8; };
@@ -1551,7 +1561,7 @@ __global__ void __launch_bounds__(kThreads)
       __syncthreads();
       const u64 bound = thr > TL::kSentinelKey ? (u64)thr << 32 : 0ull;
       for (int v = 0; v < TL::NV; ++v) {
-        if (s.count > kWideCap - kStep) prune(s, k);
+        if (prune_due(s, kWideCap - kStep)) prune(s, k);
         const u64 floor = s.thr > bound ? s.thr : bound;
         tile.append_first(s, v, floor);
         __syncthreads();
@@ -1617,7 +1627,7 @@ __global__ void __launch_bounds__(kThreads)
     }
   };
   auto take = [&](const u64 (&v)[PER]) {  // appends the entries at or above the floor (room for a list is kept)
-    if (s.count > kWideCap - kWideList) prune(s, k);
+    if (prune_due(s, kWideCap - kWideList)) prune(s, k);
     const u64 f = s.thr;
     bool keep[PER];
     bool any = false;

@@ -5,6 +5,8 @@
 //    the wave's live lanes, and __syncthreads a barrier of the block's live threads; lanes that have returned take no
 //    part, as on the hardware. Lanes of one wave reaching a barrier from different source lines, or a schedule in
 //    which no fiber can run, abort with a report;
+//  - within a workgroup, every lane runs to its next exchange point in turn, or, with EMU_WAVE_AHEAD set, each wave
+//    runs on until all of its lanes wait at a block barrier (waves ahead of one another between barriers);
 //  - workgroups run one after another (shuffled on request), or, with EMU_CONCURRENT set, each on an OS thread of its
 //    own, all at once (as co-resident workgroups that wait for one another need); __shared__ is a function-local
 //    thread_local static, so each workgroup's thread has its own;
@@ -367,26 +369,45 @@ inline void run_block() {
   std::vector<int> order(s.n);
   for (int i = 0; i < s.n; ++i) order[i] = i;
   int remaining = s.n;
+  // EMU_WAVE_AHEAD: a wave runs on (through its own cross-lane exchanges) until every one of its lanes waits at a
+  // block barrier or has ended, before the next wave starts: waves run ahead of one another between block barriers,
+  // as they may on the hardware, so a value one wave writes to __shared__ without a barrier is seen by the waves
+  // after it. Without it, every lane runs to its next exchange point in turn, and all waves read before any writes.
+  static const bool ahead = std::getenv("EMU_WAVE_AHEAD") != nullptr;
+  auto run_one = [&](Fiber& f) {
+    if (f.done) return false;
+    if (f.wait && f.wait->gen == f.wait_gen) return false;
+    f.wait = nullptr;
+    s.cur = &f;
+    if (!_setjmp(s.sched)) {
+      if (!f.started) {
+        f.started = true;
+        swapcontext(&s.sched_uc, &f.uc);
+      } else {
+        _longjmp(f.jb, 1);
+      }
+    }
+    if (f.done) --remaining;
+    return true;
+  };
+  const int waves = (s.n + kW - 1) / kW;
+  std::vector<int> worder(waves);
+  for (int w = 0; w < waves; ++w) worder[w] = w;
   while (remaining) {
     bool progress = false;
     if (s.shuffle_seed >= 0) std::shuffle(order.begin(), order.end(), s.rng);
-    for (int oi = 0; oi < s.n; ++oi) {
-      Fiber& f = s.fib[order[oi]];
-      if (f.done) continue;
-      if (f.wait && f.wait->gen == f.wait_gen) continue;
-      f.wait = nullptr;
-      s.cur = &f;
-      if (!_setjmp(s.sched)) {
-        if (!f.started) {
-          f.started = true;
-          swapcontext(&s.sched_uc, &f.uc);
-        } else {
-          _longjmp(f.jb, 1);
+    if (ahead) {
+      if (s.shuffle_seed >= 0) std::shuffle(worder.begin(), worder.end(), s.rng);
+      for (int w : worder) {
+        for (bool again = true; again;) {
+          again = false;
+          for (int oi = 0; oi < s.n; ++oi)
+            if (order[oi] / kW == w && run_one(s.fib[order[oi]])) again = progress = true;
         }
       }
-      progress = true;
-      if (f.done) --remaining;
     }
+    for (int oi = 0; oi < s.n && !ahead; ++oi)
+      if (run_one(s.fib[order[oi]])) progress = true;
     if (!progress) {
       std::fprintf(stderr, "EMU DEADLOCK in block (%u,%u): %d lanes left\n", s.block_idx.x, s.block_idx.y, remaining);
       for (int w = 0; w < (s.n + kW - 1) / kW; ++w)

@@ -10,7 +10,8 @@ sizes down to 24 and its fused KV-cache write with skipped (-1) slots. The softm
 workgroups wait for one another, runs with every workgroup on an OS thread of its own, over repeated launches (the
 pair table is reused under fresh tags), with one row per workgroup and with row groups walking several rows; also
 under the weak mode (its pairs become visible late and out of order) with the wait's clock stopped, so that every wait
-must end by its pairs, never by its time budget.
+must end by its pairs, never by its time budget. Some cases also run with each wave running ahead to the next block
+barrier before the next wave starts.
 """
 
 import os
@@ -139,3 +140,15 @@ def test_emulated_rmsnorm_matches_oracle(emu_rmsnorm, case):
 @pytest.mark.parametrize("case", ROPE, ids=[c[0] for c in ROPE])
 def test_emulated_rope_matches_oracle(emu_rope, case):
     run(emu_rope, case[1:])
+
+
+# Waves running ahead of one another between block barriers (EMU_WAVE_AHEAD: each wave runs on until it waits at a
+# block barrier before the next wave starts): the cross-wave reductions' LDS slots must not be rewritten before every
+# wave has read them.
+@pytest.mark.parametrize("op, case", [("softmax", c) for c in SOFTMAX[:6] + SOFTMAX[7:9]] +
+                         [("rmsnorm", c) for c in RMSNORM[7:10]] + [("rope", c) for c in ROPE[:1] + ROPE[5:6]],
+                         ids=lambda v: v if isinstance(v, str) else v[0])
+def test_emulated_rows_waves_ahead(emu_softmax, emu_rmsnorm, emu_rope, op, case):
+    exe = {"softmax": emu_softmax, "rmsnorm": emu_rmsnorm, "rope": emu_rope}[op]
+    run(exe, case[1:], env=dict(os.environ, EMU_WAVE_AHEAD="1"))
+

@@ -8,7 +8,9 @@ single- and split-chunk rows, every k class (1, the lane-maxima bound up to 64, 
 tiles, ties, monotone and all-negative rows, the all-ones NaN, repeated launches on the same buffers (the arrival
 counters' self-reset), and shuffled workgroup and lane schedules. The concurrent cases run every workgroup of a launch
 on an OS thread of its own, so chunks publish and count their arrivals while the row's other chunks and merger run.
-The weak cases make agent-scope stores visible to other workgroups late and out of order, as the memory system may:
+The waves-ahead cases let each wave run on to the next block barrier before the next wave starts, so that a
+__shared__ value one wave changes without a barrier reaches the waves after it. The weak cases make agent-scope stores visible to other workgroups late and
+out of order, as the memory system may:
 a store drains when its lane waits with `s_waitcnt vmcnt(0)`, at random before that, and, when its lane has ended
 without waiting, one store at a time now and then, or when the launch completes. The hand-off (result stores, the wait,
 then the arrival count) must stay exact under it, and the same cases with the wait taken out (a planted mistake, on the
@@ -100,6 +102,21 @@ def test_weak_mode_exposes_a_missing_wait(emu_topk, concurrent):
     # arrival can read stale slots (k = 1), lists (k <= 64) or lists and bound headers (k > 64)
     env = dict(os.environ, EMU_DROP_VMCNT="1")
     run(emu_topk, WEAK[1][1:], env=env, weak=True, concurrent=concurrent, expect_ok=False)
+
+
+# Waves running ahead of one another between block barriers (EMU_WAVE_AHEAD): a wave runs through its own exchanges
+# until it waits at a block barrier before the next wave starts, so a count one wave raises in __shared__ is what the
+# waves after it read. Every prune decision must still be the same in every wave (a wave that prunes alone pairs its
+# barriers with the others' other barriers): rows with ties, monotone and all-ones NaN rows take the prune-heavy paths
+# (the k > 64 tile's re-append loop, the merge's pruning gather).
+AHEAD = ["ties", "ascending", "descending", "negative", "all_ones_nan", "all_ones_nan_bf16", "shuffled_bf16",
+         "split_fp32"]
+
+
+@pytest.mark.parametrize("name", AHEAD)
+def test_emulated_topk_waves_ahead(emu_topk, name):
+    case = next(c for c in CASES if c[0] == name)
+    run(emu_topk, case[1:], env=dict(os.environ, EMU_WAVE_AHEAD="1"))
 
 
 def test_emulated_two_library_copies(tmp_path):
