@@ -605,6 +605,39 @@ def occupancy(run_dir, cus=256, xcds=8):
     return res
 
 
+WAVE_PASSES = (("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_ANY",
+                "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_SCA", "GRBM_GUI_ACTIVE"),
+               ("SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_MISC", "SQ_WAIT_INST_LDS",
+                "SQ_LDS_BANK_CONFLICT", "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR", "SQ_INSTS_LDS"))
+
+
+def wave_breakdown(run_dir):
+    """Where each kernel's wave time goes, from the two counter passes of WAVE_PASSES (run_dir/a, run_dir/b): per
+    dispatch, the share of wave-cycles (SQ_WAVE_CYCLES, like the others in units of four cycles) spent waiting for
+    anything, waiting for an instruction's dependency, and issuing VALU, scalar, LDS and memory instructions; LDS bank
+    conflict cycles and memory instructions per wave."""
+    out = {}
+    for sub, names in zip(("a", "b"), WAVE_PASSES):
+        for name in names:
+            for kernel, v in counter_means(os.path.join(run_dir, sub), name).items():
+                out.setdefault(kernel, {})[name] = v
+    res = {}
+    for kernel, c in out.items():
+        if c.get("SQ_WAVES", 0) <= 64 or not c.get("SQ_WAVE_CYCLES"):
+            continue
+        wc = c["SQ_WAVE_CYCLES"]
+        pct = lambda n: round(100 * c.get(n, 0) / wc, 1)  # noqa: E731
+        res[kernel] = {"waves": int(c["SQ_WAVES"]), "wait_any_pct": pct("SQ_WAIT_ANY"),
+                       "wait_inst_pct": pct("SQ_WAIT_INST_ANY"), "active_any_pct": pct("SQ_ACTIVE_INST_ANY"),
+                       "valu_pct": pct("SQ_ACTIVE_INST_VALU"), "scalar_pct": pct("SQ_ACTIVE_INST_SCA"),
+                       "lds_pct": pct("SQ_ACTIVE_INST_LDS"), "vmem_pct": pct("SQ_ACTIVE_INST_VMEM"),
+                       "wait_lds_pct": pct("SQ_WAIT_INST_LDS"),
+                       "lds_conflict_per_wave": round(c.get("SQ_LDS_BANK_CONFLICT", 0) / c["SQ_WAVES"], 1),
+                       "vmem_rd_per_wave": round(c.get("SQ_INSTS_VMEM_RD", 0) / c["SQ_WAVES"], 1),
+                       "vmem_wr_per_wave": round(c.get("SQ_INSTS_VMEM_WR", 0) / c["SQ_WAVES"], 1)}
+    return res
+
+
 def profile_summary(run_dir):
     """Writes profiles/ from one profiling lease (run_dir as the profiling script leaves it: bench.json and
     bench.err of the bench line, stats/ of the kernel trace, traffic/ of the FETCH_SIZE / WRITE_SIZE runs, occ/ of the
@@ -682,14 +715,39 @@ def profile_summary(run_dir):
                              f"{r['lds_per_wave']:>6}")
     with open(os.path.join(prof, "occupancy_bench_workloads.txt"), "w") as f:
         f.write("\n".join(occ_lines) + "\n")
-    print("\n".join(lines + [""] + t_lines + [""] + occ_lines))
+    w_lines = []
+    wdir = os.path.join(run_dir, "waves")
+    if os.path.isdir(wdir):
+        w_lines = ["# Where the wave time goes on MI355X (rocprofv3 SQ counters, per dispatch, mean over the dispatches of each "
+                   "kernel)", "",
+                   "Commands (from /tmp, TMPDIR=/tmp, two runs per workload W, one per counter set):",
+                   "    rocprofv3 --pmc " + " ".join(WAVE_PASSES[0]) + " --output-format csv -d <dir>/waves/W/a -o p -- "
+                   "python3 bench.py --workload W --steps 5 --warmup 1 --no-cold --no-cpu",
+                   "    rocprofv3 --pmc " + " ".join(WAVE_PASSES[1]) + " --output-format csv -d <dir>/waves/W/b -o p -- "
+                   "python3 bench.py --workload W --steps 5 --warmup 1 --no-cold --no-cpu",
+                   "Shares of SQ_WAVE_CYCLES (the time waves are resident): waiting for anything (memory, barriers, "
+                   "dependencies), waiting for an",
+                   "instruction's dependency, and issuing VALU, scalar, LDS and memory instructions (issue shares overlap "
+                   "the waits of other waves", "of the same SIMD); LDS bank-conflict cycles and memory instructions per "
+                   "wave.", "",
+                   f"{'workload':<24} {'kernel':<46} {'wait%':>6} {'dep%':>5} {'issue%':>7} {'VALU%':>6} {'SCA%':>5} "
+                   f"{'LDS%':>5} {'VMEM%':>6} {'LDSwait%':>8} {'conf/w':>7} {'rd/w':>6} {'wr/w':>6}"]
+        for w in sorted(os.listdir(wdir)):
+            for kernel, r in wave_breakdown(os.path.join(wdir, w)).items():
+                w_lines.append(f"{w:<24} {short_kernel(kernel)[:46]:<46} {r['wait_any_pct']:>6} {r['wait_inst_pct']:>5} "
+                               f"{r['active_any_pct']:>7} {r['valu_pct']:>6} {r['scalar_pct']:>5} {r['lds_pct']:>5} "
+                               f"{r['vmem_pct']:>6} {r['wait_lds_pct']:>8} {r['lds_conflict_per_wave']:>7} "
+                               f"{r['vmem_rd_per_wave']:>6} {r['vmem_wr_per_wave']:>6}")
+        with open(os.path.join(prof, "wave_cycles_bench_workloads.txt"), "w") as f:
+            f.write("\n".join(w_lines) + "\n")
+    print("\n".join(lines + [""] + t_lines + [""] + occ_lines + [""] + w_lines))
 
 
 def probe_summary(run_dir, bench_json=None):
     """Writes profiles/probe_ceiling_and_structures.txt from one probe lease (run_dir as the probe script leaves it:
     sweep.json of --probes, ceiling.json of --ceiling, pmc_FETCH_SIZE/ and pmc_WRITE_SIZE/ of the counter runs of
-    --ceiling --steps 5 --warmup 1, occ/ of its occupancy run), set beside the workloads of a bench line (bench_json,
-    from the same lease when it has one)."""
+    --ceiling --steps 5 --warmup 1, occ_probes/ (or occ/) of its occupancy run), set beside the workloads of a bench
+    line (bench_json, from the same lease when it has one)."""
     def last_json(path):
         with open(path) as f:
             return json.loads(f.read().strip().splitlines()[-1])
@@ -743,7 +801,8 @@ def probe_summary(run_dir, bench_json=None):
     # counters: every probe ran the same sizes the same number of times, so the means per dispatch compare directly
     fetch = counter_means(os.path.join(run_dir, "pmc_FETCH_SIZE"), "FETCH_SIZE")
     write = counter_means(os.path.join(run_dir, "pmc_WRITE_SIZE"), "WRITE_SIZE")
-    occ = occupancy(os.path.join(run_dir, "occ"))
+    occ_dir = os.path.join(run_dir, "occ_probes")
+    occ = occupancy(occ_dir if os.path.isdir(occ_dir) else os.path.join(run_dir, "occ"))
     with open(TRAFFIC_PATH) as f:
         tr = json.load(f)
     sizes_b = [e["bytes"] for lab, e in ceil.items() if lab != "topk_128x128256"]
