@@ -8,8 +8,8 @@
 //
 // k <= 64: topk_tile, one kernel (see its comment); the row's last workgroup merges the chunk lists, handed over
 // through device-coherent stores and loads and a per-row arrival counter, as the reference's last-block merge. k = 1
-// is an instance of its own: each lane's largest composite straight from the registers, the chunks' best folded by a
-// device-scope maximum beside the arrival counter.
+// is a kernel of its own, topk_one: each lane's largest composite straight from the registers, 1024-thread workgroups
+// over four chunks each, and the same hand-off of one composite per workgroup.
 //
 // 64 < k <= 1024: topk_wide, one kernel of the same shape (see its comment): a bound from group maxima admits about
 // 1.4k elements per tile, the row's last workgroup merges the chunks' candidate lists from a floor made of their
@@ -641,9 +641,9 @@ constexpr int kWideGroups = 8;  // groups per lane for the admission bound of th
 // What a vector load past a tile's end reads instead (all ones: the sentinel below).
 __device__ u32x4 g_sentinel_vec = {~0u, ~0u, ~0u, ~0u};
 
-// A register tile: thread t holds vectors v * 256 + t (v < NV) of elements [b0, b1) of a row, W each, as raw bits; an
-// element outside [b0, b1) holds the sentinel (all ones: the -NaN whose key is the smallest of its format), read from
-// g_sentinel_vec by a vector load past the end. load() only issues the loads.
+// A register tile: thread t of the workgroup's NT holds vectors v * NT + t (v < NV) of elements [b0, b1) of a row, W
+// each, as raw bits; an element outside [b0, b1) holds the sentinel (all ones: the -NaN whose key is the smallest of
+// its format), read from g_sentinel_vec by a vector load past the end. load() only issues the loads.
 //
 // The raw bits are ordered without forming keys: over non-negative values key order is the signed order of the bits
 // (as int32, or int16 for a bf16 half), over negative values it is the reverse. So the largest element of a set, in
@@ -651,7 +651,7 @@ __device__ u32x4 g_sentinel_vec = {~0u, ~0u, ~0u, ~0u};
 // integer, is the largest negative one: it never moves the minimum of a set holding a real element); and for a
 // threshold key K with bits t, key(u) >= K iff (int)u >= (int)t when K is a non-negative value, iff u <= t (unsigned)
 // when K is negative.
-template <typename T, bool VEC>
+template <typename T, bool VEC, int NT = kThreads>
 struct Tile {
   static constexpr int W = Fmt<T>::W;
   static constexpr int NV = kTileE / W;
@@ -660,7 +660,7 @@ struct Tile {
   int b0, b1;
   int lane0;  // b0 + threadIdx.x * W, the first element of vector 0 (kept opaque with the registers)
 
-  __device__ __forceinline__ int first(int v) const { return lane0 + v * kThreads * W; }
+  __device__ __forceinline__ int first(int v) const { return lane0 + v * NT * W; }
   __device__ __forceinline__ uint32_t bits(int v, int j) const {
     if constexpr (sizeof(T) == 4) {
       return r[v][j];
@@ -675,7 +675,7 @@ struct Tile {
 
   __device__ __forceinline__ void load(const T* row, int t0, int end) {
     b0 = t0;
-    b1 = end - t0 > kThreads * kTileE ? t0 + kThreads * kTileE : end;
+    b1 = end - t0 > NT * kTileE ? t0 + NT * kTileE : end;
     lane0 = b0 + (int)threadIdx.x * W;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
@@ -722,7 +722,7 @@ struct Tile {
         jb = eq ? j : jb;
       }
     }
-    const int off = vb * kThreads * W + jb;
+    const int off = vb * NT * W + jb;
     return ((u64)m << 32) | (u64)(~(uint32_t)(lane0 + off));
   }
 
@@ -1103,6 +1103,65 @@ __device__ __forceinline__ void sample_top(const SampleArgs& sa, float u, const 
 }
 
 
+// ---- the k = 1 kernel ----------------------------------------------------------------------------------------------
+
+constexpr int kOneThreads = 1024;                   // threads of a k = 1 workgroup
+constexpr int kOneChunks = kOneThreads / kThreads;  // consecutive chunks of the caller's chunking per k = 1 workgroup
+
+// k = 1: one 1024-thread workgroup per kOneChunks consecutive chunks of a row (the result does not depend on the
+// chunking), in register tiles of 65536 elements, all of a tile's loads in flight at once. Each lane's largest
+// composite comes straight from its registers (no bound, list or block reduction per tile), then the wave's and,
+// through LDS, the workgroup's. A row split over several workgroups hands over as topk_tile's chunks do: each stores
+// its best in the work slot of its group (work[row * nchunks + group], inside the caller's [rows, nchunks] slots),
+// waits for the store and counts its arrival on counters[row]; the row's last arrival takes the largest slot and
+// zeroes the counter.
+// A workgroup of four chunks makes a quarter of the arrivals of one per chunk (the caller's counters pack 32 rows
+// into a 128-byte line, whose device-scope adds are performed one after another) and leaves the merge a quarter of
+// the slots.
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(kOneThreads)
+    topk_one(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
+             u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
+             int groups, SampleArgs sa) {
+  __shared__ u64 best_of[kOneThreads / kWave];
+  const long long row = blockIdx.y;
+  const int group = blockIdx.x;
+  const int begin = (int)((long long)group * kOneChunks * chunk);
+  const int end = (int)(group == groups - 1 ? cols : begin + kOneChunks * chunk);  // the last group ends the row
+  const T* xr = x + row * cols;
+  using TL = Tile<T, VEC, kOneThreads>;
+  constexpr int TE = kOneThreads * kTileE;
+  u64 best = 0;
+  for (int t0 = begin; t0 < end; t0 += TE) {
+    TL tile;
+    tile.load(xr, t0, end);
+    const u64 c = tile.best_composite();
+    best = c > best ? c : best;
+  }
+  best = wave_ext64<true>(best);
+  if (lane_id() == 0) best_of[wave_id()] = best;
+  __syncthreads();
+  if (wave_id() != 0) return;
+  best = wave_ext64<true>(lane_id() < kOneThreads / kWave ? best_of[lane_id()] : 0ull);
+  if (groups > 1) {
+    u64* slots = work + row * (long long)nchunks;
+    if (lane_id() == 0) __hip_atomic_store(slots + group, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!hand_off_arrive(counters + row, groups)) return;
+    u64 m = 0;
+    for (int i = lane_id(); i < groups; i += kWave) {
+      const u64 v = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      m = v > m ? v : m;
+    }
+    best = wave_ext64<true>(m);
+    if (lane_id() == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (lane_id() != 0) return;
+  if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row] = composite_bits(best);
+  else static_cast<uint16_t*>(values)[row] = (uint16_t)(composite_bits(best) >> 16);
+  indices[row] = composite_index(best);
+  if (sa.out) sa.out[row] = composite_index(best);  // the draw from a one-entry list
+}
+
 // ---- the k <= 64 kernel --------------------------------------------------------------------------------------------
 
 // k <= 64: one 256-thread workgroup per (chunk, row). The chunk is taken in register tiles of 16384 elements, all of a
@@ -1116,7 +1175,7 @@ __device__ __forceinline__ void sample_top(const SampleArgs& sa, float u, const 
 // complete and counts its arrival on the caller's counters[row]; the row's last arrival merges the lists (merge_lists)
 // and zeroes the counter for the next launch -- no L2 write-back or invalidate, and no second kernel (the protocol of
 // topk/kernel.cu:411-442, without its __threadfence: see hand_off_arrive).
-template <typename T, bool VEC, bool ONE>
+template <typename T, bool VEC>
 __global__ void __launch_bounds__(kThreads)
     topk_tile(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
               u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
@@ -1137,44 +1196,6 @@ __global__ void __launch_bounds__(kThreads)
   const int kw = (k + kWaves - 1) / kWaves;
   using TL = Tile<T, VEC>;
   constexpr int TE = kThreads * kTileE;
-  if constexpr (ONE) {
-    // k = 1 (its own instance): the chunk's largest composite, straight from the registers (no bound, list or block
-    // reductions per tile)
-    u64 best = 0;
-    for (int t0 = begin; t0 < end; t0 += TE) {
-      TL tile;
-      tile.load(xr, t0, end);
-      const u64 c = tile.best_composite();
-      best = c > best ? c : best;
-    }
-    best = wave_ext64<true>(best);
-    if (lane_id() == 0) s.sorted[wave_id()] = best;
-    __syncthreads();
-    if (wave_id() != 0) return;
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) best = s.sorted[w] > best ? s.sorted[w] : best;
-    u64 c = best;
-    if (nchunks > 1) {
-      // the chunk's best goes to its slot work[row * nchunks + part]; the row's last arrival takes the largest slot
-      // and zeroes the row's counter for the next launch
-      u64* slots = work + row * (long long)nchunks;
-      if (lane_id() == 0) __hip_atomic_store(slots + part, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (!hand_off_arrive(counters + row, nchunks)) return;
-      u64 m = 0;
-      for (int i = lane_id(); i < nchunks; i += kWave) {
-        const u64 v = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        m = v > m ? v : m;
-      }
-      c = wave_ext64<true>(m);
-      if (lane_id() == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (lane_id() != 0) return;
-    if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row] = composite_bits(c);
-    else static_cast<uint16_t*>(values)[row] = (uint16_t)(composite_bits(c) >> 16);
-    indices[row] = composite_index(c);
-    if (sa.out) sa.out[row] = composite_index(c);  // the draw from a one-entry list
-    return;
-  }
   auto process = [&](TL& tile, bool more) __attribute__((always_inline)) {
     const bool has = tile.lane0 < tile.b1;
     const uint32_t m = tile.max_key();  // vector by vector as the loads complete
@@ -1688,13 +1709,16 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, void* 
     const long long tail = cols - (long long)(nchunks - 1) * chunk;
     if (nchunks > 1 && tail < (long long)kThreads * Tile<T, VEC>::W && chunk + tail <= (long long)kThreads * kTileE)
       --nchunks;
-    const dim3 grid((unsigned)nchunks, (unsigned)rows);
-    if (k == 1)
-      hipLaunchKernelGGL((topk_tile<T, VEC, true>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
-                         (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k, sa);
-    else
-      hipLaunchKernelGGL((topk_tile<T, VEC, false>), grid, dim3(kThreads), 0, stream, (const T*)x, values,
-                         (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k, sa);
+    if (k == 1) {
+      const int groups = (nchunks + kOneChunks - 1) / kOneChunks;
+      hipLaunchKernelGGL((topk_one<T, VEC>), dim3((unsigned)groups, (unsigned)rows), dim3(kOneThreads), 0, stream,
+                         (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk,
+                         nchunks, groups, sa);
+      return (int)hipGetLastError();
+    }
+    hipLaunchKernelGGL((topk_tile<T, VEC>), dim3((unsigned)nchunks, (unsigned)rows), dim3(kThreads), 0, stream,
+                       (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk, nchunks,
+                       k, sa);
     return (int)hipGetLastError();
   }
   // The result does not depend on the chunking, so the chunks are made long enough for a useful bound (16k elements:
@@ -1736,7 +1760,7 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
   if (per_cu <= 0) {
     if (occ <= 0) {
       int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_tile<float, true, false>, kThreads, 0) != hipSuccess ||
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_tile<float, true>, kThreads, 0) != hipSuccess ||
           n <= 0) {
         (void)hipGetLastError();
         n = 4;

@@ -3,14 +3,14 @@
 
 Each workgroup thread is a cooperative fiber and each cross-lane operation an exchange between barriers of the wave's
 live lanes. Every buffer the kernels touch (input, outputs, the caller's work and counters) lies between guard pages,
-so an out-of-bounds access ends the run with a fault, and a launch that allocates device memory fails the case. The cases cover
-single- and split-chunk rows, every k class (1, the lane-maxima bound up to 64, the wide path up to 1024), short last
-tiles, ties, monotone and all-negative rows, the all-ones NaN, repeated launches on the same buffers (the arrival
-counters' self-reset), and shuffled workgroup and lane schedules. The concurrent cases run every workgroup of a launch
-on an OS thread of its own, so chunks publish and count their arrivals while the row's other chunks and merger run.
-The waves-ahead cases let each wave run on to the next block barrier before the next wave starts, so that a
-__shared__ value one wave changes without a barrier reaches the waves after it. The weak cases make agent-scope stores visible to other workgroups late and
-out of order, as the memory system may:
+so an out-of-bounds access ends the run with a fault, and a launch that allocates device memory fails the case. The
+cases cover single- and split-chunk rows, every k class (1, the lane-maxima bound up to 64, the wide path up to
+1024), short last tiles, ties, monotone and all-negative rows, the all-ones NaN, repeated launches on the same buffers
+(the arrival counters' self-reset), and shuffled workgroup and lane schedules. The concurrent cases run every
+workgroup of a launch on an OS thread of its own, so chunks publish and count their arrivals while the row's other
+chunks and merger run. The waves-ahead cases let each wave run on to the next block barrier before the next wave
+starts, so that a __shared__ value one wave changes without a barrier reaches the waves after it. The weak cases make
+agent-scope stores visible to other workgroups late and out of order, as the memory system may:
 a store drains when its lane waits with `s_waitcnt vmcnt(0)`, at random before that, and, when its lane has ended
 without waiting, one store at a time now and then, or when the launch completes. The hand-off (result stores, the wait,
 then the arrival count) must stay exact under it, and the same cases with the wait taken out (a planted mistake, on the
@@ -52,6 +52,10 @@ CASES = [
     ("shuffled", 2, 20000, 0, ALL_K, 4096, 2048, 2, 15, 99, "randn"),
     ("shuffled_bf16", 2, 20000, 1, "1,50,1024", 2052, 2048, 2, 16, 7, "ints"),
     ("many_chunks_wide", 2, 100000, 0, "65", 1024, 2048, 1, 17, -1, "randn"),
+    # six lists of 1024 in the merge; with ties every list entry reaches the floor, and the merge prunes to k while
+    # it gathers
+    ("wide_six_lists", 2, 6 * 16384, 0, "1024", 16384, 2048, 1, 18, -1, "randn"),
+    ("wide_six_lists_ties", 2, 6 * 16384, 0, "1024", 16384, 2048, 1, 19, -1, "ints"),
 ]
 
 

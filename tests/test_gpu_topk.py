@@ -102,6 +102,18 @@ def test_ties_and_special_values(pkg, oracle, dev):
     check(pkg, oracle, s, 7, dev, chunk=1000, what="special split")
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_wide_merge_six_lists(pkg, oracle, dev, dt):
+    # six lists of 1024 in the k > 64 merge; with ties every list entry reaches the floor, and the merge prunes to k
+    # while it gathers
+    g = torch.Generator().manual_seed(21)
+    x = (torch.randn(3, 6 * 16384, generator=g) * 2).to(dt)
+    assert check(pkg, oracle, x, 1024, dev, chunk=16384, what="six lists") == 6
+    t = torch.randint(0, 6, (3, 6 * 16384), generator=g).float().to(dt)
+    check(pkg, oracle, t, 1024, dev, chunk=16384, what="six lists, ties")
+    check(pkg, oracle, t, 700, dev, chunk=16384, what="six lists, ties")
+
+
 def test_adversarial_orders(pkg, oracle, dev):
     # ascending rows: every tile beats the threshold so far (many prunes); descending: the first tile is the answer
     a = torch.arange(40000, dtype=torch.float32).view(1, -1).repeat(2, 1)
