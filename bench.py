@@ -5,6 +5,8 @@
     python bench.py --ceiling                   # the practical HBM ceiling at each workload's size (probe kernels)
     python bench.py --probes                    # every probe structure and cache policy at each workload's size
     python bench.py --build-probes              # compile the probes (bench_probes.hip) into _build/
+    python bench.py --topk-stages               # where a top-k launch's time goes, stage by stage (stage build)
+    python bench.py --build-topk-stages         # compile that build (csrc/topk.hip with its stamps) into _build/
     python bench.py --profile-summary DIR       # turn one profiling lease's outputs into profiles/
     python bench.py --traffic-from DIR          # turn FETCH_SIZE / WRITE_SIZE counter runs into profiles/traffic.json
 
@@ -61,8 +63,8 @@ def parse():
     p.add_argument("--workload", default=None, help="measure only this workload (default: all)")
     p.add_argument("--k", type=int, default=None, help="top-k: measure only this k (default: 1, 50 and 1024)")
     p.add_argument("--tune", action="append", default=[],
-                   help="op:slot=value, set before measuring through the op library's tuning hook (e.g. topk:1=1 "
-                        "for the last-arrival merge of k > 64); may be repeated")
+                   help="op:slot=value, set before measuring through the op library's tuning hook (e.g. topk:0=2 "
+                        "for plan()'s resident workgroups per CU); may be repeated")
     p.add_argument("--no-cold", action="store_true", help="skip the flushed single-launch timing")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=20.0,
@@ -81,6 +83,10 @@ def parse():
                                                          "sets beside the probes")
     p.add_argument("--build-probes", action="store_true",
                    help="compile bench_probes.hip into _build/libbench_probes.so (on a host with hipcc)")
+    p.add_argument("--topk-stages", action="store_true",
+                   help="only the top-k stage timeline at 128 x 128256 fp32, k = 1, 50 and 1024 (the stage build)")
+    p.add_argument("--build-topk-stages", action="store_true",
+                   help="compile csrc/topk.hip with its stage stamps into _build/libtopk_stages.so")
     p.add_argument("--profile-summary", default=None,
                    help="directory of one profiling lease (bench.json, stats/, traffic/, occ/): writes profiles/")
     p.add_argument("--traffic-from", default=None,
@@ -419,6 +425,130 @@ def probe_lib():
     lib.probe_run.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p] * 3 + [ctypes.c_longlong, ctypes.c_void_p]
     lib.probe_run.restype = ctypes.c_int
     return lib
+
+
+STAGES_LIB = os.path.join(ROOT, "_build", "libtopk_stages.so")
+
+
+def build_topk_stages():
+    """Compiles csrc/topk.hip with ROWKERN_TOPK_STAGES (per-workgroup stage stamps, see the file) into
+    _build/libtopk_stages.so: a timing build beside the op library, which is built without the stamps."""
+    import subprocess
+    from __graft_entry__ import load_package
+    load_package()
+    from ck5090_amd import make_libs
+    os.makedirs(os.path.dirname(STAGES_LIB), exist_ok=True)
+    tmp = STAGES_LIB + ".tmp"
+    src = os.path.join(make_libs.CSRC, "topk.hip")
+    proc = subprocess.run([make_libs.hipcc(), *make_libs.HIPCC_FLAGS, *make_libs.OP_FLAGS["topk"],
+                           "-DROWKERN_TOPK_STAGES", "-I", make_libs.CSRC, src, "-o", tmp], capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for the top-k stage build ({proc.returncode}):\n" + proc.stderr[-6000:])
+    os.replace(tmp, STAGES_LIB)
+    return STAGES_LIB
+
+
+# The stamped stages of each top-k kernel (slot: name); slots 16 + w hold wave w's loads-landed moment.
+TOPK_STAGES = {
+    "topk_one": [(0, "start"), (1, "loads landed (wave 0)"), (2, "workgroup's best"), (3, "arrival counted"),
+                 (8, "row written")],
+    "topk_tile": [(0, "start"), (1, "loads landed (wave 0)"), (2, "threshold"), (3, "tile filtered and settled"),
+                  (4, "chunk list published"), (5, "arrival counted"), (6, "merge: heads floor"),
+                  (7, "merge: lists streamed and settled"), (8, "row written")],
+    "topk_wide": [(0, "start"), (1, "loads landed (wave 0)"), (2, "bounds"), (3, "tile appended"), (4, "cut to k"),
+                  (5, "arrival counted"), (6, "merge: floor from the headers"), (7, "merge: lists gathered"),
+                  (8, "row written")],
+}
+STAGE_SLOTS, STAGE_WGS = 32, 4096
+STAGE_TICK_US = 0.01  # s_memrealtime runs at 100 MHz
+
+
+def topk_stages(launches=3, copies=5):
+    """The stage timeline of one top-k launch per k (1, 50, 1024) at 128 x 128256 fp32, from the stage build: per
+    stage, when the workgroups reach it (from the launch's first stamp) and how long each workgroup spends from the
+    stage before (the per-workgroup delta). Each timed launch reads a copy of x last read `copies` - 1 launches
+    earlier (more bytes than the caches hold), after warm-up launches. Returns the text lines."""
+    import ctypes
+    import numpy as np
+    import torch
+    if not os.path.exists(STAGES_LIB):
+        raise RuntimeError(f"no stage build at {STAGES_LIB}: build it first (python bench.py --build-topk-stages)")
+    lib = ctypes.CDLL(STAGES_LIB)
+    lib.plan.argtypes = [ctypes.c_longlong, ctypes.c_longlong, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    lib.plan.restype = ctypes.c_longlong
+    lib.launch.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_longlong, ctypes.c_longlong] + [ctypes.c_int] * 4 + \
+                          [ctypes.c_longlong, ctypes.c_void_p]
+    lib.topk_stages_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong]
+    rows, cols = 128, 128256
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    xs = [torch.randn(rows, cols, device=dev, generator=g) * 2 for _ in range(copies)]
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = []
+    for k, kernel in ((1, "topk_one"), (50, "topk_tile"), (1024, "topk_wide")):
+        chunk = lib.plan(rows, cols, 0, 256, 4, max(2048, 16 * k) if k > 64 else 2048)
+        nch = -(-cols // chunk)
+        vals = torch.empty(rows, k, device=dev)
+        idx = torch.empty(rows, k, dtype=torch.int64, device=dev)
+        work = torch.empty(rows * nch * k, dtype=torch.int64, device=dev)
+        counters = torch.zeros(rows, dtype=torch.int32, device=dev)
+
+        def go(i):
+            x = xs[i % copies]
+            rc = lib.launch(x.data_ptr(), vals.data_ptr(), idx.data_ptr(), work.data_ptr(), counters.data_ptr(), rows,
+                            cols, k, 0, 256, 4, chunk, stream)
+            if rc != 0:
+                raise RuntimeError(f"top-k stage build: launch returned {rc}")
+        for i in range(2 * copies + 1):  # the last warm-up launch reads copy 0
+            go(i)
+        torch.cuda.synchronize()
+        ref = torch.topk(xs[0], k, dim=1)
+        if not (torch.equal(vals, ref.values) and torch.equal(idx, ref.indices)):
+            raise RuntimeError(f"top-k stage build differs from torch.topk at k = {k}")
+        per = {i: ([], []) for i, _ in TOPK_STAGES[kernel]}
+        spans, wave_skew, wgs = [], [], 0
+        for rep in range(launches):
+            for i in range(1, copies):  # the other copies, then copy 0 again
+                go(i)
+            if lib.topk_stages_clear() != 0:
+                raise RuntimeError("topk_stages_clear failed")
+            go(0)
+            torch.cuda.synchronize()
+            buf = np.zeros(STAGE_WGS * STAGE_SLOTS, dtype=np.uint64)
+            if lib.topk_stages_read(buf.ctypes.data, buf.nbytes) != 0:
+                raise RuntimeError("topk_stages_read failed")
+            t = buf.reshape(STAGE_WGS, STAGE_SLOTS).astype(np.int64)
+            t = t[t[:, 0] > 0]
+            wgs = len(t)
+            t0 = t[:, 0].min()
+            spans.append((t[:, :16].max() - t0) * STAGE_TICK_US)
+            waves = t[:, 16:]
+            seen = waves > 0
+            lo = np.where(seen, waves, np.iinfo(np.int64).max).min(axis=1)
+            hi = np.where(seen, waves, 0).max(axis=1)
+            wave_skew += list((hi - lo)[seen.any(axis=1)] * STAGE_TICK_US)
+            prev = None
+            for i, _ in TOPK_STAGES[kernel]:
+                col = t[:, i]
+                per[i][0].extend(((col[col > 0] - t0) * STAGE_TICK_US).tolist())
+                if prev is not None:
+                    ok = (col > 0) & (t[:, prev] > 0)
+                    per[i][1].extend(((col[ok] - t[ok, prev]) * STAGE_TICK_US).tolist())
+                prev = i
+        out.append(f"k = {k}: {kernel}, {wgs} workgroups (chunk {chunk}), {launches} launches; launch span (first stamp "
+                   f"to last) median {np.median(spans):.2f} us; loads landed across one workgroup's waves: median "
+                   f"{np.median(wave_skew):.2f}, p90 {np.percentile(wave_skew, 90):.2f} us")
+        out.append(f"  {'stage':36s} {'workgroups':>10s} {'reached: median':>16s} {'p90':>7s} {'max':>7s}   "
+                   f"{'from the stage before: median':>29s} {'p90':>7s}")
+        for i, name in TOPK_STAGES[kernel]:
+            at, d = (np.array(v) for v in per[i])
+            if len(at) == 0:
+                continue
+            dd = f"{np.median(d):29.2f} {np.percentile(d, 90):7.2f}" if len(d) else f"{'':29s} {'':7s}"
+            out.append(f"  {name:36s} {len(at) // launches:10d} {np.median(at):16.2f} {np.percentile(at, 90):7.2f} "
+                       f"{at.max():7.2f}   {dd}")
+        out.append("")
+    return out
 
 
 def parse_probe(spec):
@@ -840,6 +970,9 @@ def main():
     if args.build_probes:
         print(build_probes())
         return
+    if args.build_topk_stages:
+        print(build_topk_stages())
+        return
     if args.probe_summary:
         probe_summary(args.probe_summary, args.summary_bench)
         return
@@ -862,6 +995,9 @@ def main():
         print(f"[tune] {op} slot {slot} = {value}", file=sys.stderr, flush=True)
     if args.ceiling:
         ceiling(pkg, args.steps, args.warmup)
+        return
+    if args.topk_stages:
+        print("\n".join(topk_stages()), flush=True)
         return
     if args.probes:
         probe_sweep(pkg, args.steps, args.warmup)

@@ -641,6 +641,35 @@ constexpr int kWideGroups = 8;  // groups per lane for the admission bound of th
 // What a vector load past a tile's end reads instead (all ones: the sentinel below).
 __device__ u32x4 g_sentinel_vec = {~0u, ~0u, ~0u, ~0u};
 
+// Stage stamps, for a separate timing build only (bench.py --topk-stages compiles this file with ROWKERN_TOPK_STAGES
+// into its own library; the op library is built without it, and there TOPK_STAGE and TOPK_WAVE_STAGE compile to
+// nothing). Thread 0 of each workgroup records the 100 MHz s_memrealtime clock at stage i of its kernel in slot i of
+// the workgroup's row of stamps, and lane 0 of each wave the moment its tile's loads have landed in slot 16 + wave.
+#ifdef ROWKERN_TOPK_STAGES
+constexpr long long kStageWGs = 4096;  // workgroups with stamps (blockIdx.y * gridDim.x + blockIdx.x below this)
+constexpr int kStageSlots = 32;
+__device__ unsigned long long g_stage_stamps[kStageWGs * kStageSlots];
+__device__ __forceinline__ void stage_stamp(int slot) {
+  const long long wg = (long long)blockIdx.y * gridDim.x + blockIdx.x;
+  if (wg < kStageWGs) g_stage_stamps[wg * kStageSlots + slot] = __builtin_amdgcn_s_memrealtime();
+}
+#define TOPK_STAGE(i) \
+  do {                              \
+    if (threadIdx.x == 0) stage_stamp(i); \
+  } while (0)
+#define TOPK_WAVE_STAGE()                                                                       \
+  do {                                                                                          \
+    if ((threadIdx.x & 63) == 0 && (threadIdx.x >> 6) < 16) stage_stamp(16 + (int)(threadIdx.x >> 6)); \
+  } while (0)
+#else
+#define TOPK_STAGE(i) \
+  do {                \
+  } while (0)
+#define TOPK_WAVE_STAGE() \
+  do {                    \
+  } while (0)
+#endif
+
 // A register tile: thread t of the workgroup's NT holds vectors v * NT + t (v < NV) of elements [b0, b1) of a row, W
 // each, as raw bits; an element outside [b0, b1) holds the sentinel (all ones: the -NaN whose key is the smallest of
 // its format), read from g_sentinel_vec by a vector load past the end. load() only issues the loads.
@@ -948,6 +977,7 @@ __device__ __forceinline__ void merge_lists(TileSmem& s, BlockRed& red, TileList
       floor = s.pick;
     }
   }
+  TOPK_STAGE(6);
   for (int base = 0; base < total; base += kThreads * PER) {
     if (base > 0) load(base);
     const int cnt0 = L.cnt;
@@ -965,6 +995,7 @@ __device__ __forceinline__ void merge_lists(TileSmem& s, BlockRed& red, TileList
         listed);
     floor = kth > floor ? kth : floor;
   }
+  TOPK_STAGE(7);
   finish_list<T>(s, L, values, indices, nullptr, row, k, true);
 }
 
@@ -1129,6 +1160,7 @@ __global__ void __launch_bounds__(kOneThreads)
   const int begin = (int)((long long)group * kOneChunks * chunk);
   const int end = (int)(group == groups - 1 ? cols : begin + kOneChunks * chunk);  // the last group ends the row
   const T* xr = x + row * cols;
+  TOPK_STAGE(0);
   using TL = Tile<T, VEC, kOneThreads>;
   constexpr int TE = kOneThreads * kTileE;
   u64 best = 0;
@@ -1138,15 +1170,20 @@ __global__ void __launch_bounds__(kOneThreads)
     const u64 c = tile.best_composite();
     best = c > best ? c : best;
   }
+  TOPK_STAGE(1);
+  TOPK_WAVE_STAGE();
   best = wave_ext64<true>(best);
   if (lane_id() == 0) best_of[wave_id()] = best;
   __syncthreads();
+  TOPK_STAGE(2);
   if (wave_id() != 0) return;
   best = wave_ext64<true>(lane_id() < kOneThreads / kWave ? best_of[lane_id()] : 0ull);
   if (groups > 1) {
     u64* slots = work + row * (long long)nchunks;
     if (lane_id() == 0) __hip_atomic_store(slots + group, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (!hand_off_arrive(counters + row, groups)) return;
+    const bool last = hand_off_arrive(counters + row, groups);
+    TOPK_STAGE(3);
+    if (!last) return;
     u64 m = 0;
     for (int i = lane_id(); i < groups; i += kWave) {
       const u64 v = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1160,6 +1197,7 @@ __global__ void __launch_bounds__(kOneThreads)
   else static_cast<uint16_t*>(values)[row] = (uint16_t)(composite_bits(best) >> 16);
   indices[row] = composite_index(best);
   if (sa.out) sa.out[row] = composite_index(best);  // the draw from a one-entry list
+  TOPK_STAGE(8);
 }
 
 // ---- the k <= 64 kernel --------------------------------------------------------------------------------------------
@@ -1192,6 +1230,7 @@ __global__ void __launch_bounds__(kThreads)
   TileList L;
   L.seg = s.seg[wave_id()];
   L.cnt = 0;
+  TOPK_STAGE(0);
   uint32_t thr = 0;
   const int kw = (k + kWaves - 1) / kWaves;
   using TL = Tile<T, VEC>;
@@ -1199,8 +1238,11 @@ __global__ void __launch_bounds__(kThreads)
   auto process = [&](TL& tile, bool more) __attribute__((always_inline)) {
     const bool has = tile.lane0 < tile.b1;
     const uint32_t m = tile.max_key();  // vector by vector as the loads complete
+    TOPK_STAGE(1);
+    TOPK_WAVE_STAGE();
     const uint32_t tw = __popcll(__ballot(has)) >= kw ? wave_kth32(m, has, kw) : 0u;
     const uint32_t tb = red.min(tw);
+    TOPK_STAGE(2);
     thr = tb > thr ? tb : thr;
     L.cnt = __builtin_amdgcn_readfirstlane(L.cnt);
     const int cnt0 = L.cnt;
@@ -1228,6 +1270,7 @@ __global__ void __launch_bounds__(kThreads)
     tile.load(xr, t0, end);
     process(tile, end - t0 > TE);
   }
+  TOPK_STAGE(3);
   if (nchunks == 1) {
     const float u = sa.uniform(row);
     finish_list<T>(s, L, values, indices, nullptr, row, k, true);
@@ -1236,11 +1279,15 @@ __global__ void __launch_bounds__(kThreads)
   }
   u64* wr = work + row * (long long)nchunks * k;
   finish_list<T>(s, L, values, indices, wr + (long long)part * k, row, k, false);
+  TOPK_STAGE(4);
   // hand-off: the row's last arrival merges the lists and zeroes the row's counter for the next launch
-  if (!block_hand_off(s, counters + row, nchunks)) return;
+  const bool last = block_hand_off(s, counters + row, nchunks);
+  TOPK_STAGE(5);
+  if (!last) return;
   const float u = sa.uniform(row);
   L.cnt = 0;
   merge_lists<T>(s, red, L, values, indices, wr, row, nchunks, k);
+  TOPK_STAGE(8);
   if (threadIdx.x == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   sample_top(sa, u, s.top, row, k);
 }
@@ -1547,6 +1594,7 @@ __global__ void __launch_bounds__(kThreads)
     s.thr = 1;
   }
   __syncthreads();
+  TOPK_STAGE(0);
   uint32_t thr = 0, thq = 0;
   const int q = (k + nchunks - 1) / nchunks;
   const int kw = (k + kWaves - 1) / kWaves, kwq = (q + kWaves - 1) / kWaves;
@@ -1559,6 +1607,8 @@ __global__ void __launch_bounds__(kThreads)
     const int cnt0 = s.count;  // block-uniform: the buffer is settled between tiles
     uint32_t g[kWideGroups];
     tile.group_keys(g);
+    TOPK_STAGE(1);
+    TOPK_WAVE_STAGE();
     const uint32_t tw = wave_kth_multi<kWideGroups>(g, kw, 0u);
     const uint32_t tb = red.min(tw);
     thr = tb > thr ? tb : thr;
@@ -1568,6 +1618,7 @@ __global__ void __launch_bounds__(kThreads)
       const uint32_t qb = red.min(wave_kth_multi<kWideGroups>(g, kwq, tw));
       thq = qb > thq ? qb : thq;
     }
+    TOPK_STAGE(2);
     tile.opaque();
     bool redo = true;
     if (thr > TL::kSentinelKey) {
@@ -1601,6 +1652,7 @@ __global__ void __launch_bounds__(kThreads)
     sample_list<T>(sa, u, values, indices, row, k);
     return;
   }
+  TOPK_STAGE(3);
   // the chunk's k largest (its k-th raises s.thr)
   if (s.count > kWideList) prune(s, k);
   else if (s.count > k) prune_bucketed(s, s.count, k);
@@ -1610,12 +1662,15 @@ __global__ void __launch_bounds__(kThreads)
   u64* mine = wr + (long long)part * k;
   for (int i = threadIdx.x; i < k; i += kThreads)
     __hip_atomic_store(mine + i, i < n ? s.buf[i] : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  TOPK_STAGE(4);
   u64* heads = reinterpret_cast<u64*>(indices + row * k);
   if (threadIdx.x == 0) {
     const uint32_t kb = (uint32_t)(s.thr >> 32) > thr ? (uint32_t)(s.thr >> 32) : thr;
     __hip_atomic_store(heads + part, ((u64)kb << 32) | thq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (!block_hand_off(s, counters + row, nchunks)) return;
+  const bool last = block_hand_off(s, counters + row, nchunks);
+  TOPK_STAGE(5);
+  if (!last) return;
   const float u = sa.uniform(row);
   // merge (the row's last arrival): the floor from the headers, then every list's entries at or above it
   auto ld = [&](const u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
@@ -1635,6 +1690,7 @@ __global__ void __launch_bounds__(kThreads)
     s.thr = floor;
   }
   __syncthreads();
+  TOPK_STAGE(6);
   constexpr int PER = kMaxK / kThreads;  // list entries per thread (k <= kMaxK)
   constexpr int kInFlight = 2;           // lists whose loads are in flight while one is taken (4 measured no faster)
   static_assert(PER * kThreads <= kWideCap - kWideList, "room for a whole list above a buffer of kWideList");
@@ -1672,8 +1728,10 @@ __global__ void __launch_bounds__(kThreads)
       }
     }
   }
+  TOPK_STAGE(7);
   if (s.count > kWideList) prune(s, k);
   write_ranked<T>(s, s.count, k, values, indices, row, floor);  // every candidate kept is at or above the floor
+  TOPK_STAGE(8);
   if (threadIdx.x == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   sample_list<T>(sa, u, values, indices, row, k);
 }
@@ -1938,3 +1996,16 @@ extern "C" int topk_sample_launch(const void* values, const void* indices, const
 }
 
 extern "C" int topk_tune(int slot, int value) { return rw_host::tune_set(slot, value); }
+
+#ifdef ROWKERN_TOPK_STAGES
+// The stage build's read-out: the stamps of the last launches (dst: host memory of `bytes`, at most the table) and
+// their reset to zero.
+extern "C" int topk_stages_read(void* dst, long long bytes) {
+  if (!dst || bytes < 0 || bytes > (long long)sizeof(g_stage_stamps)) return rw_host::kInvalid;
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_stage_stamps), (size_t)bytes, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int topk_stages_clear() {
+  static unsigned long long zeros[kStageWGs * kStageSlots];
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_stage_stamps), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+}
+#endif

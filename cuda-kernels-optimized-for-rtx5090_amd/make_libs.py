@@ -28,9 +28,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-# Per-op additions. topk: no wave-level atomic optimizer, which turns the start-order count (an atomic by one lane,
-# issued first thing in the k <= 64 kernel) into a broadcast of its result that waits for the atomic before the tile's
-# loads are issued.
+# Per-op additions. topk: no wave-level atomic optimizer: every atomic of the top-k kernels (the arrival counts, the
+# LDS list reservations) is issued by one lane already, and the optimizer's scan and broadcast around it would only
+# add instructions and waits.
 OP_FLAGS = {"topk": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
 
 

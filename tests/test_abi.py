@@ -64,6 +64,22 @@ def test_probe_library_exports_and_codes_without_gpu():
         bench.parse_probe(spec)
 
 
+def test_topk_stage_build_is_separate(pkg):
+    # the top-k stage stamps (bench.py --topk-stages) live in a build of their own: the op library exports none of
+    # the read-out, the stage build exports the op library's entry points plus the read-out, and its read-out checks
+    # its arguments before any copy
+    import bench
+    assert os.path.exists(bench.STAGES_LIB), f"{bench.STAGES_LIB} not built"
+    op = {s for s in exported(pkg.lib_path("topk")) if not s.startswith("_")}
+    staged = {s for s in exported(bench.STAGES_LIB) if not s.startswith("_")}
+    assert not any(s.startswith("topk_stages") for s in op)
+    assert staged == op | {"topk_stages_read", "topk_stages_clear"}
+    lib = ctypes.CDLL(bench.STAGES_LIB)
+    lib.topk_stages_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong]
+    assert lib.topk_stages_read(None, 8) == -1
+    assert lib.topk_stages_read(ctypes.c_void_p(16), (bench.STAGE_WGS * bench.STAGE_SLOTS + 1) * 8) == -1
+
+
 def test_softmax_codes_without_gpu(pkg):
     lib = ctypes.CDLL(pkg.lib_path("softmax"))
     assert lib.launch(None, None, ctypes.c_longlong(0), ctypes.c_longlong(5), 0, 256, 1024, None) == 0
