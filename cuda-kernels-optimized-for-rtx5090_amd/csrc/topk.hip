@@ -1750,10 +1750,48 @@ __global__ void __launch_bounds__(kWave)
   if (lane_id() == 0) out[row] = drawn;
 }
 
+// ---- the naive tier ------------------------------------------------------------------------------------------------
+
+// The naive tier (the harness's "seed" column; launch() takes it when tuning slot 1 is 1): one workgroup per row
+// takes the row's k largest one at a time, each round a scan of the whole row, element by element, for the largest
+// composite below the previous round's. Exact by construction (the composites are distinct) and k passes over the row.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    topk_seed(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices, long long cols,
+              int k) {
+  __shared__ u64 part[kWaves];
+  const long long row = blockIdx.x;
+  const T* xr = x + row * cols;
+  u64 prev = ~0ull;  // above every composite
+  for (int r = 0; r < k; ++r) {
+    u64 best = 0;  // below every composite of an element
+    for (long long j = threadIdx.x; j < cols; j += kThreads) {
+      uint32_t u;
+      if constexpr (sizeof(T) == 4) u = reinterpret_cast<const uint32_t*>(xr)[j];
+      else u = (uint32_t)reinterpret_cast<const uint16_t*>(xr)[j] << 16;
+      const u64 c = composite(u, (uint32_t)j);
+      best = c < prev && c > best ? c : best;
+    }
+    best = wave_ext64<true>(best);
+    if (lane_id() == 0) part[wave_id()] = best;
+    __syncthreads();
+    u64 m = part[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) m = part[w] > m ? part[w] : m;
+    __syncthreads();  // every wave has read part before the next round rewrites it
+    if (threadIdx.x == 0) {
+      if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + r] = composite_bits(m);
+      else static_cast<uint16_t*>(values)[row * k + r] = (uint16_t)(composite_bits(m) >> 16);
+      indices[row * k + r] = composite_index(m);
+    }
+    prev = m;
+  }
+}
+
 // ---- host side ------------------------------------------------------------------------------------------------------
 
-// Tuning slot (0 = automatic): 0 resident workgroups per CU assumed by plan().
-enum { kTuneBlocksPerCu = 0 };
+// Tuning slots (0 = automatic): 0 resident workgroups per CU assumed by plan(); 1 the naive tier for launch() (1).
+enum { kTuneBlocksPerCu = 0, kTuneSeed = 1 };
 
 // The kernels of a launch whose rows are split into nchunks chunks of `chunk` columns. work and counters are the
 // caller's (work: u64 [rows * nchunks * k]; counters: u32 [rows], zero); the launch may join chunks (fewer, longer
@@ -1856,6 +1894,16 @@ int launch_impl(const void* x, void* values, void* indices, void* work, void* co
   if ((threads != 128 && threads != 256 && threads != 512) || (depth != 2 && depth != 4 && depth != 8))
     return rw_host::kInvalid;
   if (nchunks > 1 && (!work || !counters)) return rw_host::kInvalid;
+  if (dtype != 0 && dtype != 1) return rw_host::kInvalid;
+  if (!sa.out && rw_host::tune_get(kTuneSeed) == 1) {
+    if (dtype == 0)
+      hipLaunchKernelGGL(topk_seed<float>, dim3((unsigned)rows), dim3(kThreads), 0, stream, (const float*)x, values,
+                         (long long*)indices, cols, k);
+    else
+      hipLaunchKernelGGL(topk_seed<uint16_t>, dim3((unsigned)rows), dim3(kThreads), 0, stream, (const uint16_t*)x,
+                         values, (long long*)indices, cols, k);
+    return (int)hipGetLastError();
+  }
   const int n = (int)nchunks;
   if (dtype == 0) {
     if (cols % 4 == 0 && rw_host::aligned16(x))

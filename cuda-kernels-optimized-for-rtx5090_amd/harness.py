@@ -2,7 +2,7 @@
 other ops' READMEs): each workload is run through the op's candidate wrapper (`run(inputs)`, with the op's
 params.json), the PyTorch GPU path the reference calls its baseline, and the op's naive kernel (the "seed": this
 build's scalar tier, forced through the tuning hook); correctness is checked against an fp64 (or exact) reference
-computed here, and a Markdown table is printed:
+computed here, for the seed's output too, and a Markdown table is printed:
 
     | workload | correctness | timing | candidate ms | baseline ms | seed ms | vs baseline | vs seed | dtype |
 
@@ -136,7 +136,7 @@ class Case:
 
     def seed(self):
         """The naive scalar tier of this build (None when the op has none)."""
-        slot = {"softmax": (5, 3), "rmsnorm": (3, 1), "rope": (2, 1)}.get(self.op)
+        slot = {"softmax": (5, 3), "rmsnorm": (3, 1), "rope": (2, 1), "topk": (1, 1)}.get(self.op)
         if slot is None:
             return None
         tune = getattr(self.cand._lib, f"{self.op}_tune")
@@ -206,10 +206,13 @@ def run(ops=("softmax", "rmsnorm", "rope", "topk"), quick=False, reps=20):
         for name, dt, shape in WORKLOADS[op](quick):
             case = Case(pkg, op, dt, shape, dev)
             ok = case.check(case.candidate())
+            seed_out = case.seed()
+            seed_ok = seed_out is None or case.check(seed_out)
             cand = time_ms(case.candidate, reps, flush)
             base = time_ms(case.baseline, reps, flush)
-            seed = time_ms(case.seed, reps, flush) if case.seed() is not None else None
-            rows.append({"op": op, "workload": name, "correctness": "PASS" if ok else "FAIL",
+            seed = time_ms(case.seed, reps, flush) if seed_out is not None else None
+            correct = ("PASS" if seed_ok else "FAIL (seed)") if ok else "FAIL"
+            rows.append({"op": op, "workload": name, "correctness": correct,
                          "timing": "PASS" if cand <= base else "FAIL", "candidate_ms": cand, "baseline_ms": base,
                          "seed_ms": seed, "dtype": dt})
             del case

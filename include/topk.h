@@ -68,7 +68,8 @@ int topk_launch_sample(const void* x, void* values, void* indices, void* work, v
                        void* out, float temperature, float top_p, hipStream_t stream);
 
 /* No counterpart in the reference: tuning override for parameter sweeps. Slot 0: resident workgroups per CU assumed by
- * plan(). Returns 0 or -1. */
+ * plan(); slot 1: 1 makes launch() take the naive tier (one workgroup per row, one scan of the row per output
+ * position: the harness's seed column). Returns 0 or -1. */
 int topk_tune(int slot, int value);
 
 #ifdef __cplusplus

@@ -31,6 +31,7 @@ extern "C" int topk_launch_sample(const void* x, void* values, void* indices, vo
 extern "C" int topk_sample_launch(const void* values, const void* indices, const float* uniforms, void* out,
                                   long long rows, int k, int dtype, float temperature, float top_p,
                                   hipStream_t stream);
+extern "C" int topk_tune(int slot, int value);
 extern "C" void oracle_topk(const void* x, void* values, int64_t* indices, long long rows, long long cols, int k,
                             int dtype);
 extern "C" void oracle_topk_sample_band(const void* values, const float* u, int* lo, int* hi, long long rows, int k,
@@ -62,6 +63,7 @@ int main(int argc, char** argv) {
   emu::S().shuffle_seed = argc > 9 ? atoi(argv[9]) : -1;
   if (emu::S().shuffle_seed >= 0) emu::S().rng.seed(emu::S().shuffle_seed);
   const std::string pattern = argc > 10 ? argv[10] : "randn";
+  if (std::getenv("EMU_TOPK_NAIVE") && topk_tune(1, 1) != 0) return 2;  // launch() takes the naive tier
   const size_t esz = dtype == 0 ? 4 : 2;
   const size_t n = (size_t)rows * cols;
   std::vector<char> host(n * esz);

@@ -79,6 +79,19 @@ def test_emulated_topk_concurrent_workgroups(emu_topk, case):
     run(emu_topk, case[1:], concurrent=True)
 
 
+# the naive tier (tuning slot 1, the harness's seed column): rows, cols, dtype, ks, chunk, min_chunk, reps, seed,
+# shuffle seed, pattern
+NAIVE = [
+    ("naive_fp32", 2, 3001, 0, "1,7,50,64,65,300", 0, 2048, 1, 51, -1, "randn"),
+    ("naive_bf16_ties", 2, 2000, 1, "1,50,100", 0, 2048, 1, 52, 3, "ints"),
+]
+
+
+@pytest.mark.parametrize("case", NAIVE, ids=[c[0] for c in NAIVE])
+def test_emulated_topk_naive_tier(emu_topk, case):
+    run(emu_topk, case[1:], env=dict(os.environ, EMU_TOPK_NAIVE="1"))
+
+
 def test_emulated_topk_guard_below_start(emu_topk):
     # the same buffers placed flush against their lower guard page
     env = dict(os.environ, EMU_ALIGN_START="1")

@@ -114,6 +114,22 @@ def test_wide_merge_six_lists(pkg, oracle, dev, dt):
     check(pkg, oracle, t, 700, dev, chunk=16384, what="six lists, ties")
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_naive_tier(pkg, oracle, dev, dt):
+    # the naive tier (tuning slot 1: the harness's seed column), one scan of the row per output position, against the
+    # oracle: ties, every k class, unaligned lengths
+    L = lib(pkg)
+    g = torch.Generator().manual_seed(31)
+    cases = [(torch.randn(3, 5000, generator=g) * 2, 50), (torch.randint(0, 6, (2, 3001), generator=g).float(), 64),
+             (torch.randn(2, 1001, generator=g), 1), (torch.randn(2, 2003, generator=g), 300)]
+    assert L.topk_tune(1, 1) == 0
+    try:
+        for x, k in cases:
+            check(pkg, oracle, x.to(dt), k, dev, what="naive tier")
+    finally:
+        assert L.topk_tune(1, 0) == 0
+
+
 def test_adversarial_orders(pkg, oracle, dev):
     # ascending rows: every tile beats the threshold so far (many prunes); descending: the first tile is the answer
     a = torch.arange(40000, dtype=torch.float32).view(1, -1).repeat(2, 1)
