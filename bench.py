@@ -50,8 +50,8 @@ TRAFFIC_PATH = os.path.join(ROOT, "profiles", "traffic.json")
 # it are summed (the whole launch for the two-kernel paths)
 KERNELS = {"rmsnorm_16384x4096": "rmsnorm_rows", "softmax_4096x4096": "softmax_rows",
            "softmax_64x262144": "softmax_coop", "rope_4x4096_32q_8kv_128": "rope_vec",
-           "topk_128x128256_k50": "topk_tile", "topk_128x128256_k1024": "topk_wide",
-           "rmsnorm_add_16384x4096": "rmsnorm_rows",
+           "topk_128x128256_k1": "topk_one", "topk_128x128256_k50": "topk_tile",
+           "topk_128x128256_k1024": "topk_wide", "rmsnorm_add_16384x4096": "rmsnorm_rows",
            "rope_kv_4x4096_32q_8kv_128": "rope_vec"}
 
 
