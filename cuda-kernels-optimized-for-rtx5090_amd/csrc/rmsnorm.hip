@@ -283,14 +283,23 @@ int launch_typed(const void* x, const void* w, void* y, long long rows, int cols
                    (!RES || (rw_host::aligned16(res) && rw_host::aligned16(res_out)));
   const long long nvec = cols / T::V;
   if (vec && rw_host::tune_get(kTuneGeneric) != 1 && nvec <= (long long)kMaxWaves * kWave * kMaxNv) {
+    // One wave per row up to 4 vectors per lane (2048 two-byte columns), then more waves at 4 vectors per lane (and 8
+    // per lane once 16 waves are not enough).
+    auto auto_waves = [&] {
+      const int w = pow2_at_least((nvec + (long long)kWave * 4 - 1) / ((long long)kWave * 4));
+      return w > kMaxWaves ? kMaxWaves : w;
+    };
+    auto auto_nv = [&](int w) { return pow2_at_least((nvec + (long long)w * kWave - 1) / ((long long)w * kWave)); };
     int waves = rw_host::tune_get(kTuneWaves), nv = rw_host::tune_get(kTuneNv);
-    if (waves <= 0) {
-      // One wave per row up to 4 vectors per lane (2048 two-byte columns), then more waves at 4 vectors per lane
-      // (and 8 per lane once 16 waves are not enough).
-      waves = pow2_at_least((nvec + (long long)kWave * 4 - 1) / ((long long)kWave * 4));
-      if (waves > kMaxWaves) waves = kMaxWaves;
+    if (waves <= 0) waves = auto_waves();
+    if (nv <= 0) nv = auto_nv(waves);
+    // a tuned shape the row kernel does not have (launch_rows below) is ignored: the automatic choice runs
+    const bool shape = (waves == 1 || waves == 2 || waves == 4 || waves == 8 || waves == 16) &&
+                       (nv == 1 || nv == 2 || nv == 4 || nv == 8);
+    if (!shape) {
+      waves = auto_waves();
+      nv = auto_nv(waves);
     }
-    if (nv <= 0) nv = pow2_at_least((nvec + (long long)waves * kWave - 1) / ((long long)waves * kWave));
     if ((long long)waves * kWave * nv >= nvec) {
       const Args a{x, w, y, res, res_out, rows, nvec, cols, eps, stream};
       // non-temporal loads unless switched off (2): x is read once

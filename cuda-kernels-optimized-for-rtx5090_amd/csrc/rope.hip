@@ -333,6 +333,7 @@ int launch_shape(const Ptrs& p, const Shape& s, bool vec, hipStream_t stream) {
   if (vec && rw_host::tune_get(kTuneScalar) != 1) {
     const long long items = (long long)heads * (s.head_dim >> 4);
     int threads = rw_host::tune_get(kTuneThreads);
+    if (threads % kWave != 0 || threads > 1024) threads = 0;  // a tuned block the kernel cannot take: automatic
     if (threads <= 0) {
       // at most 256 threads per token block, the items spread evenly over them (e.g. 320 items: 192 threads, 2 each);
       // beyond 4 items per thread, up to 1024 threads

@@ -584,13 +584,22 @@ int launch_typed(const void* x, void* y, long long rows, long long cols, hipStre
   const bool ntl = rw_host::tune_get(kTuneNtLoads) == 1;
   if (tier != 4 && nvec <= (long long)kMaxWaves * kWave * kMaxNv) {
     // Row tier: 4 vectors per lane as long as 16 waves suffice, then up to 8.
-    int waves = rw_host::tune_get(kTuneWaves), nv = rw_host::tune_get(kTuneNv);
-    if (waves <= 0) {
+    auto auto_waves = [&] {
       const long long lanes = (nvec + 3) / 4;
-      waves = pow2_at_least((lanes + kWave - 1) / kWave);
-      if (waves > kMaxWaves) waves = kMaxWaves;
+      const int w = pow2_at_least((lanes + kWave - 1) / kWave);
+      return w > kMaxWaves ? kMaxWaves : w;
+    };
+    auto auto_nv = [&](int w) { return pow2_at_least((nvec + (long long)w * kWave - 1) / ((long long)w * kWave)); };
+    int waves = rw_host::tune_get(kTuneWaves), nv = rw_host::tune_get(kTuneNv);
+    if (waves <= 0) waves = auto_waves();
+    if (nv <= 0) nv = auto_nv(waves);
+    // a tuned shape the row kernel does not have (launch_rows below) is ignored: the automatic choice runs
+    const bool shape = (waves == 1 || waves == 2 || waves == 4 || waves == 8 || waves == 16) &&
+                       (nv == 1 || nv == 2 || nv == 4 || nv == 8 || (nv == 16 && waves <= 2));
+    if (!shape) {
+      waves = auto_waves();
+      nv = auto_nv(waves);
     }
-    if (nv <= 0) nv = pow2_at_least((nvec + (long long)waves * kWave - 1) / ((long long)waves * kWave));
     if ((long long)waves * kWave * nv >= nvec) {
       return ntl ? launch_rows<T, true>(waves, nv, x, y, rows, nvec, stream)
                  : launch_rows<T, false>(waves, nv, x, y, rows, nvec, stream);
