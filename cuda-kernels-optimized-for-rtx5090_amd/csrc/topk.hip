@@ -115,6 +115,22 @@ __device__ __forceinline__ int lanes_below(u64 mask) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+constexpr int kDppRowShr = 0x110;  // + n: row_shr:n, lane l reads lane l - n of its 16-lane row (0 below it)
+
+// Inclusive prefix sum of a u32 over the wave's lanes (lane order): DPP row shifts inside each 16-lane row, then the
+// sums of the rows below (lanes 15, 31 and 47) added.
+__device__ __forceinline__ uint32_t wave_incl_u32(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr + 1, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr + 2, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr + 4, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr + 8, 0xF, 0xF, false);
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+  const uint32_t r01 = r0 + (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t r012 = r01 + (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+  const int wrow = lane_id() >> 4;
+  return wrow == 0 ? v : v + (wrow == 1 ? r0 : wrow == 2 ? r01 : r012);
+}
+
 // The exclusive prefix over the wave's lanes of a count n in [0, 2^B), and the wave's total in `total`: a ballot per
 // bit of n.
 template <int B>
@@ -172,12 +188,7 @@ __device__ int narrow(S& s, const Each& each, u64& lo, u64& hi, int& r, int& abo
   __syncthreads();
   // thread t holds bin 255 - t: the inclusive count of the bins at or above it
   const unsigned mine = s.hist[kBins - 1 - t];
-  unsigned incl = mine;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const unsigned o = __shfl_up(incl, d, kWave);
-    if (lane_id() >= d) incl += o;
-  }
+  unsigned incl = wave_incl_u32(mine);
   if (lane_id() == kWave - 1) s.wsum[wave_id()] = incl;
   __syncthreads();
   for (int w = 0; w < wave_id(); ++w) incl += s.wsum[w];
@@ -884,8 +895,27 @@ struct Tile {
     if (total == 0) return;
     int base = 0;
     if (lane_id() == 0) base = atomicAdd(&s.count, total);
-    int pos = __builtin_amdgcn_readfirstlane(base) + excl;
+    base = __builtin_amdgcn_readfirstlane(base);
     constexpr int kCap = (int)(sizeof(s.buf) / sizeof(u64));
+    if (base + total <= kCap) {
+      // every element of the wave fits: no bound check per element. Over a non-negative threshold every admitted
+      // element is non-negative, and its key is its bits with the top bit set.
+      u64* at = s.buf + base + excl;
+      uint32_t nl = ~(uint32_t)lane0;  // ~(lane0 + off) = nl - off: one add per element
+      asm volatile("" : "+v"(nl));
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int j = 0; j < W; ++j)
+          if (admits<NEG>(v, j, t)) {
+            const uint32_t u = bits(v, j);
+            const uint32_t key = NEG ? key_of(u) : (u | 0x80000000u);
+            *at = ((u64)key << 32) | (u64)(nl - (uint32_t)(v * NT * W + j));
+            ++at;
+          }
+      return;
+    }
+    int pos = base + excl;
 #pragma unroll
     for (int v = 0; v < NV; ++v)
 #pragma unroll
@@ -1002,7 +1032,6 @@ __device__ __forceinline__ void merge_lists(TileSmem& s, BlockRed& red, TileList
 // ---- sampling from the top k ---------------------------------------------------------------------------------------
 
 constexpr int kSamplePer = kMaxK / kWave;  // list entries per lane (k <= 1024)
-constexpr int kDppRowShr = 0x110;          // + n: row_shr:n, lane l reads lane l - n of its 16-lane row (0 below it)
 
 __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), lane));
@@ -1365,12 +1394,7 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
     own[i + 1] = w >> 16;
     sum += own[i] + own[i + 1];
   }
-  unsigned incl = sum;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const unsigned o = __shfl_up(incl, d, kWave);
-    if (lane_id() >= d) incl += o;
-  }
+  const unsigned incl = wave_incl_u32(sum);
   if (lane_id() == kWave - 1) s.wsum[wave_id()] = incl;
   __syncthreads();
   unsigned run = incl - sum;
@@ -1427,95 +1451,131 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   }
 }
 
-// Keeps exactly the k largest of the m candidates s.buf[0, m) (k < m <= kWideList) and raises s.thr to the k-th: one
-// pass of bucket counts, (max - c) >> sh into kRankBuckets 16-bit LDS counters as write_ranked does, and a scan find
-// the bucket holding the k-th; its members (about m / kRankBuckets on spread-out values) are gathered and ranked among
-// themselves. A bucket of more than kThreads members (values clustered far below an outlier) takes the general prune
-// (histogram narrowing). Every thread calls it; the block is synchronized on return.
+// Writes the k largest of a chunk's m candidates s.buf[0, m) (k < m <= kWideList) to list[0, k) with device-coherent
+// stores, in no particular order, and returns the k-th largest (block-uniform): the candidates stay in registers from
+// one read. Their keys are counted in kRankBuckets 16-bit LDS counters, bucket (max key - key) >> sh with sh set so
+// that the keys' range fills them; a scan finds the bucket B holding the k-th; B's members (about m / kRankBuckets on
+// spread-out values) are gathered and ranked among themselves for the k-th; each thread then stores its candidates
+// above B and B's members at or above the k-th at positions from a block scan of the kept counts. A bucket of more
+// than kThreads members (values clustered far below an outlier) takes the general prune (histogram narrowing) and
+// stores the buffer. Every thread calls it; the block is synchronized on entry (the caller's) and on return.
 template <typename S>
-__device__ void prune_bucketed(S& s, int m, int k) {
+__device__ u64 cut_publish(S& s, int m, int k, u64* list) {
   constexpr int P = kWideList / kThreads;
-  constexpr int BPT = kRankBuckets / kThreads;
-  const int t = (int)threadIdx.x;
-  __syncthreads();
+  constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan (BPT / 4 u64 words of counters)
+  static_assert(BPT % 4 == 0 && kWideList < 65536, "counts fit 16 bits");
+  const int t = (int)threadIdx.x, lane = lane_id(), wave = wave_id();
+  unsigned* cnt2 = reinterpret_cast<unsigned*>(s.buf + kWideList);  // bucket b: half b & 1 of word b >> 1
+  u64* members = s.buf + kWideList + kRankBuckets / 4;                // after the counters (kRankBuckets * 2 bytes)
+  u64* own = reinterpret_cast<u64*>(cnt2) + t * (BPT / 4);
+#pragma unroll
+  for (int i = 0; i < BPT / 4; ++i) own[i] = 0ull;  // past the candidates (m <= kWideList)
+  if (t == 0) s.members = 0;
   u64 c[P];
-  u64 mx = 0, mn = ~0ull;
+  uint32_t kmx = 0, kmn = 0xffffffffu;
 #pragma unroll
   for (int r = 0; r < P; ++r) {
     const int i = r * kThreads + t;
     c[r] = i < m ? s.buf[i] : 0ull;
+    const uint32_t key = (uint32_t)(c[r] >> 32);
     if (i < m) {
-      mx = c[r] > mx ? c[r] : mx;
-      mn = c[r] < mn ? c[r] : mn;
+      kmx = key > kmx ? key : kmx;
+      kmn = key < kmn ? key : kmn;
     }
   }
-  mx = block_ext64<true>(mx, s);
-  mn = block_ext64<false>(mn, s);
-  const u64 range = mx - mn;
-  const int bits = range ? 64 - __clzll(range) : 0;
-  const int sh = bits > 12 ? bits - 12 : 0;  // (mx - mn) >> sh < kRankBuckets
-  unsigned* cnt2 = reinterpret_cast<unsigned*>(s.buf + kWideList);  // bucket b: half b & 1 of word b >> 1
-  u64* members = s.buf + kWideList + kRankBuckets / 4;                // after the counters (kRankBuckets * 2 bytes)
-  for (int w = t; w < kRankBuckets / 2; w += kThreads) cnt2[w] = 0;
-  if (t == 0) s.members = 0;
+  kmx = wave_ext32<true>(kmx);
+  kmn = wave_ext32<false>(kmn);
+  if (lane == 0) s.red[wave] = ((u64)kmx << 32) | kmn;
   __syncthreads();
+  kmx = 0;
+  kmn = 0xffffffffu;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const u64 e = s.red[w];
+    kmx = (uint32_t)(e >> 32) > kmx ? (uint32_t)(e >> 32) : kmx;
+    kmn = (uint32_t)e < kmn ? (uint32_t)e : kmn;
+  }
+  const uint32_t D = kmx - kmn;
+  const int sh = (D >> 12) ? (32 - __builtin_clz(D)) - 12 : 0;  // D >> sh < kRankBuckets
   int bk[P];
 #pragma unroll
   for (int r = 0; r < P; ++r) {
-    const u64 d = (mx - c[r]) >> sh;
-    bk[r] = d < (u64)kRankBuckets ? (int)d : kRankBuckets - 1;
-    if (r * kThreads + t < m) atomicAdd(&cnt2[bk[r] >> 1], 1u << (16 * (bk[r] & 1)));
+    bk[r] = r * kThreads + t < m ? (int)((kmx - (uint32_t)(c[r] >> 32)) >> sh) : kRankBuckets;
+    if (bk[r] < kRankBuckets) atomicAdd(&cnt2[bk[r] >> 1], 1u << (16 * (bk[r] & 1)));
   }
   __syncthreads();
   // the bucket holding position k - 1 (bucket 0 holds the largest candidates)
-  unsigned own[BPT], sum = 0;
+  unsigned cn[BPT], sum = 0;
 #pragma unroll
-  for (int i = 0; i < BPT; i += 2) {
-    const unsigned w = cnt2[(t * BPT + i) >> 1];
-    own[i] = w & 0xffffu;
-    own[i + 1] = w >> 16;
-    sum += own[i] + own[i + 1];
+  for (int i = 0; i < BPT / 4; ++i) {
+    const u64 w = own[i];
+    cn[4 * i] = (unsigned)w & 0xffffu;
+    cn[4 * i + 1] = (unsigned)w >> 16;
+    cn[4 * i + 2] = (unsigned)(w >> 32) & 0xffffu;
+    cn[4 * i + 3] = (unsigned)(w >> 48);
   }
-  unsigned incl = sum;
 #pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const unsigned o = __shfl_up(incl, d, kWave);
-    if (lane_id() >= d) incl += o;
-  }
-  if (lane_id() == kWave - 1) s.wsum[wave_id()] = incl;
+  for (int i = 0; i < BPT; ++i) sum += cn[i];
+  const unsigned incl = wave_incl_u32(sum);
+  if (lane == kWave - 1) s.wsum[wave] = incl;
   __syncthreads();
   unsigned run = incl - sum;
-  for (int w = 0; w < wave_id(); ++w) run += s.wsum[w];
 #pragma unroll
-  for (int i = 0; i < BPT; ++i) {
-    if (run < (unsigned)k && (unsigned)k <= run + own[i]) {
-      s.bin = t * BPT + i;
-      s.above = (int)run;
-      s.hist[0] = own[i];
+  for (int w = 0; w < kWaves; ++w) run += w < wave ? s.wsum[w] : 0u;
+  if (run < (unsigned)k && (unsigned)k <= run + sum) {
+    // the last bucket whose count from the top before it is short of k (no register array indexed at run time)
+    unsigned acc = run, before = run, here = 0;
+    int at = 0;
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const bool short_of_k = acc < (unsigned)k;
+      at = short_of_k ? i : at;
+      before = short_of_k ? acc : before;
+      here = short_of_k ? cn[i] : here;
+      acc += cn[i];
     }
-    run += own[i];
+    s.bin = t * BPT + at;
+    s.above = (int)before;
+    s.hist[0] = here;
   }
   __syncthreads();
-  const int B = s.bin, r = k - s.above, pop = (int)s.hist[0];  // the k-th is the r-th largest of bucket B's pop
+  const int B = s.bin, rb = k - s.above, pop = (int)s.hist[0];  // the k-th is the rb-th largest of bucket B's pop
   if (pop > kThreads) {
     prune(s, k);
-    return;
+    for (int i = t; i < k; i += kThreads)
+      __hip_atomic_store(list + i, s.buf[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return s.thr;
   }
 #pragma unroll
   for (int i = 0; i < P; ++i)
-    if (i * kThreads + t < m && bk[i] == B) members[atomicAdd(&s.members, 1)] = c[i];
+    if (bk[i] == B) members[atomicAdd(&s.members, 1)] = c[i];
   __syncthreads();
   if (t < pop) {
-    const u64 mine = members[t];
+    const u64 mem = members[t];
     int above = 0;
-    for (int j = 0; j < pop; ++j) above += members[j] > mine;
-    if (above == r - 1) s.pick = mine;
+    for (int j = 0; j < pop; ++j) above += members[j] > mem;
+    if (above == rb - 1) s.pick = mem;
   }
   __syncthreads();
   const u64 kth = s.pick;
-  keep_at_least(s, m, kth);
-  if (t == 0 && kth > s.thr) s.thr = kth;
+  // positions: a block scan of the kept counts (exactly k kept)
+  bool keep[P];
+  unsigned nk = 0;
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    keep[i] = bk[i] < B || (bk[i] == B && c[i] >= kth);
+    nk += keep[i] ? 1u : 0u;
+  }
+  const unsigned kincl = wave_incl_u32(nk);
+  if (lane == kWave - 1) s.wsum[wave] = kincl;
   __syncthreads();
+  unsigned pos = kincl - nk;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) pos += w < wave ? s.wsum[w] : 0u;
+#pragma unroll
+  for (int i = 0; i < P; ++i)
+    if (keep[i]) __hip_atomic_store(list + pos++, c[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return kth;
 }
 
 // A lower bound of the k-th largest of the wave's values v[i] (N per lane; 0 marks no value and is never counted) with
@@ -1559,6 +1619,87 @@ __device__ __forceinline__ uint32_t wave_kth_multi(const uint32_t (&v)[N], int k
   return p;
 }
 
+constexpr uint32_t kBoundWindow = (1u << 24) - 1u;  // two binades of fp32 keys below the largest, less one
+
+// The block's k- and q-bounds of a tile from its group maxima g (0: no group): the k-th (q-th) largest of the block's
+// group maxima has k (q) distinct elements at or above it. They are counted in kRankBuckets buckets (16-bit LDS
+// counters, two to a word) over the window [M - kBoundWindow, M] below the largest, M: bucket (M - g) >> sh, sh set
+// so that the window fits. Where the count from the top first reaches k (q), bucket b, the bound is that bucket's
+// lower edge M - ((b + 1) << sh) + 1 (1 if that is not positive): every group maximum of buckets 0..b is at or above
+// it, and it lies within 2^sh of the k-th (q-th) largest. One count per group instead of a ballot per group and
+// candidate bit. Returns false, with no bounds, when fewer than k group maxima lie in the window (group maxima spread
+// over more than two binades; the caller then searches each wave's whole range). q = 0 asks for no q-bound (bq = 0).
+// Uses the last kRankBuckets / 4 entries of s.buf (the buffer holds at most kWideCap - kWideList candidates between
+// tiles). Every thread calls it; the result is block-uniform.
+template <typename S>
+__device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t (&g)[kWideGroups], int k, int q, uint32_t& bk,
+                            uint32_t& bq) {
+  constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan (BPT / 4 u64 words of counters)
+  static_assert(kRankBuckets / 4 <= kWideList && BPT % 4 == 0 && kThreads * kWideGroups < 65536,
+                "the counters lie past the candidates kept between tiles; counts fit 16 bits");
+  unsigned* cnt2 = reinterpret_cast<unsigned*>(s.buf + kWideCap - kRankBuckets / 4);  // bucket b: half b & 1 of word b >> 1
+  const int t = (int)threadIdx.x;
+  u64* mine = reinterpret_cast<u64*>(cnt2) + t * (BPT / 4);
+#pragma unroll
+  for (int i = 0; i < BPT / 4; ++i) mine[i] = 0ull;
+  uint32_t mx = 0;
+#pragma unroll
+  for (int i = 0; i < kWideGroups; ++i) mx = g[i] > mx ? g[i] : mx;
+  const uint32_t M = red.max(wave_ext32<true>(mx));  // its barrier also orders the zeroing before the counts
+  if (M == 0) return false;
+  const uint32_t lo = M > kBoundWindow ? M - kBoundWindow : 1u;
+  const uint32_t D = M - lo;
+  const int sh = (D >> 12) ? (32 - __builtin_clz(D)) - 12 : 0;  // D >> sh < 4096 = kRankBuckets
+#pragma unroll
+  for (int i = 0; i < kWideGroups; ++i) {
+    if (g[i] >= lo) {
+      const uint32_t b = (M - g[i]) >> sh;
+      atomicAdd(&cnt2[b >> 1], 1u << (16 * (b & 1)));
+    }
+  }
+  __syncthreads();
+  // (the tile's registers are live here: the counts stay packed, four to a u64, and are unpacked where used)
+  u64 w4[BPT / 4];
+  uint32_t sum = 0;
+#pragma unroll
+  for (int i = 0; i < BPT / 4; ++i) {
+    w4[i] = mine[i];
+    const uint32_t lo = (uint32_t)w4[i], hi = (uint32_t)(w4[i] >> 32);
+    sum += (lo & 0xffffu) + (lo >> 16) + (hi & 0xffffu) + (hi >> 16);
+  }
+  const uint32_t incl = wave_incl_u32(sum);
+  if (lane_id() == kWave - 1) s.wsum[wave_id()] = incl;
+  __syncthreads();
+  uint32_t run = incl - sum, total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const uint32_t v = s.wsum[w];
+    run += w < wave_id() ? v : 0u;
+    total += v;
+  }
+  if (total < (uint32_t)k) return false;
+  // the thread whose buckets hold the k-th (q-th) from the top records the bucket: the last one whose count from the
+  // top before it is short of k (q)
+  uint32_t acc = run;
+  int atk = 0, atq = 0;
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    atk = acc < (uint32_t)k ? i : atk;
+    atq = acc < (uint32_t)q ? i : atq;
+    acc += (uint32_t)(w4[i >> 2] >> (16 * (i & 3))) & 0xffffu;
+  }
+  if (run < (uint32_t)k && (uint32_t)k <= run + sum) s.hist[0] = (unsigned)(t * BPT + atk);
+  if (run < (uint32_t)q && (uint32_t)q <= run + sum) s.hist[1] = (unsigned)(t * BPT + atq);
+  __syncthreads();
+  auto edge = [&](unsigned b) {
+    const u64 below = (u64)(b + 1) << sh;
+    return below >= (u64)M ? 1u : M - (uint32_t)below + 1u;
+  };
+  bk = edge(s.hist[0]);
+  bq = q > 0 ? edge(s.hist[1]) : 0u;
+  return true;
+}
+
 // 64 < k <= 1024: one 256-thread workgroup per (chunk, row), the chunk in register tiles as topk_tile. Per tile: each
 // lane's 64 elements form kWideGroups groups; a group's largest element has the group behind it, so each wave's ceil(k
 // / 4)-th largest group maximum has that many distinct elements at or above it and the smallest of the four waves' has
@@ -1575,7 +1716,7 @@ __device__ __forceinline__ uint32_t wave_kth_multi(const uint32_t (&v)[N], int k
 // row's k-th from below; the lists' entries at or above that floor (about k * 1.4) are gathered, ranked and the first
 // k written out, and the counter is zeroed for the next launch.
 template <typename T, bool VEC>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPRs, four workgroups per CU
     topk_wide(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
               u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
               int k, SampleArgs sa) {
@@ -1609,15 +1750,17 @@ __global__ void __launch_bounds__(kThreads)
     tile.group_keys(g);
     TOPK_STAGE(1);
     TOPK_WAVE_STAGE();
-    const uint32_t tw = wave_kth_multi<kWideGroups>(g, kw, 0u);
-    const uint32_t tb = red.min(tw);
-    thr = tb > thr ? tb : thr;
-    if (nchunks > 1) {
+    uint32_t tb, qb;
+    if (!hist_bounds(s, red, g, k, nchunks > 1 ? q : 0, tb, qb)) {
+      // the group maxima spread over more than the window: each wave's bound from a search over its whole range
+      const uint32_t tw = wave_kth_multi<kWideGroups>(g, kw, 0u);
+      tb = red.min(tw);
       // q <= k, so the wave's q-th largest group maximum is at or above its k-bound: the search starts there (the
       // groups' smallest maximum is often negative, and 12 bits over that range resolve the bound to about 0.5)
-      const uint32_t qb = red.min(wave_kth_multi<kWideGroups>(g, kwq, tw));
-      thq = qb > thq ? qb : thq;
+      qb = nchunks > 1 ? red.min(wave_kth_multi<kWideGroups>(g, kwq, tw)) : 0u;
     }
+    thr = tb > thr ? tb : thr;
+    thq = qb > thq ? qb : thq;
     TOPK_STAGE(2);
     tile.opaque();
     bool redo = true;
@@ -1653,19 +1796,23 @@ __global__ void __launch_bounds__(kThreads)
     return;
   }
   TOPK_STAGE(3);
-  // the chunk's k largest (its k-th raises s.thr)
-  if (s.count > kWideList) prune(s, k);
-  else if (s.count > k) prune_bucketed(s, s.count, k);
-  const int n = s.count;
-  // publish: the list, zero-padded to k, and the header (k-bound key << 32 | q-bound key) in the row's output
+  // publish: the chunk's k largest (the list, zero-padded to k when it holds fewer) and the header (k-bound key << 32 |
+  // q-bound key) in the row's output
   u64* wr = work + row * (long long)nchunks * k;
   u64* mine = wr + (long long)part * k;
-  for (int i = threadIdx.x; i < k; i += kThreads)
-    __hip_atomic_store(mine + i, i < n ? s.buf[i] : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (s.count > kWideList) prune(s, k);
+  const int n = s.count;
+  u64 kth = s.thr;
+  if (n > k) {
+    kth = cut_publish(s, n, k, mine);
+  } else {
+    for (int i = threadIdx.x; i < k; i += kThreads)
+      __hip_atomic_store(mine + i, i < n ? s.buf[i] : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   TOPK_STAGE(4);
   u64* heads = reinterpret_cast<u64*>(indices + row * k);
   if (threadIdx.x == 0) {
-    const uint32_t kb = (uint32_t)(s.thr >> 32) > thr ? (uint32_t)(s.thr >> 32) : thr;
+    const uint32_t kb = (uint32_t)(kth >> 32) > thr ? (uint32_t)(kth >> 32) : thr;
     __hip_atomic_store(heads + part, ((u64)kb << 32) | thq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   const bool last = block_hand_off(s, counters + row, nchunks);

@@ -10,7 +10,8 @@
 //   dtype 0 fp32, 1 bf16; ks comma-separated; chunk 0 takes plan()'s (min_chunk max 16k for k > 64, as the
 //   wrapper); reps launches per k on the same buffers; shuffle_seed >= 0 shuffles the workgroup order and each
 //   round of the lane schedule; pattern: randn (N(0, 2)), ints (0..5: ties), ascending, descending, negative (all
-//   values below -1), allones (rows of the all-ones NaN with a few real values).
+//   values below -1), allones (rows of the all-ones NaN with a few real values), outlier (randn and one value of 1e30
+//   per row), binades (randn scaled over 24 binades).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -78,6 +79,8 @@ int main(int argc, char** argv) {
     else if (pattern == "descending") f = (float)(cols - c);
     else if (pattern == "negative") f = -1.0f - std::fabs(f);
     else if (pattern == "allones") ones = r % 3 == 0 ? c % 7 == 0 : r % 3 == 1 ? c != 5 : c < cols - 10;
+    else if (pattern == "outlier") f = c == (r * 7919) % cols ? 1e30f : f;  // one value far above the rest
+    else if (pattern == "binades") f = std::ldexp(f, (int)(c % 24) - 12);  // magnitudes over 24 binades
     else if (pattern != "randn") {
       std::fprintf(stderr, "unknown pattern %s\n", pattern.c_str());
       return 2;

@@ -56,6 +56,11 @@ CASES = [
     # it gathers
     ("wide_six_lists", 2, 6 * 16384, 0, "1024", 16384, 2048, 1, 18, -1, "randn"),
     ("wide_six_lists_ties", 2, 6 * 16384, 0, "1024", 16384, 2048, 1, 19, -1, "ints"),
+    # the wide bounds' count window (two binades below the largest group maximum): one outlier leaves fewer than k
+    # group maxima in it (the whole-range search); magnitudes over 24 binades leave it sparse
+    ("wide_outlier", 2, 3 * 16384 + 500, 0, "65,300,1024", 16384, 2048, 1, 20, -1, "outlier"),
+    ("wide_binades", 2, 3 * 16384 + 500, 1, "65,300,1024", 16384, 2048, 1, 21, -1, "binades"),
+    ("wide_binades_fp32", 2, 40000, 0, "65,1024", 40000, 2048, 1, 22, -1, "binades"),
 ]
 
 
@@ -127,7 +132,7 @@ def test_weak_mode_exposes_a_missing_wait(emu_topk, concurrent):
 # barriers with the others' other barriers): rows with ties, monotone and all-ones NaN rows take the prune-heavy paths
 # (the k > 64 tile's re-append loop, the merge's pruning gather).
 AHEAD = ["ties", "ascending", "descending", "negative", "all_ones_nan", "all_ones_nan_bf16", "shuffled_bf16",
-         "split_fp32"]
+         "split_fp32", "wide_outlier", "wide_binades"]
 
 
 @pytest.mark.parametrize("name", AHEAD)
