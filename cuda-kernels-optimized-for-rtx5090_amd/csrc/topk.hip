@@ -40,6 +40,8 @@ struct Smem {
   unsigned hist[kBins];
   unsigned wsum[kWaves];
   u64 red[kWaves];
+  u64 red2[kWaves];  // reductions of two values at one barrier (with red), and of a second pair (with wsum)
+  u64 red3[kWaves];
   u64 thr;       // admit composites >= thr (>= 1: composite 0 is never admitted)
   int count;     // composites in buf
   int bin;       // narrowing: the bin holding the wanted rank
@@ -1344,10 +1346,12 @@ constexpr int kRankBuckets = 4096;  // buckets of write_ranked (16-bit counters 
 // its bucket's members above it. Nearly linear on spread-out values; a bucket holding many candidates (values
 // clustered far below an outlier) costs its size per member. `lo`, when not 0, is a lower bound of the candidates known
 // to the caller, used in place of their minimum (a candidate below it would still be ordered exactly: it lands in the
-// last bucket, below every other bucket's members). Every thread calls it.
+// last bucket, below every other bucket's members). `hi`, when not 0 (with lo not 0), is the largest candidate, known
+// to the caller; the block is then not reduced here, and the caller's barrier after its writes of s.buf suffices.
+// Every thread calls it.
 template <typename T, typename S>
 __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, long long* indices, long long row,
-                                             u64 lo) {
+                                             u64 lo, u64 hi = 0) {
   constexpr int P = kWideList / kThreads;
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan
   static_assert(kWideList * 2 <= kWideCap && kRankBuckets * 2 * sizeof(uint16_t) <= kWideList * sizeof(u64) &&
@@ -1365,8 +1369,13 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
       mn = c[r] < mn ? c[r] : mn;
     }
   }
-  mx = block_ext64<true>(mx, s);  // also orders every read of s.buf above before the writes below
-  mn = lo ? lo : block_ext64<false>(mn, s);
+  if (hi && lo) {  // the reads above need no barrier before the writes below: the counters lie past s.buf[0, m), and
+    mx = hi;        // the scatter into s.buf[0, m) comes after the barriers of the counts
+    mn = lo;
+  } else {
+    mx = block_ext64<true>(mx, s);  // also orders every read of s.buf above before the writes below
+    mn = lo ? lo : block_ext64<false>(mn, s);
+  }
   const u64 range = mx - mn;
   const int bits = range ? 64 - __clzll(range) : 0;
   const int sh = bits > 12 ? bits - 12 : 0;  // (mx - mn) >> sh < 4096 = kRankBuckets
@@ -1452,15 +1461,18 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
 }
 
 // Writes the k largest of a chunk's m candidates s.buf[0, m) (k < m <= kWideList) to list[0, k) with device-coherent
-// stores, in no particular order, and returns the k-th largest (block-uniform): the candidates stay in registers from
-// one read. Their keys are counted in kRankBuckets 16-bit LDS counters, bucket (max key - key) >> sh with sh set so
-// that the keys' range fills them; a scan finds the bucket B holding the k-th; B's members (about m / kRankBuckets on
-// spread-out values) are gathered and ranked among themselves for the k-th; each thread then stores its candidates
-// above B and B's members at or above the k-th at positions from a block scan of the kept counts. A bucket of more
-// than kThreads members (values clustered far below an outlier) takes the general prune (histogram narrowing) and
-// stores the buffer. Every thread calls it; the block is synchronized on entry (the caller's) and on return.
+// stores, in no particular order, and returns (a lower bound of) the k-th largest, block-uniform: the candidates stay
+// in registers from one read. Their keys are counted in kRankBuckets 16-bit LDS counters, bucket (hi - key) >> sh,
+// with [lo, hi] the caller's range of the keys (hi the chunk's largest, lo its admission key; a candidate below lo,
+// kept from an earlier tile, counts in the last bucket) and sh set so that it fills them. A scan finds the bucket B
+// holding the k-th. When B is kept whole (the usual case: about m / kRankBuckets members), everything in buckets up to
+// B is kept and B's lower edge is returned; otherwise B's members are gathered and ranked among themselves for the
+// k-th. Each thread stores its kept candidates at positions from a block scan of the kept counts. A bucket of more than
+// kThreads members (values clustered far below an outlier) takes the general prune (histogram narrowing) and stores the
+// buffer. `zeroed`: the caller has zeroed the counters (s.buf[kWideList, kWideList + kRankBuckets / 4)) and s.members
+// behind a barrier. Every thread calls it; the block is synchronized on entry (the caller's) and on return.
 template <typename S>
-__device__ u64 cut_publish(S& s, int m, int k, u64* list) {
+__device__ u64 cut_publish(S& s, int m, int k, u64* list, uint32_t lo, uint32_t hi, bool zeroed) {
   constexpr int P = kWideList / kThreads;
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan (BPT / 4 u64 words of counters)
   static_assert(BPT % 4 == 0 && kWideList < 65536, "counts fit 16 bits");
@@ -1468,39 +1480,23 @@ __device__ u64 cut_publish(S& s, int m, int k, u64* list) {
   unsigned* cnt2 = reinterpret_cast<unsigned*>(s.buf + kWideList);  // bucket b: half b & 1 of word b >> 1
   u64* members = s.buf + kWideList + kRankBuckets / 4;                // after the counters (kRankBuckets * 2 bytes)
   u64* own = reinterpret_cast<u64*>(cnt2) + t * (BPT / 4);
+  if (!zeroed) {
 #pragma unroll
-  for (int i = 0; i < BPT / 4; ++i) own[i] = 0ull;  // past the candidates (m <= kWideList)
-  if (t == 0) s.members = 0;
+    for (int i = 0; i < BPT / 4; ++i) own[i] = 0ull;  // past the candidates (m <= kWideList)
+    if (t == 0) s.members = 0;
+    __syncthreads();
+  }
+  lo = lo < hi ? lo : hi;
+  const uint32_t D = hi - lo;
+  const int sh = (D >> 12) ? (32 - __builtin_clz(D)) - 12 : 0;  // D >> sh < kRankBuckets
   u64 c[P];
-  uint32_t kmx = 0, kmn = 0xffffffffu;
+  int bk[P];
 #pragma unroll
   for (int r = 0; r < P; ++r) {
     const int i = r * kThreads + t;
     c[r] = i < m ? s.buf[i] : 0ull;
-    const uint32_t key = (uint32_t)(c[r] >> 32);
-    if (i < m) {
-      kmx = key > kmx ? key : kmx;
-      kmn = key < kmn ? key : kmn;
-    }
-  }
-  kmx = wave_ext32<true>(kmx);
-  kmn = wave_ext32<false>(kmn);
-  if (lane == 0) s.red[wave] = ((u64)kmx << 32) | kmn;
-  __syncthreads();
-  kmx = 0;
-  kmn = 0xffffffffu;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const u64 e = s.red[w];
-    kmx = (uint32_t)(e >> 32) > kmx ? (uint32_t)(e >> 32) : kmx;
-    kmn = (uint32_t)e < kmn ? (uint32_t)e : kmn;
-  }
-  const uint32_t D = kmx - kmn;
-  const int sh = (D >> 12) ? (32 - __builtin_clz(D)) - 12 : 0;  // D >> sh < kRankBuckets
-  int bk[P];
-#pragma unroll
-  for (int r = 0; r < P; ++r) {
-    bk[r] = r * kThreads + t < m ? (int)((kmx - (uint32_t)(c[r] >> 32)) >> sh) : kRankBuckets;
+    const uint32_t d = (hi - (uint32_t)(c[r] >> 32)) >> sh;
+    bk[r] = i < m ? (d < (uint32_t)kRankBuckets ? (int)d : kRankBuckets - 1) : kRankBuckets;
     if (bk[r] < kRankBuckets) atomicAdd(&cnt2[bk[r] >> 1], 1u << (16 * (bk[r] & 1)));
   }
   __syncthreads();
@@ -1540,30 +1536,37 @@ __device__ u64 cut_publish(S& s, int m, int k, u64* list) {
   }
   __syncthreads();
   const int B = s.bin, rb = k - s.above, pop = (int)s.hist[0];  // the k-th is the rb-th largest of bucket B's pop
-  if (pop > kThreads) {
-    prune(s, k);
-    for (int i = t; i < k; i += kThreads)
-      __hip_atomic_store(list + i, s.buf[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return s.thr;
-  }
+  u64 kth, least;  // the returned bound; the smallest composite kept from bucket B
+  if (rb == pop && B < kRankBuckets - 1) {  // B kept whole: its lower edge bounds the k-th (B's members are above it)
+    const u64 below = (u64)(B + 1) << sh;
+    kth = (u64)(below >= (u64)hi ? 1u : hi - (uint32_t)below + 1u) << 32;
+    least = 0;
+  } else {
+    if (pop > kThreads) {
+      prune(s, k);
+      for (int i = t; i < k; i += kThreads)
+        __hip_atomic_store(list + i, s.buf[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return s.thr;
+    }
 #pragma unroll
-  for (int i = 0; i < P; ++i)
-    if (bk[i] == B) members[atomicAdd(&s.members, 1)] = c[i];
-  __syncthreads();
-  if (t < pop) {
-    const u64 mem = members[t];
-    int above = 0;
-    for (int j = 0; j < pop; ++j) above += members[j] > mem;
-    if (above == rb - 1) s.pick = mem;
+    for (int i = 0; i < P; ++i)
+      if (bk[i] == B) members[atomicAdd(&s.members, 1)] = c[i];
+    __syncthreads();
+    if (t < pop) {
+      const u64 mem = members[t];
+      int above = 0;
+      for (int j = 0; j < pop; ++j) above += members[j] > mem;
+      if (above == rb - 1) s.pick = mem;
+    }
+    __syncthreads();
+    kth = least = s.pick;
   }
-  __syncthreads();
-  const u64 kth = s.pick;
   // positions: a block scan of the kept counts (exactly k kept)
   bool keep[P];
   unsigned nk = 0;
 #pragma unroll
   for (int i = 0; i < P; ++i) {
-    keep[i] = bk[i] < B || (bk[i] == B && c[i] >= kth);
+    keep[i] = bk[i] < B || (bk[i] == B && c[i] >= least);
     nk += keep[i] ? 1u : 0u;
   }
   const unsigned kincl = wave_incl_u32(nk);
@@ -1630,10 +1633,11 @@ constexpr uint32_t kBoundWindow = (1u << 24) - 1u;  // two binades of fp32 keys 
 // candidate bit. Returns false, with no bounds, when fewer than k group maxima lie in the window (group maxima spread
 // over more than two binades; the caller then searches each wave's whole range). q = 0 asks for no q-bound (bq = 0).
 // Uses the last kRankBuckets / 4 entries of s.buf (the buffer holds at most kWideCap - kWideList candidates between
-// tiles). Every thread calls it; the result is block-uniform.
+// tiles). M is set to the largest group maximum (the tile's largest key) in every case. Every thread calls it; the
+// result is block-uniform.
 template <typename S>
-__device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t (&g)[kWideGroups], int k, int q, uint32_t& bk,
-                            uint32_t& bq) {
+__device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t (&g)[kWideGroups], int k, int q,
+                                            uint32_t& bk, uint32_t& bq, uint32_t& M) {
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan (BPT / 4 u64 words of counters)
   static_assert(kRankBuckets / 4 <= kWideList && BPT % 4 == 0 && kThreads * kWideGroups < 65536,
                 "the counters lie past the candidates kept between tiles; counts fit 16 bits");
@@ -1645,7 +1649,7 @@ __device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t 
   uint32_t mx = 0;
 #pragma unroll
   for (int i = 0; i < kWideGroups; ++i) mx = g[i] > mx ? g[i] : mx;
-  const uint32_t M = red.max(wave_ext32<true>(mx));  // its barrier also orders the zeroing before the counts
+  M = red.max(wave_ext32<true>(mx));  // its barrier also orders the zeroing before the counts
   if (M == 0) return false;
   const uint32_t lo = M > kBoundWindow ? M - kBoundWindow : 1u;
   const uint32_t D = M - lo;
@@ -1736,7 +1740,8 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   }
   __syncthreads();
   TOPK_STAGE(0);
-  uint32_t thr = 0, thq = 0;
+  uint32_t thr = 0, thq = 0, cmax = 0;  // the admission key, the q-bound, the chunk's largest key
+  bool cut_zeroed = false;
   const int q = (k + nchunks - 1) / nchunks;
   const int kw = (k + kWaves - 1) / kWaves, kwq = (q + kWaves - 1) / kWaves;
   using TL = Tile<T, VEC>;
@@ -1750,8 +1755,17 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     tile.group_keys(g);
     TOPK_STAGE(1);
     TOPK_WAVE_STAGE();
-    uint32_t tb, qb;
-    if (!hist_bounds(s, red, g, k, nchunks > 1 ? q : 0, tb, qb)) {
+    const bool last_tile = end - t0 <= TE;
+    if (last_tile && nchunks > 1) {
+      // the cut's counters, zeroed ahead of the bounds' barriers while no wave appends (the buffer holds at most
+      // kWideList candidates between tiles); kept zero unless this tile's appends pass kWideList
+      u64* cz = s.buf + kWideList + (int)threadIdx.x * (kRankBuckets / 4 / kThreads);
+#pragma unroll
+      for (int i = 0; i < kRankBuckets / 4 / kThreads; ++i) cz[i] = 0ull;
+      if (threadIdx.x == 0) s.members = 0;
+    }
+    uint32_t tb, qb, tm;
+    if (!hist_bounds(s, red, g, k, nchunks > 1 ? q : 0, tb, qb, tm)) {
       // the group maxima spread over more than the window: each wave's bound from a search over its whole range
       const uint32_t tw = wave_kth_multi<kWideGroups>(g, kw, 0u);
       tb = red.min(tw);
@@ -1761,6 +1775,7 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     }
     thr = tb > thr ? tb : thr;
     thq = qb > thq ? qb : thq;
+    cmax = tm > cmax ? tm : cmax;
     TOPK_STAGE(2);
     tile.opaque();
     bool redo = true;
@@ -1770,6 +1785,7 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
       __syncthreads();
       redo = s.count > kWideCap;
     }
+    cut_zeroed = last_tile && !redo && s.count <= kWideList;  // (the appends left the counters alone)
     if (redo) {  // every element may pass, or the buffer overflowed: append again vector by vector, pruning to k
       __syncthreads();
       if (threadIdx.x == 0) s.count = cnt0;
@@ -1804,7 +1820,7 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   const int n = s.count;
   u64 kth = s.thr;
   if (n > k) {
-    kth = cut_publish(s, n, k, mine);
+    kth = cut_publish(s, n, k, mine, thr, cmax, cut_zeroed);
   } else {
     for (int i = threadIdx.x; i < k; i += kThreads)
       __hip_atomic_store(mine + i, i < n ? s.buf[i] : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1821,23 +1837,87 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   const float u = sa.uniform(row);
   // merge (the row's last arrival): the floor from the headers, then every list's entries at or above it
   auto ld = [&](const u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  const int t = (int)threadIdx.x, lane = lane_id(), wave = wave_id();
+  // Rows whose lists fit the registers (C5: 8 x 1024 entries) read them all at once, before the headers: the floor's
+  // reduction runs while the loads are in flight, and one block scan places the entries at or above it.
+  constexpr int kGatherAll = 8192;  // list entries the merger reads in one batch
+  constexpr int PB = kGatherAll / kThreads;
+  const int entries = nchunks * k;  // the row's lists, contiguous in wr
+  u64 e[PB];
+  if (entries <= kGatherAll) {
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+      const int at = i * kThreads + t;
+      e[i] = at < entries ? ld(wr + at) : 0ull;
+    }
+  }
   u64 kmax = 0, qmn = ~0ull;
-  for (int c = threadIdx.x; c < nchunks; c += kThreads) {
+  for (int c = t; c < nchunks; c += kThreads) {
     const u64 h = ld(heads + c);
     const u64 kb = h & 0xffffffff00000000ull, qb = h << 32;
     kmax = kb > kmax ? kb : kmax;
     qmn = qb < qmn ? qb : qmn;
   }
-  kmax = block_ext64<true>(kmax, s);
-  qmn = block_ext64<false>(qmn, s);  // 0 when a chunk has no q-bound
+  kmax = wave_ext64<true>(kmax);
+  qmn = wave_ext64<false>(qmn);
+  if (lane == 0) {
+    s.red[wave] = kmax;
+    s.red2[wave] = qmn;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    kmax = s.red[w] > kmax ? s.red[w] : kmax;
+    qmn = s.red2[w] < qmn ? s.red2[w] : qmn;  // 0 when a chunk has no q-bound
+  }
   u64 floor = kmax > qmn ? kmax : qmn;
   floor = floor > 1 ? floor : 1;
-  if (threadIdx.x == 0) {
+  TOPK_STAGE(6);
+  if (entries <= kGatherAll) {
+    unsigned n = 0;
+    u64 mx = 0;
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+      const bool keep = e[i] >= floor;
+      n += keep ? 1u : 0u;
+      mx = keep && e[i] > mx ? e[i] : mx;
+    }
+    const unsigned incl = wave_incl_u32(n);
+    mx = wave_ext64<true>(mx);
+    if (lane == kWave - 1) s.wsum[wave] = incl;
+    if (lane == 0) s.red3[wave] = mx;
+    __syncthreads();
+    unsigned m = 0, pos = incl - n;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      m += s.wsum[w];
+      pos += w < wave ? s.wsum[w] : 0u;
+      mx = s.red3[w] > mx ? s.red3[w] : mx;
+    }
+    if (m <= (unsigned)kWideCap) {  // (block-uniform) all of them fit the buffer: one write, then the ordering
+#pragma unroll
+      for (int i = 0; i < PB; ++i)
+        if (e[i] >= floor) s.buf[pos++] = e[i];
+      if (t == 0) {
+        s.count = (int)m;
+        s.thr = floor;
+      }
+      __syncthreads();
+      TOPK_STAGE(7);
+      if (m > (unsigned)kWideList) prune(s, k);
+      write_ranked<T>(s, s.count, k, values, indices, row, floor, mx);
+      TOPK_STAGE(8);
+      if (t == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sample_list<T>(sa, u, values, indices, row, k);
+      return;
+    }
+  }
+  // longer rows (or more entries at the floor than the buffer holds): the lists in turn, pruning as they come
+  if (t == 0) {
     s.count = 0;
     s.thr = floor;
   }
   __syncthreads();
-  TOPK_STAGE(6);
   constexpr int PER = kMaxK / kThreads;  // list entries per thread (k <= kMaxK)
   constexpr int kInFlight = 2;           // lists whose loads are in flight while one is taken (4 measured no faster)
   static_assert(PER * kThreads <= kWideCap - kWideList, "room for a whole list above a buffer of kWideList");

@@ -56,6 +56,8 @@ CASES = [
     # it gathers
     ("wide_six_lists", 2, 6 * 16384, 0, "1024", 16384, 2048, 1, 18, -1, "randn"),
     ("wide_six_lists_ties", 2, 6 * 16384, 0, "1024", 16384, 2048, 1, 19, -1, "ints"),
+    # four lists of ties: every entry reaches the floor, more than the merge ranks at once but within its buffer
+    ("wide_four_lists_ties", 2, 4 * 16384, 1, "1024,700", 16384, 2048, 1, 23, -1, "ints"),
     # the wide bounds' count window (two binades below the largest group maximum): one outlier leaves fewer than k
     # group maxima in it (the whole-range search); magnitudes over 24 binades leave it sparse
     ("wide_outlier", 2, 3 * 16384 + 500, 0, "65,300,1024", 16384, 2048, 1, 20, -1, "outlier"),
