@@ -1348,10 +1348,11 @@ constexpr int kRankBuckets = 4096;  // buckets of write_ranked (16-bit counters 
 // to the caller, used in place of their minimum (a candidate below it would still be ordered exactly: it lands in the
 // last bucket, below every other bucket's members). `hi`, when not 0 (with lo not 0), is the largest candidate, known
 // to the caller; the block is then not reduced here, and the caller's barrier after its writes of s.buf suffices.
+// `zeroed`: the caller has zeroed the counters (s.buf[kWideList, kWideList + kRankBuckets / 4)) behind that barrier.
 // Every thread calls it.
 template <typename T, typename S>
 __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, long long* indices, long long row,
-                                             u64 lo, u64 hi = 0) {
+                                             u64 lo, u64 hi = 0, bool zeroed = false) {
   constexpr int P = kWideList / kThreads;
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan
   static_assert(kWideList * 2 <= kWideCap && kRankBuckets * 2 * sizeof(uint16_t) <= kWideList * sizeof(u64) &&
@@ -1383,8 +1384,10 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   unsigned* cnt2 = reinterpret_cast<unsigned*>(s.buf + kWideList);  // bucket b's count: half b & 1 of word b >> 1
   uint16_t* first = reinterpret_cast<uint16_t*>(cnt2 + kRankBuckets / 2);
   auto count_of = [&](int b) { return (int)((cnt2[b >> 1] >> (16 * (b & 1))) & 0xffffu); };
-  for (int w = t; w < kRankBuckets / 2; w += kThreads) cnt2[w] = 0;
-  __syncthreads();
+  if (!zeroed) {
+    for (int w = t; w < kRankBuckets / 2; w += kThreads) cnt2[w] = 0;
+    __syncthreads();
+  }
   int bk[P], slot[P];
 #pragma unroll
   for (int r = 0; r < P; ++r) {
@@ -1838,11 +1841,14 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   // merge (the row's last arrival): the floor from the headers, then every list's entries at or above it
   auto ld = [&](const u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   const int t = (int)threadIdx.x, lane = lane_id(), wave = wave_id();
-  // Rows whose lists fit the registers (C5: 8 x 1024 entries) read them all at once, before the headers: the floor's
-  // reduction runs while the loads are in flight, and one block scan places the entries at or above it.
+  // Rows whose lists fit the registers (C5: 8 x 1024 entries) read them all at once, right after the headers: the
+  // floor's reduction runs while the lists' loads are in flight (loads return in order), and one block scan places the
+  // entries at or above it.
   constexpr int kGatherAll = 8192;  // list entries the merger reads in one batch
   constexpr int PB = kGatherAll / kThreads;
   const int entries = nchunks * k;  // the row's lists, contiguous in wr
+  u64 kmax = 0, qmn = ~0ull;
+  u64 h0 = t < nchunks ? ld(heads + t) : 0ull;
   u64 e[PB];
   if (entries <= kGatherAll) {
 #pragma unroll
@@ -1851,9 +1857,8 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
       e[i] = at < entries ? ld(wr + at) : 0ull;
     }
   }
-  u64 kmax = 0, qmn = ~0ull;
   for (int c = t; c < nchunks; c += kThreads) {
-    const u64 h = ld(heads + c);
+    const u64 h = c == t ? h0 : ld(heads + c);
     const u64 kb = h & 0xffffffff00000000ull, qb = h << 32;
     kmax = kb > kmax ? kb : kmax;
     qmn = qb < qmn ? qb : qmn;
@@ -1886,6 +1891,10 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     mx = wave_ext64<true>(mx);
     if (lane == kWave - 1) s.wsum[wave] = incl;
     if (lane == 0) s.red3[wave] = mx;
+    // the ordering's counters, zeroed behind the barrier below (they stay zero unless more than kWideList are kept)
+    u64* cz = s.buf + kWideList + t * (kRankBuckets / 4 / kThreads);
+#pragma unroll
+    for (int i = 0; i < kRankBuckets / 4 / kThreads; ++i) cz[i] = 0ull;
     __syncthreads();
     unsigned m = 0, pos = incl - n;
 #pragma unroll
@@ -1905,7 +1914,7 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
       __syncthreads();
       TOPK_STAGE(7);
       if (m > (unsigned)kWideList) prune(s, k);
-      write_ranked<T>(s, s.count, k, values, indices, row, floor, mx);
+      write_ranked<T>(s, s.count, k, values, indices, row, floor, mx, m <= (unsigned)kWideList);
       TOPK_STAGE(8);
       if (t == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       sample_list<T>(sa, u, values, indices, row, k);
