@@ -1424,12 +1424,14 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   // Ranked in bucket order: lane i takes sorted[i], so neighbouring lanes read the same bucket's members (LDS
   // broadcasts rather than scattered reads) and write neighbouring output positions. Every position first, then the
   // stores. A thread's reads are issued together, stage by stage (its entries, their buckets' ranges, the buckets'
-  // first four members), with no branch between them: every index stays inside the buffer whether or not the entry
-  // exists (i < kWideList; f + 3 <= m + 3 < kWideCap), and a missing entry's position is discarded. Buckets of more
-  // than four members (rare) are finished after.
+  // first four members), with no branch between them but the block-uniform one that skips the entry slots r with
+  // r * kThreads >= m (C5 at k = 65 fills one of the eight): every index stays inside the buffer whether or not the
+  // entry exists (i < kWideList; f + 3 <= m + 3 < kWideCap), and a missing entry's position is discarded. Buckets of
+  // more than four members (rare) are finished after.
   int pos[P], f[P], n[P];
 #pragma unroll
   for (int r = 0; r < P; ++r) {
+    if (r * kThreads >= m) break;
     c[r] = sorted[r * kThreads + t];
     const u64 d = (mx - c[r]) >> sh;
     const int b = d < (u64)kRankBuckets ? (int)d : kRankBuckets - 1;
@@ -1438,11 +1440,13 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   }
 #pragma unroll
   for (int r = 0; r < P; ++r) {
+    if (r * kThreads >= m) break;
     const u64 a = sorted[f[r]], e1 = sorted[f[r] + 1], e2 = sorted[f[r] + 2], e3 = sorted[f[r] + 3];
     pos[r] = f[r] + (a > c[r]) + (1 < n[r] && e1 > c[r]) + (2 < n[r] && e2 > c[r]) + (3 < n[r] && e3 > c[r]);
   }
 #pragma unroll
   for (int r = 0; r < P; ++r) {
+    if (r * kThreads >= m) break;
     if (r * kThreads + t >= m) {
       pos[r] = k;
       continue;
@@ -1455,6 +1459,7 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   }
 #pragma unroll
   for (int r = 0; r < P; ++r) {
+    if (r * kThreads >= m) break;
     if (pos[r] < k) {
       if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + pos[r]] = composite_bits(c[r]);
       else static_cast<uint16_t*>(values)[row * k + pos[r]] = (uint16_t)(composite_bits(c[r]) >> 16);
