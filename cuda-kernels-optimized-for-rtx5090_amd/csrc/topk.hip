@@ -1569,23 +1569,33 @@ __device__ u64 cut_publish(S& s, int m, int k, u64* list, uint32_t lo, uint32_t 
     __syncthreads();
     kth = least = s.pick;
   }
-  // positions: a block scan of the kept counts (exactly k kept)
+  // positions (exactly k kept), slot-major: every thread's slot i before any slot i + 1, waves in order within a slot
+  // and lanes in order within a wave, so that one store instruction writes a contiguous run (coherent stores of
+  // scattered 8-byte entries each cost the memory a whole sector)
   bool keep[P];
-  unsigned nk = 0;
+  u64 km[P];
+  unsigned* per = s.hist + 64;  // [P][kWaves] kept counts (s.hist[0] holds pop, read above without a barrier since)
 #pragma unroll
   for (int i = 0; i < P; ++i) {
     keep[i] = bk[i] < B || (bk[i] == B && c[i] >= least);
-    nk += keep[i] ? 1u : 0u;
+    km[i] = __ballot(keep[i]);
+    if (lane == 0) per[i * kWaves + wave] = (unsigned)__popcll(km[i]);
   }
-  const unsigned kincl = wave_incl_u32(nk);
-  if (lane == kWave - 1) s.wsum[wave] = kincl;
   __syncthreads();
-  unsigned pos = kincl - nk;
+  unsigned base = 0;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) pos += w < wave ? s.wsum[w] : 0u;
+  for (int i = 0; i < P; ++i) {
+    unsigned before = 0, all = 0;
 #pragma unroll
-  for (int i = 0; i < P; ++i)
-    if (keep[i]) __hip_atomic_store(list + pos++, c[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int w = 0; w < kWaves; ++w) {
+      const unsigned v = per[i * kWaves + w];
+      before += w < wave ? v : 0u;
+      all += v;
+    }
+    if (keep[i])
+      __hip_atomic_store(list + base + before + lanes_below(km[i]), c[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    base += all;
+  }
   return kth;
 }
 
