@@ -453,8 +453,8 @@ TOPK_STAGES = {
     "topk_one": [(0, "start"), (1, "loads landed (wave 0)"), (2, "workgroup's best"), (3, "arrival counted"),
                  (8, "row written")],
     "topk_tile": [(0, "start"), (1, "loads landed (wave 0)"), (2, "threshold"), (3, "tile filtered and settled"),
-                  (4, "chunk list published"), (5, "arrival counted"), (6, "merge: heads floor"),
-                  (7, "merge: lists streamed and settled"), (8, "row written")],
+                  (4, "chunk list published"), (5, "arrival counted"), (6, "merge: floor, candidates counted"),
+                  (7, "merge: candidates compacted"), (8, "row written")],
     "topk_wide": [(0, "start"), (1, "loads landed (wave 0)"), (2, "bounds"), (3, "tile appended"), (4, "cut to k"),
                   (5, "arrival counted"), (6, "merge: floor from the headers"), (7, "merge: lists gathered"),
                   (8, "row written")],

@@ -975,6 +975,13 @@ struct Tile {
   }
 };
 
+// Orders one wave's LDS writes before its later LDS reads of other lanes' entries (a wave's LDS operations execute in
+// order; this keeps the compiler from moving them across).
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
+
 // k <= 64 merge of a split row (the row's last workgroup). Every chunk list holds its chunk's k largest, descending,
 // so the first h = ceil(k / nchunks) entries of the lists give nchunks * h >= k distinct composites: the k-th largest
 // of these heads bounds the row's k-th from below and, the row's top k being spread over the chunks, admits little
@@ -999,7 +1006,72 @@ __device__ __forceinline__ void merge_lists(TileSmem& s, BlockRed& red, TileList
   };
   load(0);  // in flight together with the heads
   u64 floor = 1;
-  if (nh <= kTileSort) {
+  if (nh <= kWave && total <= kThreads * PER) {
+    // Every wave finds the floor itself from its own copy of the heads, one per lane. No barrier: the waves agree.
+    // Up to 16 heads: the head ranked k-1 among them, ranked in the wave's list segment (unused until the streamed
+    // merge below) in one step of reads. More: a key with at least k heads at or above it (the wave's bitwise search,
+    // within 2^-kThrBits of the range below the k-th head's key), whose lowest composite is then at or below the
+    // row's k-th; a dozen ballots cost less than ranking 32 or more heads.
+    const int l = lane_id(), wave = wave_id();
+    const u64 hv = l < nh ? ld((l / h) * k + l % h) : 0ull;
+    if (__popcll(__ballot(hv != 0)) >= k) {
+      if (nh <= 16) {
+        u64* hs = s.seg[wave];
+        if (l < 16) hs[l] = hv;  // zero past nh: the padding rank_in reads
+        wave_lds_sync();
+        const u64 at = __ballot(hv != 0 && rank_in(hs, 16, hv) == k - 1);  // one lane: composites are distinct
+        floor = readlane64(hv, __builtin_ctzll(at));
+      } else {
+        const uint32_t p = wave_kth32((uint32_t)(hv >> 32), hv != 0, k);
+        floor = p ? (u64)p << 32 : 1ull;
+      }
+    }
+    // the entries at or above the floor, compacted into s.sorted by one exchange of the waves' counts
+    u64 m[PER];
+    int wn = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      m[i] = __ballot(c[i] >= floor);  // (c[i] is 0 past the lists' ends and in a short list's padding)
+      wn += __popcll(m[i]);
+    }
+    if (l == 0) s.cnt[wave] = wn;
+    __syncthreads();
+    TOPK_STAGE(6);
+    int pre = 0, n = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const int cw = s.cnt[w];
+      pre += w < wave ? cw : 0;
+      n += cw;
+    }
+    if (n <= kTileSort) {  // uniform over the block
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        if (c[i] >= floor) {
+          const int at = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m[i] >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m[i], (uint32_t)pre));
+          s.sorted[at] = c[i];
+        }
+        pre += __popcll(m[i]);
+      }
+      const int n16 = (n + 15) & ~15;
+      if (t >= n && t < n16) s.sorted[t] = 0ull;
+      __syncthreads();
+      TOPK_STAGE(7);
+      if (t < n) {
+        const u64 mine = s.sorted[t];
+        const int rank = rank_in(s.sorted, n16, mine);
+        if (rank < k) {
+          if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + rank] = composite_bits(mine);
+          else static_cast<uint16_t*>(values)[row * k + rank] = (uint16_t)(composite_bits(mine) >> 16);
+          indices[row * k + rank] = composite_index(mine);
+          s.top[rank] = mine;
+        }
+      }
+      return;
+    }
+    // more than a rank sort holds (ties, adversarial orders): the streamed merge below, from this floor
+  } else if (nh <= kTileSort) {
     const u64 hv = t < nh ? ld((t / h) * k + t % h) : 0ull;
     s.sorted[t] = hv;  // zero past nh: the padding rank_in reads
     const int real = (int)red.sum((uint32_t)__popcll(__ballot(hv != 0)));
@@ -1324,13 +1396,6 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // ---- wide kernel (64 < k <= 1024) ----------------------------------------------------------------------------------
-
-// Orders one wave's LDS writes before its later LDS reads of other lanes' entries (a wave's LDS operations execute in
-// order; this keeps the compiler from moving them across).
-__device__ __forceinline__ void wave_lds_sync() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_wave_barrier();
-}
 
 constexpr int kWideCap = 4096;    // the wide kernel's candidate buffer (composites)
 constexpr int kWideList = 2048;   // the most candidates ranked at once (write_ranked)
