@@ -544,6 +544,35 @@ __device__ __forceinline__ int rank_in(const u64* list, int n16, u64 c) {
   return r;
 }
 
+// The rank sort of a short list split over the block: for n <= 64 every wave ranks all n entries against a quarter of
+// the list, for n <= 128 each half of the block against a half, so that a thread reads a quarter or a half of the list
+// instead of all of it (below 129 entries one thread per entry would leave two or three waves idle); the partial
+// counts meet behind one barrier. (C5: about 75 candidates per chunk, 60 in the merge; a list of 16 or fewer loses a
+// little to the barrier, but a separate path for it made the kernel's code larger and every k slower.) rank_pad(n) is
+// the length the list must be zero-padded to (the zeros rank below every composite).
+__device__ __forceinline__ int rank_groups(int n) { return n <= 64 ? 4 : n <= 128 ? 2 : 1; }
+__device__ __forceinline__ int rank_pad(int n) {
+  return rank_groups(n) == 4 ? 64 : rank_groups(n) == 2 ? ((n + 31) & ~31) : ((n + 15) & ~15);
+}
+
+// The number of entries of list[0, n) (distinct composites, n <= kThreads, zero-padded to rank_pad(n)) greater than
+// list[t] for thread t < n; kTileSort for the others. The partial counts meet in part[0, kThreads) (LDS ints apart from
+// the list) behind one barrier. Every thread of the block calls it.
+__device__ __forceinline__ int split_rank(const u64* list, int n, int* part) {
+  const int t = (int)threadIdx.x;
+  const int groups = rank_groups(n);  // block-uniform
+  const int per = kThreads / groups;                 // entries per group's pass: 64, 128 or 256 (>= n)
+  const int len = rank_pad(n) / groups;              // a multiple of 16
+  const int i = t & (per - 1), g = t / per;
+  int r = i < n ? rank_in(list + g * len, len, list[i]) : 0;
+  if (groups > 1) {
+    part[t] = r;
+    __syncthreads();
+    for (int j = 1; j < groups; ++j) r += part[j * per + i];  // t < n: group 0, i == t
+  }
+  return t < n ? r : kTileSort;
+}
+
 // Keeps exactly the k largest of the block's list of n composites (k < n <= kTileSort) by ranking every entry against
 // all of them (one per thread; cheaper than a bitwise search for short lists) and returns the k-th.
 __device__ __forceinline__ u64 prune_ranked(TileSmem& s, TileList& L, int k) {
@@ -586,12 +615,12 @@ __device__ __forceinline__ void finish_list(TileSmem& s, const TileList& L, void
     n += c;
   }
   for (int i = lane; i < L.cnt; i += kWave) s.sorted[pre + i] = L.seg[i];
-  const int n16 = (n + 15) & ~15;
-  if (t >= n && t < n16) s.sorted[t] = 0ull;
+  if (t >= n && t < rank_pad(n)) s.sorted[t] = 0ull;
   __syncthreads();
+  // the partial ranks in the list segments, read above, behind the barrier
+  const int rank = split_rank(s.sorted, n, reinterpret_cast<int*>(&s.seg[0][0]));
   if (t < n) {
     const u64 mine = s.sorted[t];
-    const int rank = rank_in(s.sorted, n16, mine);
     if (rank < k) {
       if (to_output) {
         if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + rank] = composite_bits(mine);
@@ -1054,13 +1083,13 @@ __device__ __forceinline__ void merge_lists(TileSmem& s, BlockRed& red, TileList
         }
         pre += __popcll(m[i]);
       }
-      const int n16 = (n + 15) & ~15;
-      if (t >= n && t < n16) s.sorted[t] = 0ull;
+      if (t >= n && t < rank_pad(n)) s.sorted[t] = 0ull;
       __syncthreads();
       TOPK_STAGE(7);
+      // the partial ranks in the list segments (the heads' copies there were read before the barrier)
+      const int rank = split_rank(s.sorted, n, reinterpret_cast<int*>(&s.seg[0][0]));
       if (t < n) {
         const u64 mine = s.sorted[t];
-        const int rank = rank_in(s.sorted, n16, mine);
         if (rank < k) {
           if constexpr (sizeof(T) == 4) static_cast<uint32_t*>(values)[row * k + rank] = composite_bits(mine);
           else static_cast<uint16_t*>(values)[row * k + rank] = (uint16_t)(composite_bits(mine) >> 16);
