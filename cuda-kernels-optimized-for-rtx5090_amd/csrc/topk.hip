@@ -833,6 +833,10 @@ struct Tile {
   template <bool NEG, typename Lst>
   __device__ __forceinline__ void filter(Lst& L, uint32_t K) {
     const uint32_t t = bits_of(K);
+    // over a non-negative threshold every admitted element is non-negative, and its key is its bits with the top bit
+    // set; ~(lane0 + off) = nl - off: one instruction each per push instead of two
+    uint32_t nl = ~(uint32_t)lane0;
+    asm volatile("" : "+v"(nl));
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       bool a[W];
@@ -852,7 +856,11 @@ struct Tile {
       }
       if (any) {
 #pragma unroll
-        for (int j = 0; j < W; ++j) L.push_mask(m[j], a[j], [&] { return comp(v, j); });
+        for (int j = 0; j < W; ++j)
+          L.push_mask(m[j], a[j], [&] {
+            if constexpr (NEG) return comp(v, j);
+            return ((u64)(bits(v, j) | 0x80000000u) << 32) | (u64)(nl - (uint32_t)(v * NT * W + j));
+          });
       }
     }
   }
