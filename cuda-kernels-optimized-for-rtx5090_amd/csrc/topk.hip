@@ -1289,11 +1289,12 @@ constexpr int kOneChunks = kOneThreads / kThreads;  // consecutive chunks of the
 // A workgroup of four chunks makes a quarter of the arrivals of one per chunk (the caller's counters pack 32 rows
 // into a 128-byte line, whose device-scope adds are performed one after another) and leaves the merge a quarter of
 // the slots.
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool DRAW>
 __global__ void __launch_bounds__(kOneThreads)
     topk_one(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
              u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
              int groups, SampleArgs sa) {
+  if constexpr (!DRAW) sa.out = nullptr;  // a launch without the draw: its code compiles away
   __shared__ u64 best_of[kOneThreads / kWave];
   const long long row = blockIdx.y;
   const int group = blockIdx.x;
@@ -1353,11 +1354,12 @@ __global__ void __launch_bounds__(kOneThreads)
 // complete and counts its arrival on the caller's counters[row]; the row's last arrival merges the lists (merge_lists)
 // and zeroes the counter for the next launch -- no L2 write-back or invalidate, and no second kernel (the protocol of
 // topk/kernel.cu:411-442, without its __threadfence: see hand_off_arrive).
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool DRAW>
 __global__ void __launch_bounds__(kThreads)
     topk_tile(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
               u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
               int k, SampleArgs sa) {
+  if constexpr (!DRAW) sa.out = nullptr;  // a launch without the draw: its code compiles away
   __shared__ TileSmem s;
   const long long row = blockIdx.y;
   const int part = blockIdx.x;
@@ -1839,11 +1841,12 @@ __device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t 
 // k-bound and, when every chunk has one, the smallest q-bound (nchunks * q >= k elements at or above it) bound the
 // row's k-th from below; the lists' entries at or above that floor (about k * 1.4) are gathered, ranked and the first
 // k written out, and the counter is zeroed for the next launch.
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool DRAW>
 __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPRs, four workgroups per CU
     topk_wide(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
               u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
               int k, SampleArgs sa) {
+  if constexpr (!DRAW) sa.out = nullptr;  // a launch without the draw: its code compiles away
   __shared__ Smem<kWideCap> s;
   __shared__ uint32_t redslots[2][kWaves];
   const long long row = blockIdx.y;
@@ -2160,14 +2163,24 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, void* 
       --nchunks;
     if (k == 1) {
       const int groups = (nchunks + kOneChunks - 1) / kOneChunks;
-      hipLaunchKernelGGL((topk_one<T, VEC>), dim3((unsigned)groups, (unsigned)rows), dim3(kOneThreads), 0, stream,
-                         (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk,
-                         nchunks, groups, sa);
+      if (sa.out)
+        hipLaunchKernelGGL((topk_one<T, VEC, true>), dim3((unsigned)groups, (unsigned)rows), dim3(kOneThreads), 0,
+                           stream, (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols,
+                           chunk, nchunks, groups, sa);
+      else
+        hipLaunchKernelGGL((topk_one<T, VEC, false>), dim3((unsigned)groups, (unsigned)rows), dim3(kOneThreads), 0,
+                           stream, (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols,
+                           chunk, nchunks, groups, sa);
       return (int)hipGetLastError();
     }
-    hipLaunchKernelGGL((topk_tile<T, VEC>), dim3((unsigned)nchunks, (unsigned)rows), dim3(kThreads), 0, stream,
-                       (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk, nchunks,
-                       k, sa);
+    if (sa.out)
+      hipLaunchKernelGGL((topk_tile<T, VEC, true>), dim3((unsigned)nchunks, (unsigned)rows), dim3(kThreads), 0, stream,
+                         (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk,
+                         nchunks, k, sa);
+    else
+      hipLaunchKernelGGL((topk_tile<T, VEC, false>), dim3((unsigned)nchunks, (unsigned)rows), dim3(kThreads), 0,
+                         stream, (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols,
+                         chunk, nchunks, k, sa);
     return (int)hipGetLastError();
   }
   // The result does not depend on the chunking, so the chunks are made long enough for a useful bound (16k elements:
@@ -2181,8 +2194,12 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, void* 
     nchunks = (int)((cols + chunk - 1) / chunk);
   }
   const dim3 wgrid((unsigned)nchunks, (unsigned)rows);
-  hipLaunchKernelGGL((topk_wide<T, VEC>), wgrid, dim3(kThreads), 0, stream, (const T*)x, values, (long long*)indices,
-                     (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k, sa);
+  if (sa.out)
+    hipLaunchKernelGGL((topk_wide<T, VEC, true>), wgrid, dim3(kThreads), 0, stream, (const T*)x, values,
+                       (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k, sa);
+  else
+    hipLaunchKernelGGL((topk_wide<T, VEC, false>), wgrid, dim3(kThreads), 0, stream, (const T*)x, values,
+                       (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk, nchunks, k, sa);
   return (int)hipGetLastError();
 }
 
@@ -2209,7 +2226,7 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
   if (per_cu <= 0) {
     if (occ <= 0) {
       int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_tile<float, true>, kThreads, 0) != hipSuccess ||
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_tile<float, true, false>, kThreads, 0) != hipSuccess ||
           n <= 0) {
         (void)hipGetLastError();
         n = 4;
