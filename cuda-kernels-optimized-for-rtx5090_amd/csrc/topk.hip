@@ -1584,7 +1584,7 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
 // buffer. `zeroed`: the caller has zeroed the counters (s.buf[kWideList, kWideList + kRankBuckets / 4)) and s.members
 // behind a barrier. Every thread calls it; the block is synchronized on entry (the caller's) and on return.
 template <typename S>
-__device__ u64 cut_publish(S& s, int m, int k, u64* list, uint32_t lo, uint32_t hi, bool zeroed) {
+__device__ __forceinline__ u64 cut_publish(S& s, int m, int k, u64* list, uint32_t lo, uint32_t hi, bool zeroed) {
   constexpr int P = kWideList / kThreads;
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan (BPT / 4 u64 words of counters)
   static_assert(BPT % 4 == 0 && kWideList < 65536, "counts fit 16 bits");
