@@ -304,7 +304,7 @@ static_assert(kTileSort == kThreads, "the rank sort and the merge heads use one 
 typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
 
 struct TileSmem {
-  u64 seg[kWaves][kTileSeg];
+  u64 seg[kWaves][kTileSeg + 2];  // (+ a spare slot for a batch's writes past the end, padded to 16 bytes)
   alignas(16) u64 sorted[kTileSort];
   u64 top[kSeedMaxK];  // an output row's composites in order (for the fused draw)
   uint32_t red[2][kWaves];
@@ -467,17 +467,17 @@ struct TileList {
   }
 
   // push() for a batch whose ballot m is already known: keep is this lane's bit of m, comp() its composite. A batch
-  // that would pass the segment's end is counted and not stored (the list then overflows, see settle()).
+  // that passes the segment's end is counted, and its writes past the end land in the segment's spare slot (the list
+  // then overflows and the batch is pushed again, see settle()): a clamp per lane instead of a scalar bound check.
   template <typename C>
   __device__ __forceinline__ void push_mask(u64 m, bool keep, const C& comp) {
     if (m) {
-      const int n = __popcll(m);
-      if (cnt + n <= kTileSeg && keep) {
+      if (keep) {
         const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)cnt));
-        seg[pos] = comp();
+        seg[pos < kTileSeg ? pos : kTileSeg] = comp();
       }
-      cnt += n;
+      cnt += __popcll(m);
     }
   }
 
