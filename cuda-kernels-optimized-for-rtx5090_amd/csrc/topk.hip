@@ -841,7 +841,6 @@ struct Tile {
     for (int v = 0; v < NV; ++v) {
       bool a[W];
       u64 m[W];
-      u64 any = 0;
 #pragma unroll
       for (int j = 0; j < W; ++j) {
         if constexpr (sizeof(T) == 4) {
@@ -852,16 +851,15 @@ struct Tile {
           else a[j] = NEG ? (uint16_t)w <= (uint16_t)(t >> 16) : (int16_t)(uint16_t)w >= (int16_t)(uint16_t)(t >> 16);
         }
         m[j] = __ballot(a[j]);
-        any |= m[j];
       }
-      if (any) {
+      // (no test of the vector as a whole first: most vectors of a wave admit an element, and the test cost more
+      // scalar instructions than the per-element tests it skipped)
 #pragma unroll
-        for (int j = 0; j < W; ++j)
-          L.push_mask(m[j], a[j], [&] {
-            if constexpr (NEG) return comp(v, j);
-            return ((u64)(bits(v, j) | 0x80000000u) << 32) | (u64)(nl - (uint32_t)(v * NT * W + j));
-          });
-      }
+      for (int j = 0; j < W; ++j)
+        L.push_mask(m[j], a[j], [&] {
+          if constexpr (NEG) return comp(v, j);
+          return ((u64)(bits(v, j) | 0x80000000u) << 32) | (u64)(nl - (uint32_t)(v * NT * W + j));
+        });
     }
   }
 
