@@ -14,7 +14,8 @@
 //  - stream tier (longer rows still): one workgroup per row, two passes, no workspace; see softmax_stream.
 //  - generic tier (any length or alignment): one workgroup per row, three scalar passes (max, sum, write).
 // The library allocates no device memory: the co-resident tier exchanges its chunk pairs through a static device
-// table whose entries carry a per-launch tag, so nothing has to be cleared between launches.
+// table whose entries carry a per-launch tag, so nothing has to be cleared between launches; launches recorded into a
+// HIP graph take fresh tags at every replay (see softmax_coop).
 // The normalisation multiplies by the fp32 reciprocal of the row sum (the reference divides, softmax/kernel.cu:240;
 // the two differ by at most 1.5 ulp in fp32 and are within the 1e-5 relative tolerance of the fp64 oracle).
 #include <climits>
@@ -211,11 +212,16 @@ __global__ void __launch_bounds__(WAVES * 64)
 // chunk is written as e * (exp(m - M) / S), within 3 fp32 ulp of the once-rounded value before the output's rounding.
 //
 // The pair table needs no clearing: each pair is two 64-bit words, (tag << 32 | m bits) and (tag << 32 | s bits),
-// stored with device-coherent stores, and a word counts only when its tag is this launch's tag for the iteration (the
-// host hands every launch a fresh range of tags; tag 0, the table's load-time contents, is never handed out). The
-// table is double-buffered by iteration parity: a chunk writes its slot of parity p again two iterations later, by
-// which time every workgroup of its group has published the iteration in between, and so has read parity p. A launch
-// on another stream that uses the same slots at the same time can only make a wait fail (its tags differ), never pass.
+// stored with device-coherent stores, and a word counts only when its tag is this launch's tag for the iteration.
+// Every launch gets a fresh range of tags; tag 0, the table's load-time contents, is never handed out. An eager launch
+// takes its range from the host, in [1, 2^31). A launch recorded into a HIP graph cannot: its kernel arguments are
+// replayed as they were captured, and every replay would wait for the tags the previous replay left in the table. It
+// takes its range on the device instead, at every replay, from a cell of its own that a one-wave kernel node just
+// before it fills from a device counter (softmax_coop_cell), in [2^31, 2^32); so no two launches, eager or replayed,
+// share a tag. The table is double-buffered by iteration parity: a chunk writes its slot of parity p again two
+// iterations later, by which time every workgroup of its group has published the iteration in between, and so has
+// read parity p. A launch on another stream that uses the same slots at the same time can only make a wait fail (its
+// tags differ), never pass.
 //
 // The wait is bounded by time: after wait_ticks of the 100 MHz s_memrealtime clock with pairs still missing (other
 // kernels holding CUs, so that the row's workgroups are not all resident) the workgroup takes the row's M and S from x
@@ -223,15 +229,50 @@ __global__ void __launch_bounds__(WAVES * 64)
 // either way; only the time suffers, by about one read of the row per waiting workgroup.
 constexpr int kCoopMaxChunks = 64;   // a row's chunks: one slot each, polled by one lane each of one wave
 constexpr int kCoopSlots = 4096;     // pair slots per parity: the most workgroups one launch may have
+constexpr int kCoopCells = 4096;     // captured launches per device with a tag cell of their own
+constexpr unsigned kDeviceTags = 0x80000000u;  // the top bit marks the tags handed out on the device
 __device__ __align__(256) unsigned long long g_coop_pairs[2][kCoopSlots][2];
+__device__ unsigned g_coop_cells[kCoopCells];     // each captured launch's first tag, refreshed at every replay
+__device__ unsigned long long g_coop_device_next;  // tags handed out on the device so far
+
+// The tag of iteration it of a launch whose first tag is tag0: host tags never reach the top bit (the host restarts
+// its range before they would), device tags keep it and wrap within the top half.
+__device__ __forceinline__ unsigned coop_tag(unsigned tag0, int it) {
+  return (((tag0 & ~kDeviceTags) + (unsigned)it) & ~kDeviceTags) | (tag0 & kDeviceTags);
+}
+
+// Clears the pair table (before a launch whose tags restart after the tag counter wrapped).
+__device__ __forceinline__ void coop_clear_table(unsigned first, unsigned stride) {
+  unsigned long long* p = &g_coop_pairs[0][0][0];
+  for (unsigned i = first; i < 2u * kCoopSlots * 2u; i += stride)
+    __hip_atomic_store(p + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The kernel node ahead of a captured co-resident launch: takes `iters` fresh device tags and leaves the first in the
+// launch's cell. When the range reaches the end of the device half of the tag space the table is cleared first, as the
+// host does for its half, so that a pair left from the previous round of the counter can never match (another
+// stream's launch using the table meanwhile can only see its wait fail).
+__global__ void __launch_bounds__(256) softmax_coop_cell(int cell, unsigned iters) {
+  __shared__ unsigned long long old;
+  if (threadIdx.x == 0)
+    old = __hip_atomic_fetch_add(&g_coop_device_next, (unsigned long long)iters, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const unsigned long long lo = old & ~(unsigned long long)kDeviceTags;
+  if (lo + iters > (unsigned long long)kDeviceTags) coop_clear_table(threadIdx.x, 256);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&g_coop_cells[cell], kDeviceTags | (unsigned)lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // LOOP: some row group has more than one row (groups < rows); without it every workgroup takes one row, and the
 // kernel is compiled without the loop (which costs registers: fewer resident workgroups).
 template <typename T, int WAVES, int NV, bool NTL, bool NTS, bool LOOP>
 __global__ void __launch_bounds__(WAVES * 64)
     softmax_coop(const void* __restrict__ x, void* __restrict__ y, long long rows, long long nvec, int chunks,
-                 int groups, unsigned tag0, unsigned wait_ticks) {
+                 int groups, unsigned tag0, int cell, unsigned wait_ticks) {
   constexpr int G = WAVES * kWave;
+  // a captured launch (cell >= 0) reads its first tag from its cell, filled by the kernel node just before it
+  if (cell >= 0) tag0 = __hip_atomic_load(&g_coop_cells[cell], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   constexpr long long CH = (long long)G * NV;
   constexpr int PER = kCoopMaxChunks / kWave;
   __shared__ float slots[2][WAVES];
@@ -251,7 +292,7 @@ __global__ void __launch_bounds__(WAVES * 64)
     // registers for its whole length)
     int t = t0;
     if constexpr (LOOP) asm volatile("" : "+v"(t));
-    const unsigned long long tag = (unsigned long long)(tag0 + (unsigned)it) << 32;
+    const unsigned long long tag = (unsigned long long)coop_tag(tag0, it) << 32;
     unsigned long long(*table)[2] = g_coop_pairs[it & 1] + (long long)group * chunks;
     Regs<NV> r;
     if constexpr (PREFETCH) r = next;
@@ -384,10 +425,9 @@ __global__ void __launch_bounds__(WAVES * 64)
   }
 }
 
-// Clears the pair table (before a launch whose tags restart after the tag counter wrapped).
+// Clears the pair table (before an eager launch whose tags restart after the host's tag counter wrapped).
 __global__ void __launch_bounds__(256) softmax_coop_clear() {
-  unsigned long long* p = &g_coop_pairs[0][0][0];
-  for (int i = (int)(blockIdx.x * 256 + threadIdx.x); i < 2 * kCoopSlots * 2; i += (int)(gridDim.x * 256)) p[i] = 0;
+  coop_clear_table(blockIdx.x * 256 + threadIdx.x, gridDim.x * 256);
 }
 
 // Generic tier: any row length and alignment; one 256-thread block per row (grid-strided), three scalar passes.
@@ -505,16 +545,16 @@ int launch_stream(const void* x, void* y, long long rows, long long nvec, hipStr
   }
 }
 
-// The co-resident tier's tags: per device, the next unused one (0 is never handed out: it is the pair table's contents
-// at load). A launch takes one per iteration; when the 32-bit counter would wrap, the table is cleared on the launch's
-// stream and the tags start again at 1.
+// The co-resident tier's tags of eager launches: per device, the next unused one of the host's half of the tag space,
+// [1, 2^31) (0 is never handed out: it is the pair table's contents at load). A launch takes one per iteration; when the
+// range would pass 2^31 - 1, the table is cleared on the launch's stream and the tags start again at 1.
 unsigned coop_tags(int dev, unsigned n, hipStream_t stream, int* err) {
   static std::mutex mu;
   static unsigned next[64];
   std::lock_guard<std::mutex> lock(mu);
   unsigned& nx = next[dev & 63];
   *err = rw_host::kOk;
-  if (nx == 0 || nx + n < nx) {
+  if (nx == 0 || (unsigned long long)nx + n > (unsigned long long)kDeviceTags) {
     hipLaunchKernelGGL(softmax_coop_clear, dim3(16), dim3(256), 0, stream);
     *err = (int)hipGetLastError();
     nx = 1;
@@ -522,6 +562,29 @@ unsigned coop_tags(int dev, unsigned n, hipStream_t stream, int* err) {
   const unsigned t = nx;
   nx += n;
   return t;
+}
+
+// A captured launch's tag cell: per device, cells are handed out once each, in capture order, and never reused (a
+// graph may be replayed at any time). Returns -1 when the device's cells are used up; such a launch takes the stream
+// tier, which keeps no state between launches.
+int coop_cell(int dev) {
+  static std::mutex mu;
+  static int next[64];
+  std::lock_guard<std::mutex> lock(mu);
+  int& nx = next[dev & 63];
+  if (nx >= kCoopCells) return -1;
+  return nx++;
+}
+
+// Whether work issued to `stream` is being recorded into a graph (an error reads as not capturing: the launch then
+// fails or runs as an eager one would).
+bool capturing(hipStream_t stream) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &status) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return status != hipStreamCaptureStatusNone;
 }
 
 // Co-resident tier: chunks of 4 waves x 64 lanes x 64 elements (16 fp32 or 8 bf16 vectors per lane), at most
@@ -556,13 +619,25 @@ int launch_coop(const void* x, void* y, long long rows, long long nvec, hipStrea
   if (iters > 0x40000000LL) return 1;
   int dev = 0, err = (int)hipGetDevice(&dev);
   if (err != rw_host::kOk) return err;
-  const unsigned tag0 = coop_tags(dev, (unsigned)iters, stream, &err);
+  unsigned tag0 = 0;
+  int cell = -1;
+  if (capturing(stream)) {
+    // recorded into a graph: the tags are taken on the device at every replay, by a kernel node ahead of the launch
+    cell = coop_cell(dev);
+    if (cell < 0) return 1;
+    hipLaunchKernelGGL(softmax_coop_cell, dim3(1), dim3(256), 0, stream, cell, (unsigned)iters);
+    err = (int)hipGetLastError();
+  } else {
+    tag0 = coop_tags(dev, (unsigned)iters, stream, &err);
+  }
   if (err != rw_host::kOk) return err;
   const int budget = rw_host::tune_get(kTuneWaitTicks);
   const unsigned ticks = budget > 0 ? (unsigned)budget : kCoopWaitTicks;
   const dim3 grid((unsigned)(groups * chunks)), block(WAVES * kWave);
-  if (single) hipLaunchKernelGGL(one, grid, block, 0, stream, x, y, rows, nvec, (int)chunks, (int)groups, tag0, ticks);
-  else hipLaunchKernelGGL(loop, grid, block, 0, stream, x, y, rows, nvec, (int)chunks, (int)groups, tag0, ticks);
+  if (single)
+    hipLaunchKernelGGL(one, grid, block, 0, stream, x, y, rows, nvec, (int)chunks, (int)groups, tag0, cell, ticks);
+  else
+    hipLaunchKernelGGL(loop, grid, block, 0, stream, x, y, rows, nvec, (int)chunks, (int)groups, tag0, cell, ticks);
   return (int)hipGetLastError();
 }
 

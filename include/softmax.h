@@ -5,7 +5,11 @@
  * on the GPU at once are done in one pass by co-resident workgroups that exchange their chunk statistics through a
  * static device table of the library (entries tagged per launch, nothing to clear); launches on one stream are ordered
  * by it, and a launch overlapping another on a second stream stays exact (at worst its workgroups stop waiting after
- * about 100 us and read their row again). Return: 0 success (rows <= 0 or cols <= 0 is a no-op), -1 unsupported dtype,
+ * about 100 us and read their row again). Graph capture: a call on a capturing stream records a one-wave kernel node
+ * ahead of the softmax kernel node, which gives every replay fresh tags on the device, so replays of a captured launch
+ * are exact on whatever x holds at replay time; no memset node is recorded. Each captured co-resident launch keeps one
+ * of 4096 tag cells per device for the life of the process; once they are used up, further captured launches of such
+ * rows take the two-pass stream tier. Return: 0 success (rows <= 0 or cols <= 0 is a no-op), -1 unsupported dtype,
  * otherwise the hipError_t of the launch. */
 #ifndef ROWKERN_SOFTMAX_H
 #define ROWKERN_SOFTMAX_H

@@ -12,6 +12,9 @@
 //   an all -inf row, a row of one huge value); reps: launches on the same buffers, each checked (the co-resident
 //   tier's pair table is reused by the next launch, under fresh tags); wait_ticks bounds the co-resident tier's wait
 //   (1 makes its workgroups stop waiting and take the row's statistics from x).
+// EMU_GRAPH set: after an eager launch, the launch is recorded as a graph (the emulation's capture) and every rep replays it, each with
+// new values in x (seed + rep); odd reps first run an eager launch of the same shape on other values and buffers,
+// which leaves its own pairs in the table. Every replay is checked against the oracle of its own x.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -60,32 +63,38 @@ int main(int argc, char** argv) {
     softmax_tune(1, nv);
   }
   const size_t esz = dtype == 0 ? 4 : 2, n = (size_t)rows * cols;
-  std::mt19937_64 g(seed);
-  std::normal_distribution<float> nd(0.0f, 4.0f);
-  std::vector<float> f(n);
-  for (size_t i = 0; i < n; ++i) {
-    const long long r = (long long)(i / cols), c = (long long)(i % cols);
-    f[i] = nd(g);
-    if (pattern == "special") {
-      if (r % 4 == 0 && c % 5 == 1) f[i] = -INFINITY;
-      if (r % 4 == 1) f[i] = -INFINITY;
-      if (r % 4 == 2 && c == cols / 2) f[i] = 80.0f;
-    } else if (pattern != "randn") {
-      std::fprintf(stderr, "unknown pattern %s\n", pattern.c_str());
-      return 2;
-    }
+  const bool graph = std::getenv("EMU_GRAPH") != nullptr;
+  if (pattern != "randn" && pattern != "special") {
+    std::fprintf(stderr, "unknown pattern %s\n", pattern.c_str());
+    return 2;
   }
-  std::vector<char> host(n * esz);
-  for (size_t i = 0; i < n; ++i) {
-    if (dtype == 0) std::memcpy(&host[i * 4], &f[i], 4);
-    else {
-      const uint16_t b = bf16_rne(f[i]);
-      std::memcpy(&host[i * 2], &b, 2);
+  // the input of rep r: seed + r (rep 0 only, without EMU_GRAPH)
+  auto make_input = [&](int s, std::vector<char>& host) {
+    std::mt19937_64 g(s);
+    std::normal_distribution<float> nd(0.0f, 4.0f);
+    host.assign(n * esz, 0);
+    for (size_t i = 0; i < n; ++i) {
+      const long long r = (long long)(i / cols), c = (long long)(i % cols);
+      float v = nd(g);
+      if (pattern == "special") {
+        if (r % 4 == 0 && c % 5 == 1) v = -INFINITY;
+        if (r % 4 == 1) v = -INFINITY;
+        if (r % 4 == 2 && c == cols / 2) v = 80.0f;
+      }
+      if (dtype == 0) std::memcpy(&host[i * 4], &v, 4);
+      else {
+        const uint16_t b = bf16_rne(v);
+        std::memcpy(&host[i * 2], &b, 2);
+      }
     }
-  }
-  char *xb, *yb;
+  };
+  std::vector<char> host;
+  make_input(seed, host);
+  char *xb, *yb, *x2, *y2;
   hipMalloc((void**)&xb, (n + offset) * esz);
   hipMalloc((void**)&yb, (n + offset) * esz);
+  hipMalloc((void**)&x2, n * esz);
+  hipMalloc((void**)&y2, n * esz);
   char* x = xb + offset * esz;
   char* y = yb + offset * esz;
   std::memcpy(x, host.data(), n * esz);
@@ -93,9 +102,34 @@ int main(int argc, char** argv) {
   oracle_softmax(host.data(), ref.data(), rows, cols, dtype);
   int err = 0;
   long long bad = 0, first = -1;
-  for (int rep = 0; rep < reps && !err && !bad; ++rep) {
-    std::memset(y, 0xA5, n * esz);
+  emu::Graph recorded;
+  if (graph) {
+    // an eager launch first (a warm-up, as a graph capture usually follows one), then the capture
+    std::memcpy(x2, host.data(), n * esz);
+    err = launch(x2, y2, rows, cols, dtype, 256, 0, nullptr);
+    emu::capture_begin(recorded);
     err = launch(x, y, rows, cols, dtype, 256, 0, nullptr);
+    emu::capture_end();
+  }
+  for (int rep = 0; rep < reps && !err && !bad; ++rep) {
+    if (graph && rep > 0) {
+      make_input(seed + rep, host);
+      std::memcpy(x, host.data(), n * esz);
+      oracle_softmax(host.data(), ref.data(), rows, cols, dtype);
+    }
+    std::memset(y, 0xA5, n * esz);
+    if (graph) {
+      if (rep % 2) {
+        // an eager launch of the same shape on other values in between: its pairs sit in the same table slots
+        std::vector<char> other;
+        make_input(seed + 1000 + rep, other);
+        std::memcpy(x2, other.data(), n * esz);
+        err = launch(x2, y2, rows, cols, dtype, 256, 0, nullptr);
+      }
+      emu::replay(recorded);
+    } else {
+      err = launch(x, y, rows, cols, dtype, 256, 0, nullptr);
+    }
     for (size_t i = 0; i < n && !err; ++i) {
       bool ok;
       if (dtype == 0) {
@@ -121,5 +155,7 @@ int main(int argc, char** argv) {
               rows, cols, dtype, tier, ok ? "ALL OK" : "FAILED", err, bad, first, input_kept);
   hipFree(xb);
   hipFree(yb);
+  hipFree(x2);
+  hipFree(y2);
   return ok ? 0 : 1;
 }

@@ -466,7 +466,12 @@ inline void launch(dim3 grid, dim3 block, std::function<void()> body) {
     w->block_idx = blocks[j];
     w->shuffle_seed = s.shuffle_seed;
     if (s.shuffle_seed >= 0) w->rng.seed((unsigned)(s.shuffle_seed * 7919 + j));
-    threads.emplace_back([w] {
+    // EMU_STAGGER: workgroups start up to 400 ms apart (a workgroup's work takes tens of ms here), so that early ones
+    // reach their waits long before late ones have published anything
+    static const bool stagger = std::getenv("EMU_STAGGER") != nullptr;
+    const int delay_ms = stagger ? (int)(j % 3) * 200 : 0;
+    threads.emplace_back([w, delay_ms] {
+      if (delay_ms) std::this_thread::sleep_for(std::chrono::milliseconds(delay_ms));
       tls_state() = w;
       run_block();
     });
@@ -629,4 +634,32 @@ inline hipError_t hipMemsetAsync(void* p, int v, size_t n, hipStream_t) {
   std::memset(p, v, n);
   return hipSuccess;
 }
-#define hipLaunchKernelGGL(K, G, B, SH, ST, ...) emu::launch(dim3(G), dim3(B), [&]() { K(__VA_ARGS__); })
+// Graph capture: between emu::capture_begin() and emu::capture_end() launches are recorded, not run, and
+// hipStreamIsCapturing reports an active capture; emu::replay() runs a recorded sequence again (kernel arguments as
+// they were captured, like a HIP graph's kernel nodes).
+namespace emu {
+typedef std::vector<std::function<void()>> Graph;
+inline Graph*& recording() {
+  static Graph* g = nullptr;
+  return g;
+}
+inline void capture_begin(Graph& g) {
+  g.clear();
+  recording() = &g;
+}
+inline void capture_end() { recording() = nullptr; }
+inline void replay(const Graph& g) {
+  for (const auto& node : g) node();
+}
+inline void launch_or_record(dim3 grid, dim3 block, std::function<void()> body) {
+  if (recording()) recording()->push_back([grid, block, body] { launch(grid, block, body); });
+  else launch(grid, block, std::move(body));
+}
+}  // namespace emu
+enum hipStreamCaptureStatus { hipStreamCaptureStatusNone = 0, hipStreamCaptureStatusActive = 1 };
+inline hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus* st) {
+  *st = emu::recording() ? hipStreamCaptureStatusActive : hipStreamCaptureStatusNone;
+  return hipSuccess;
+}
+// arguments are captured by value: a recorded launch runs after the launching function has returned
+#define hipLaunchKernelGGL(K, G, B, SH, ST, ...) emu::launch_or_record(dim3(G), dim3(B), [=]() { K(__VA_ARGS__); })

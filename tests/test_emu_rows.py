@@ -10,7 +10,8 @@ sizes down to 24 and its fused KV-cache write with skipped (-1) slots. The softm
 workgroups wait for one another, runs with every workgroup on an OS thread of its own, over repeated launches (the
 pair table is reused under fresh tags), with one row per workgroup and with row groups walking several rows; also
 under the weak mode (its pairs become visible late and out of order) with the wait's clock stopped, so that every wait
-must end by its pairs, never by its time budget. Some cases also run with each wave running ahead to the next block
+must end by its pairs, never by its time budget; and recorded once as a graph (the emulation's capture) and replayed
+on new values, with eager launches in between. Some cases also run with each wave running ahead to the next block
 barrier before the next wave starts.
 """
 
@@ -120,6 +121,19 @@ def test_emulated_softmax_coresident_weak_stopped_clock(emu_softmax, case):
     rows, cols, dtype, seed, pattern, reps, groups = case[1:]
     env = dict(os.environ, EMU_CLOCK_STOPPED="1")
     run(emu_softmax, [rows, cols, dtype, 4, seed, 0, groups, 0, pattern, reps], env=env, concurrent=True, weak=True,
+        timeout=300)
+
+
+@pytest.mark.parametrize("case", COOP, ids=[c[0] for c in COOP])
+def test_emulated_softmax_coresident_graph_replay(emu_softmax, case):
+    # after an eager launch, the launch recorded once and replayed four times, each replay on new values of x, with
+    # eager launches of other values on the same table slots between some replays; workgroups starting up to 400 ms
+    # apart, pairs visible late and out of order and the clock stopped,
+    # so a wait can only end by pairs carrying its own tags: a replay that accepted a pair left by the replay before it
+    # (the same captured arguments) or by the eager launch would normalise with the wrong statistics
+    rows, cols, dtype, seed, pattern, _, groups = case[1:]
+    env = dict(os.environ, EMU_CLOCK_STOPPED="1", EMU_GRAPH="1", EMU_STAGGER="1")
+    run(emu_softmax, [rows, cols, dtype, 4, seed, 0, groups, 0, pattern, 4], env=env, concurrent=True, weak=True,
         timeout=300)
 
 

@@ -8,6 +8,7 @@ vector width and for misaligned pointers.
 """
 
 import ctypes
+import time
 
 import numpy as np
 import pytest
@@ -105,6 +106,70 @@ def test_long_rows_single_pass_and_stream(pkg, oracle, dev, rows, cols, dtype):
             else:
                 assert_rel(y.cpu().numpy(), ref, FP32_TOL, f"tier {tier}")
     finally:
+        lib.softmax_tune(5, 0)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_coresident_graph_replay(pkg, oracle, dev, dtype):
+    """A C4-shaped launch (64 x 262144, the co-resident tier) recorded into a HIP graph with torch.cuda.graph and
+    replayed on new values of x, with eager launches of other values on the same pair-table slots between some
+    replays. Each replay must take fresh tags on the device: with the tags of the capture it would accept the pairs
+    the replay before it left. The wait budget is raised to 2^30 ticks (about 10 s), so a replay can only finish
+    quickly by finding its own pairs, not by the fallback; each replay is checked against the oracle of its x."""
+    lib = pkg.candidate("softmax")._lib
+    rows, cols = 64, 262144
+    g = torch.Generator().manual_seed(31)
+    xs = []
+    for i in range(4):
+        x = torch.randn(rows, cols, generator=g) * (5 if i % 2 == 0 else 2)
+        x.view(-1)[torch.randperm(rows * cols, generator=g)[: rows * cols // 100]] = 20.0 - 3 * i
+        xs.append(x.bfloat16() if dtype == "bf16" else x)
+    code = 1 if dtype == "bf16" else 0
+
+    def ref(x):
+        return oracle.softmax(bits16(x), "bf16") if dtype == "bf16" else oracle.softmax(x.numpy(), "fp32")
+
+    def check(y, x, what):
+        if dtype == "bf16":
+            assert_ulp(bits16(y), ref(x), 1, what)
+        else:
+            assert_rel(y.cpu().numpy(), ref(x), FP32_TOL, what)
+
+    xd, yd = xs[0].to(dev), torch.empty(rows, cols, dtype=xs[0].dtype, device=dev)
+    x2, y2 = torch.empty_like(xd), torch.empty_like(yd)
+    try:
+        lib.softmax_tune(5, 4)
+        lib.softmax_tune(7, 1 << 30)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # the eager warm-up launch, on a side stream as torch's capture recipe has it
+            assert lib.launch(xd.data_ptr(), yd.data_ptr(), rows, cols, code, 256, 1024, side.cuda_stream) == 0
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        check(yd, xs[0], "eager warm-up")
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            rc = lib.launch(xd.data_ptr(), yd.data_ptr(), rows, cols, code, 256, 1024,
+                            torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        for rep in range(6):
+            x = xs[rep % 4]
+            print(f"[softmax graph] {dtype} replay {rep}", flush=True)
+            xd.copy_(x.to(dev))
+            yd.fill_(float("nan"))
+            if rep % 3 == 2:  # an eager launch of other values first: its pairs sit in the same table slots
+                x2.copy_(xs[(rep + 1) % 4].to(dev))
+                s = torch.cuda.current_stream().cuda_stream
+                assert lib.launch(x2.data_ptr(), y2.data_ptr(), rows, cols, code, 256, 1024, s) == 0
+            torch.cuda.synchronize()
+            t0 = time.monotonic()
+            graph.replay()
+            torch.cuda.synchronize()
+            took = time.monotonic() - t0
+            assert took < 1.0, f"replay {rep} took {took:.2f} s: its waits ended by the time budget, not by its pairs"
+            check(yd, x, f"replay {rep}")
+    finally:
+        lib.softmax_tune(7, 0)
         lib.softmax_tune(5, 0)
 
 
