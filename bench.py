@@ -31,6 +31,7 @@ whole workload (--cpu-seconds of host time shared by all); the headline's is als
 import argparse
 import glob
 import csv
+import hashlib
 import json
 import os
 import sys
@@ -38,6 +39,7 @@ import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
+PKG_DIR = os.path.join(ROOT, "cuda-kernels-optimized-for-rtx5090_amd")
 
 METRIC = "per-kernel µs/call + achieved HBM GB/s (% of MI355X peak) at named shape, 1 GPU"
 PEAK_GBS = 8000.0
@@ -367,13 +369,32 @@ def cpu_model():
     return "unknown"
 
 
+def sources_sha16():
+    """A digest of the op libraries' kernel sources (csrc/), naming the code a measurement was made on."""
+    h = hashlib.sha256()
+    csrc = os.path.join(PKG_DIR, "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".hpp")):
+            with open(os.path.join(csrc, name), "rb") as f:
+                h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
+
+
 def roofline_entry(res, label):
-    traffic = None
+    """The roofline object of the bench line. `traffic` is not measured by this run: it is read from the committed
+    profiles/traffic.json (FETCH_SIZE and WRITE_SIZE counter runs of a separate profiling lease), and
+    `traffic_source` says so, with whether those runs counted the kernel sources this run uses."""
+    traffic, source = None, None
     if os.path.exists(TRAFFIC_PATH):
         with open(TRAFFIC_PATH) as f:
-            traffic = json.load(f).get(label, {}).get("bytes_per_launch")
+            table = json.load(f)
+        traffic = table.get(label, {}).get("bytes_per_launch")
+        counted = table.get("sources_sha16")
+        source = {"file": "profiles/traffic.json",
+                  "how": "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of a separate profiling lease, not this run",
+                  "sources_sha16": counted, "same_sources_as_this_run": counted == sources_sha16()}
     return {"bound": "hbm", "achieved": round(res["gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
-            "frac": round(res["gbs"] / PEAK_GBS, 4), "traffic": traffic}
+            "frac": round(res["gbs"] / PEAK_GBS, 4), "traffic": traffic, "traffic_source": source}
 
 
 def copy_calibration(steps):
@@ -684,7 +705,8 @@ def traffic_from(run_dir):
                       "launch), each scaled by the known bytes of the matching kernel of bench.py --copy-calibration "
                       "(a 256 MiB sum for FETCH_SIZE, a 256 MiB fill for WRITE_SIZE) over its counted bytes",
            "calibration_fetch_kib": cf and round(cf, 1), "calibration_write_kib": cw and round(cw, 1),
-           "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}
+           "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+           "sources_sha16": sources_sha16()}
     for label, kernel in KERNELS.items():
         f = pick(fetch, f"{label}_fetch", kernel)
         w = pick(write, f"{label}_write", kernel)

@@ -14,11 +14,13 @@
 // q_out may be q and k_out may be k (in place): every lane reads its elements before it writes the same elements and
 // no other lane touches them, so the input and output pointers are not declared restrict.
 //
-// Vector path (D % 16 == 0, all tensors 16-byte aligned): an item is 8 pairs of one head (two 16-byte vectors of x);
-// a token has heads * D / 16 items and a block takes one token at a time, IPT items per lane, walking the tokens with
-// the grid's stride and loading its next token's items while it rotates and stores the current one. The on-the-fly
-// entry computes a token's D/2 (cos, sin) pairs once per block into LDS (double-buffered by token parity, one barrier
-// per token) instead of once per head. Other shapes run a scalar kernel (one pair per thread per head).
+// Vector path (D % 16 == 0, D <= 1024, all tensors 16-byte aligned): an item is 8 pairs of one head (two 16-byte
+// vectors of x); a token has heads * D / 16 items and a block takes one token at a time, IPT items per lane, walking
+// the tokens with the grid's stride and loading its next token's items while it rotates and stores the current one.
+// A token's cos/sin are put into an LDS table once per block (double-buffered by token parity, one barrier per token)
+// and read from there by every head: the on-the-fly entry computes its D/2 (cos, sin) pairs, the cache entry loads
+// the token's cos and sin rows (as the reference loads them once per thread for all its heads, rope/kernel.cu:103-135),
+// prefetched with the token's items. Other shapes run a scalar kernel (one pair per thread per head).
 #include <climits>
 #include <cmath>
 
@@ -31,21 +33,21 @@ using namespace rw;
 
 namespace {
 
-constexpr int kMaxHalf = 512;  // on-the-fly vector path: D <= 1024
+constexpr int kMaxHalf = 512;  // vector path: D <= 1024
 
-// Eight cache values [i, i + 8) of a cos or sin row as floats.
-template <typename C> __device__ __forceinline__ void load8(const void* p, long long i, float* v);
-template <> __device__ __forceinline__ void load8<F32>(const void* p, long long i, float* v) {
-  const u32x4 a = load16<false>(p, i / 4), b = load16<false>(p, i / 4 + 1);
-  unpack<F32>(a, v);
-  unpack<F32>(b, v + 4);
-}
-template <> __device__ __forceinline__ void load8<BF16>(const void* p, long long i, float* v) {
-  unpack<BF16>(load16<false>(p, i / 8), v);
-}
-template <> __device__ __forceinline__ void load8<F16>(const void* p, long long i, float* v) {
-  unpack<F16>(load16<false>(p, i / 8), v);
-}
+// The LDS tables of a token's cos/sin. Lane j's item covers pairs [8c, 8c + 8) with c = j % 8 (a block's threads are a
+// multiple of 64 and a head has D / 16 items), so the 8 lanes of one read step read 8 different 8-entry groups at once.
+// Each group is padded so that those 8 reads fall in distinct LDS banks (with 32 or 64 banks of 4 bytes) while every
+// read stays a 16-byte one:
+//  - on the fly: (cos, sin) of pair i as a float2 at float2 index i + 2 (i / 8): groups 80 bytes apart;
+//  - cache: the token's cos row then its sin row, fp32, element e of a row at float index e + 4 (e / 32) of it (16
+//    bytes after every 128), the sin row at kCacheRow floats after the cos row: groups 32 bytes apart, 48 across the
+//    padding.
+__device__ __forceinline__ int freq_slot(int i) { return i + 2 * (i >> 3); }
+__device__ __forceinline__ int cache_slot(int e) { return e + 4 * (e >> 5); }
+constexpr int kFreqTable = 2 * (kMaxHalf + kMaxHalf / 4);          // floats of one buffer: kMaxHalf padded float2
+constexpr int kCacheRow = 2 * kMaxHalf + (2 * kMaxHalf) / 8;       // floats of one padded row of D <= 1024
+constexpr int kCacheTable = 2 * kCacheRow;                          // cos row and sin row
 
 struct Shape {
   long long tokens;
@@ -100,6 +102,7 @@ __device__ __forceinline__ void* head_dst(void* q_out, void* k_out, const Cache&
 template <int IPT>
 struct Items {
   u32x4 a[IPT], b[IPT];
+  u32x4 trig;  // cache entry: this thread's 16-byte vector of the token's cos and sin rows (see load_trig)
 };
 
 // Loads the IPT items of lane j for `token` (an out-of-range item is clamped to the token's last item, never stored).
@@ -117,6 +120,35 @@ __device__ __forceinline__ void load_items(Items<IPT>& r, const void* q, const v
     o += 8 * c;
     r.a[u] = load16<true>(x, o / 8);
     r.b[u] = load16<true>(x, (o + half) / 8);
+  }
+}
+
+// Cache entry: thread j < 2 D / W (W cache elements per 16-byte vector) loads vector j of the token's cos row followed
+// by its sin row (row ids[token] of each), into r.trig.
+template <typename C>
+__device__ __forceinline__ void load_trig(u32x4& v, const void* cos_rows, const void* sin_rows, long long id,
+                                          int head_dim, int j) {
+  const int per_row = head_dim / C::V;  // vectors per row
+  if (j < 2 * per_row) {
+    const void* rows = j < per_row ? cos_rows : sin_rows;
+    const int jv = j < per_row ? j : j - per_row;
+    v = load16<false>(rows, id * per_row + jv);
+  }
+}
+
+// Cache entry: the thread's vector of load_trig into the LDS table, as fp32 at its padded positions.
+template <typename C>
+__device__ __forceinline__ void store_trig(const u32x4& v, float* tab, int head_dim, int j) {
+  const int per_row = head_dim / C::V;
+  if (j < 2 * per_row) {
+    float f[C::V];
+    unpack<C>(v, f);
+    const int row = j < per_row ? 0 : 1;
+    const int e0 = (j - row * per_row) * C::V;
+    float* dst = tab + row * kCacheRow;
+#pragma unroll
+    for (int e = 0; e < C::V; e += 4)  // 4 consecutive elements never straddle the padding (it falls every 32)
+      *reinterpret_cast<float4*>(dst + cache_slot(e0 + e)) = make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]);
   }
 }
 
@@ -155,30 +187,35 @@ __device__ __forceinline__ void rotate_items(const Items<IPT>& r, void* q_out, v
   }
 }
 
-// cos/sin from the cache row of the token's position.
-template <typename C>
-struct CacheTrig {
-  const void* cos_rows;
-  const void* sin_rows;
-  long long row;  // element offset of the row
+// cos/sin from the block's LDS table of the token's cache rows (store_trig's layout).
+struct LdsCacheTrig {
+  const float* tab;
   int half;
   __device__ __forceinline__ void operator()(int i, float* c1, float* s1, float* c2, float* s2) const {
-    load8<C>(cos_rows, row + i, c1);
-    load8<C>(sin_rows, row + i, s1);
-    load8<C>(cos_rows, row + i + half, c2);
-    load8<C>(sin_rows, row + i + half, s2);
+    auto row8 = [&](const float* row, int e, float* v) {
+      const float4 a = *reinterpret_cast<const float4*>(row + cache_slot(e));
+      const float4 b = *reinterpret_cast<const float4*>(row + cache_slot(e + 4));
+      v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    };
+    row8(tab, i, c1);
+    row8(tab + kCacheRow, i, s1);
+    row8(tab, i + half, c2);
+    row8(tab + kCacheRow, i + half, s2);
   }
 };
 
-// cos/sin from the block's LDS table of the token.
+// cos/sin from the block's LDS table of the token's (cos, sin) pairs (freq_slot's layout).
 struct LdsTrig {
   const float2* cs;
   __device__ __forceinline__ void operator()(int i, float* c1, float* s1, float* c2, float* s2) const {
+    const float4* p = reinterpret_cast<const float4*>(cs + freq_slot(i));  // 8 pairs, 16-byte aligned (i % 8 == 0)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float2 v = cs[i + e];
-      c1[e] = c2[e] = v.x;
-      s1[e] = s2[e] = v.y;
+    for (int e = 0; e < 4; ++e) {
+      const float4 v = p[e];
+      c1[2 * e] = c2[2 * e] = v.x;
+      s1[2 * e] = s2[2 * e] = v.y;
+      c1[2 * e + 1] = c2[2 * e + 1] = v.z;
+      s1[2 * e + 1] = s2[2 * e + 1] = v.w;
     }
   }
 };
@@ -192,34 +229,39 @@ __device__ __forceinline__ float2 freq_trig(long long pos, float inv_freq) {
 }
 
 template <typename T, typename C, bool FREQ, bool KV, int IPT>
-__device__ __forceinline__ void token_step(const Items<IPT>& r, const void* cos_rows, const void* sin_rows,
-                                           const float* inv_freq, const long long* ids, void* q_out, void* k_out,
-                                           const Cache& kv, long long token, const Shape& s, int items,
-                                           int lanes_per_head, int j, float2* cs) {
+__device__ __forceinline__ void token_step(const Items<IPT>& r, const float* inv_freq, const long long* ids,
+                                           void* q_out, void* k_out, const Cache& kv, long long token, const Shape& s,
+                                           int items, int lanes_per_head, int j, float* tab) {
   const bool active = token < s.tokens;
   const long long tok = active ? token : s.tokens - 1;
   const long long slot = KV ? kv.slots[tok] : tok;  // the k output row: the token's cache slot when fused
   const int half = s.head_dim >> 1;
   if constexpr (FREQ) {
     const long long pos = ids[tok];
-    for (int i = j; i < half; i += blockDim.x) cs[i] = freq_trig(pos, inv_freq[i]);
+    float2* cs = reinterpret_cast<float2*>(tab);
+    for (int i = j; i < half; i += blockDim.x) cs[freq_slot(i)] = freq_trig(pos, inv_freq[i]);
     __syncthreads();
     rotate_items<T, KV, IPT>(r, q_out, k_out, kv, tok, slot, s, items, lanes_per_head, j, active, LdsTrig{cs});
   } else {
-    const long long row = ids[tok] * (long long)s.head_dim;
+    store_trig<C>(r.trig, tab, s.head_dim, j);
+    __syncthreads();
     rotate_items<T, KV, IPT>(r, q_out, k_out, kv, tok, slot, s, items, lanes_per_head, j, active,
-                             CacheTrig<C>{cos_rows, sin_rows, row, half});
+                             LdsCacheTrig{tab, half});
   }
 }
 
 // Persistent vector kernel: block b takes tokens b, b + grid, ... with a uniform trip count (a block past the last
-// token loads an in-bounds token and stores nothing), two register sets of items alternating between tokens.
+// token loads an in-bounds token and stores nothing), two register sets of items (and, for the cache entry, of the
+// token's cos/sin vectors) alternating between tokens. The LDS table is double-buffered by token parity: a buffer is
+// written again two tokens later, after the barrier of the token in between, which every thread passes only once it
+// has read the buffer.
 template <typename T, typename C, bool FREQ, bool KV, int IPT>
 __global__ void __launch_bounds__(1024)
     rope_vec(const void* q, const void* k, const void* __restrict__ cos_rows, const void* __restrict__ sin_rows,
              const float* __restrict__ inv_freq, const long long* __restrict__ ids, void* q_out, void* k_out,
              Cache kv, Shape s) {
-  __shared__ float2 cs[2][FREQ ? kMaxHalf : 1];
+  constexpr int TABLE = FREQ ? kFreqTable : kCacheTable;
+  __shared__ __align__(16) float tab[2][TABLE];
   const int lanes_per_head = s.head_dim >> 4;
   const int items = (s.q_heads + s.kv_heads + (KV ? s.v_heads : 0)) * lanes_per_head;
   const int j = threadIdx.x;
@@ -227,18 +269,20 @@ __global__ void __launch_bounds__(1024)
   if (t >= s.tokens) return;
   const long long last = s.tokens - 1;
   Items<IPT> a, b;
-  load_items<KV, IPT>(a, q, k, kv, t, s, items, lanes_per_head, j);
+  auto load = [&](Items<IPT>& r, long long tok) __attribute__((always_inline)) {
+    load_items<KV, IPT>(r, q, k, kv, tok, s, items, lanes_per_head, j);
+    if constexpr (!FREQ) load_trig<C>(r.trig, cos_rows, sin_rows, ids[tok], s.head_dim, j);
+  };
+  load(a, t);
   while (true) {
     const long long tb = t + gridDim.x;
-    load_items<KV, IPT>(b, q, k, kv, tb < s.tokens ? tb : last, s, items, lanes_per_head, j);
-    token_step<T, C, FREQ, KV, IPT>(a, cos_rows, sin_rows, inv_freq, ids, q_out, k_out, kv, t, s, items, lanes_per_head,
-                                j, cs[0]);
+    load(b, tb < s.tokens ? tb : last);
+    token_step<T, C, FREQ, KV, IPT>(a, inv_freq, ids, q_out, k_out, kv, t, s, items, lanes_per_head, j, tab[0]);
     t = tb;
     if (t >= s.tokens) break;
     const long long tc = t + gridDim.x;
-    load_items<KV, IPT>(a, q, k, kv, tc < s.tokens ? tc : last, s, items, lanes_per_head, j);
-    token_step<T, C, FREQ, KV, IPT>(b, cos_rows, sin_rows, inv_freq, ids, q_out, k_out, kv, t, s, items, lanes_per_head,
-                                j, cs[1]);
+    load(a, tc < s.tokens ? tc : last);
+    token_step<T, C, FREQ, KV, IPT>(b, inv_freq, ids, q_out, k_out, kv, t, s, items, lanes_per_head, j, tab[1]);
     t = tc;
     if (t >= s.tokens) break;
   }
@@ -342,6 +386,11 @@ int launch_shape(const Ptrs& p, const Shape& s, bool vec, hipStream_t stream) {
       threads = (int)(((items + per - 1) / per + 63) / 64 * 64);
       if (threads > 1024) threads = 1024;
     }
+    if (!FREQ) {
+      // the cache entry: one thread per 16-byte vector of the token's cos and sin rows (at most 512: D <= 1024)
+      const int trig = 2 * s.head_dim / C::V;
+      if (threads < trig) threads = (trig + 63) / 64 * 64;
+    }
     const long long ipt = (items + threads - 1) / threads;
     if (ipt <= 1) return launch_vec_k<T, C, FREQ, KV, 1>(p, s, threads, stream);
     if (ipt <= 2) return launch_vec_k<T, C, FREQ, KV, 2>(p, s, threads, stream);
@@ -363,7 +412,7 @@ bool all_aligned(const Ptrs& p, bool freq) {
 
 template <typename T>
 int launch_cache(int cache_dtype, const Ptrs& p, const Shape& s, hipStream_t stream) {
-  const bool vec = s.head_dim % 16 == 0 && all_aligned(p, false);
+  const bool vec = s.head_dim % 16 == 0 && s.head_dim / 2 <= kMaxHalf && all_aligned(p, false);
   if (cache_dtype == 0) return launch_shape<T, F32, false>(p, s, vec, stream);
   if (cache_dtype == 1) return launch_shape<T, BF16, false>(p, s, vec, stream);
   if (cache_dtype == 2) return launch_shape<T, F16, false>(p, s, vec, stream);

@@ -148,11 +148,11 @@ __device__ __forceinline__ int wave_excl_count(int n, int& total) {
   return excl;
 }
 
-// Appends the lane's composites c with keep to buf: one LDS atomic per wave reserves the wave's total. Returns the
-// buffer fill right after the wave's append (0 if it appended nothing); the largest over a block's appends is the
-// block's final count.
+// Appends the lane's composites c with keep to buf, in lane order within each of the N rounds: one LDS atomic per wave
+// reserves the positions of all of the wave's kept composites, and each kept lane writes at the reserved base plus
+// the kept lanes below it. The buffer's count is s.count once every wave has appended.
 template <int N, typename S>
-__device__ __forceinline__ int append(S& s, const u64 (&c)[N], const bool (&keep)[N]) {
+__device__ __forceinline__ void append(S& s, const u64 (&c)[N], const bool (&keep)[N]) {
   u64 m[N];
   int total = 0;
 #pragma unroll
@@ -160,7 +160,7 @@ __device__ __forceinline__ int append(S& s, const u64 (&c)[N], const bool (&keep
     m[i] = __ballot(keep[i]);
     total += __popcll(m[i]);
   }
-  if (total == 0) return 0;
+  if (total == 0) return;
   int base = 0;
   if (lane_id() == 0) base = atomicAdd(&s.count, total);
   base = __builtin_amdgcn_readfirstlane(base);
@@ -169,7 +169,6 @@ __device__ __forceinline__ int append(S& s, const u64 (&c)[N], const bool (&keep
     if (keep[i]) s.buf[base + lanes_below(m[i])] = c[i];
     base += __popcll(m[i]);
   }
-  return base;
 }
 
 // One narrowing pass: histograms the composites in [lo, hi] (visited through `each`, which calls its argument once per
@@ -2147,18 +2146,45 @@ __global__ void __launch_bounds__(kThreads)
 // Tuning slots (0 = automatic): 0 resident workgroups per CU assumed by plan(); 1 the naive tier for launch() (1).
 enum { kTuneBlocksPerCu = 0, kTuneSeed = 1 };
 
+// The chunking a launch of the caller's nchunks chunks of `chunk` columns actually runs, and the u64 slots of the
+// caller's work it uses (0 for unsplit rows). The result does not depend on the chunking, so the launch may join
+// chunks (fewer, longer ones), which keeps every slot it uses inside the caller's rows * nchunks * k:
+//  - k <= 64: a last chunk too short to give each of the four waves a vector would leave a wave without a bound, and
+//    the tile would take the exact re-push path; when the previous chunk can take it within one register tile, it
+//    does. k = 1 uses one slot per chunk (its workgroups take four chunks each and use the first slots of the row).
+//  - k > 64: chunks long enough for a useful bound (16k elements: a tile holds the 4 * ceil(k / 4) group maxima the
+//    bound needs) and few enough for the merge: at most kWideMaxChunks, and at most k, so that the chunks' bound
+//    headers fit the row's output indices.
+struct Chunking {
+  long long chunk;
+  int nchunks;
+  long long slots;
+};
+Chunking chunking(long long rows, long long cols, long long chunk, int nchunks, int k, int width) {
+  if (k <= kSeedMaxK) {
+    const long long tail = cols - (long long)(nchunks - 1) * chunk;
+    if (nchunks > 1 && tail < (long long)kThreads * width && chunk + tail <= (long long)kThreads * kTileE) --nchunks;
+  } else {
+    const long long most = k < kWideMaxChunks ? k : kWideMaxChunks;
+    long long want = 16LL * k;
+    if (want < (cols + most - 1) / most) want = (cols + most - 1) / most;
+    if (chunk < want && nchunks > 1) {
+      chunk = want < cols ? (want + 7) / 8 * 8 : cols;
+      nchunks = (int)((cols + chunk - 1) / chunk);
+    }
+  }
+  return Chunking{chunk, nchunks, nchunks > 1 ? rows * nchunks * (k == 1 ? 1LL : (long long)k) : 0LL};
+}
+
 // The kernels of a launch whose rows are split into nchunks chunks of `chunk` columns. work and counters are the
-// caller's (work: u64 [rows * nchunks * k]; counters: u32 [rows], zero); the launch may join chunks (fewer, longer
-// ones), which keeps every slot it uses inside that work.
+// caller's (work: u64 [rows * nchunks * k]; counters: u32 [rows], zero), rechunked by chunking().
 template <typename T, bool VEC>
 int launch_chunks(const void* x, void* values, void* indices, void* work, void* counters, long long rows,
-                  long long cols, long long chunk, int nchunks, int k, const SampleArgs& sa, hipStream_t stream) {
+                  long long cols, long long chunk0, int nchunks0, int k, const SampleArgs& sa, hipStream_t stream) {
+  const Chunking c = chunking(rows, cols, chunk0, nchunks0, k, Tile<T, VEC>::W);
+  const long long chunk = c.chunk;
+  const int nchunks = c.nchunks;
   if (k <= kSeedMaxK) {
-    // A last chunk too short to give each of the four waves a vector would leave a wave without a bound, and the tile
-    // would take the exact re-push path; when the previous chunk can take it within one register tile, it does.
-    const long long tail = cols - (long long)(nchunks - 1) * chunk;
-    if (nchunks > 1 && tail < (long long)kThreads * Tile<T, VEC>::W && chunk + tail <= (long long)kThreads * kTileE)
-      --nchunks;
     if (k == 1) {
       const int groups = (nchunks + kOneChunks - 1) / kOneChunks;
       if (sa.out)
@@ -2180,16 +2206,6 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, void* 
                          stream, (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols,
                          chunk, nchunks, k, sa);
     return (int)hipGetLastError();
-  }
-  // The result does not depend on the chunking, so the chunks are made long enough for a useful bound (16k elements:
-  // a tile holds the 4 * ceil(k / 4) group maxima the bound needs) and few enough for the merge: at most
-  // kWideMaxChunks, and at most k, so that the chunks' bound headers fit the row's output indices.
-  const long long most = k < kWideMaxChunks ? k : kWideMaxChunks;
-  long long want = 16LL * k;
-  if (want < (cols + most - 1) / most) want = (cols + most - 1) / most;
-  if (chunk < want && nchunks > 1) {
-    chunk = want < cols ? (want + 7) / 8 * 8 : cols;
-    nchunks = (int)((cols + chunk - 1) / chunk);
   }
   const dim3 wgrid((unsigned)nchunks, (unsigned)rows);
   if (sa.out)
@@ -2351,17 +2367,20 @@ unsigned char* scratch_address(int* err) {
 // capture, tight serving loops, harnesses that forbid hipMalloc). The same arguments without work and counters: the
 // library's static per-GPU scratch holds them, and the call allocates nothing. Each call first zeroes the scratch's
 // counters for its rows with a small kernel (no memset node, so the call may be captured into a graph), then runs
-// launch()'s kernels. -1 as launch(), and also when a split row's results would not fit the scratch (rows * nchunks *
-// k * 8 bytes above 16 MiB, nchunks = ceil(cols / chunk)). Every call on one GPU uses that GPU's one scratch: calls that
+// launch()'s kernels. -1 as launch(), and also when a split row's results would not fit the scratch: more than 16 MiB
+// of u64 slots in the chunking the launch runs (rows * nchunks * k for k > 1, rows * nchunks for k = 1, after k > 64
+// lengthens short chunks and k <= 64 folds a short last one). Every call on one GPU uses that GPU's one scratch: calls that
 // overlap on one GPU (two streams, or two host threads) race and must be ordered by the caller.
 extern "C" int topk_launch_noalloc(const void* x, void* values, void* indices, long long rows, long long cols, int k,
                                    int dtype, int threads, int depth, long long chunk, hipStream_t stream) {
   if (rows <= 0 || k <= 0) return rw_host::kOk;
   if (k > cols || k > kMaxK || cols > INT_MAX / 2 || rows > 65535 || chunk <= 0) return rw_host::kInvalid;
   const long long nchunks = (cols + chunk - 1) / chunk;
-  if (nchunks > 1 && (unsigned long long)rows * (unsigned long long)nchunks * (unsigned long long)k * 8ull >
-                         (unsigned long long)kNoAllocWork)
-    return rw_host::kInvalid;
+  if (nchunks > 1 && (chunk % 4 || nchunks * k > INT_MAX / 2)) return rw_host::kInvalid;  // launch()'s own checks
+  // the slots the launch will use, after its rechunking (the width only matters for short last tiles, and bf16's is
+  // the wider: its fold takes no fewer chunks than fp32's)
+  const Chunking c = chunking(rows, cols, chunk, (int)nchunks, k, dtype == 1 ? Fmt<uint16_t>::W : Fmt<float>::W);
+  if ((unsigned long long)c.slots * 8ull > (unsigned long long)kNoAllocWork) return rw_host::kInvalid;
   int err = rw_host::kOk;
   unsigned char* base = scratch_address(&err);
   if (!base) return err;

@@ -14,10 +14,12 @@
 #include <torch/library.h>
 
 #include <algorithm>
+#include <cstdint>
 #include <mutex>
 #include <string>
 #include <tuple>
 #include <unordered_map>
+#include <utility>
 
 namespace {
 
@@ -278,8 +280,12 @@ void rope_kv_inplace_gpu(at::Tensor& q, const at::Tensor& k_in, const at::Tensor
 
 // ---- top-k (topk/kernel.cu:520-570) and the sampling extensions -----------------------------------------------------
 
-// The caller's side of the top-k launch protocol, kept per device: a zeroed int32 counter array (at least 4096, as the
-// reference's wrapper sizes it) and the plan and workspace of the most recent shape.
+// The caller's side of the top-k launch protocol, kept per (device, stream): a zeroed int32 counter array (at least
+// 4096, as the reference's wrapper sizes it) and the plan and workspace of the most recent shape. A split row's
+// chunks count their arrivals on counters[row] and hand their lists over in work, so two launches in flight at once
+// must not share them: launches on one stream are ordered, and each stream has its own pair. The buffers are
+// allocated while their stream is current and used only on it, so the caching allocator's stream-ordered reuse covers
+// them (a buffer replaced by a larger one is freed behind the launches already queued on that stream).
 struct TopkState {
   at::Tensor counters;
   std::tuple<long long, long long, int, int> shape{-1, -1, -1, -1};
@@ -291,15 +297,23 @@ struct TopkLaunchArgs {
   long long chunk;
   void* work;
   void* counters;
+  hipStream_t stream;
+};
+
+struct TopkKeyHash {
+  size_t operator()(const std::pair<int, uintptr_t>& k) const {
+    return std::hash<uintptr_t>()(k.second) * 31u + (size_t)k.first;
+  }
 };
 
 TopkLaunchArgs topk_plan(const at::Tensor& x, int k) {
   static std::mutex mu;
-  static std::unordered_map<int, TopkState> per_device;
+  static std::unordered_map<std::pair<int, uintptr_t>, TopkState, TopkKeyHash> per_stream;
   std::lock_guard<std::mutex> lock(mu);
   const long long rows = x.size(0), cols = x.size(1);
   const int dtype = x.scalar_type() == at::kFloat ? 0 : 1;
-  TopkState& st = per_device[x.device().index()];
+  const hipStream_t stream = current_stream(x);
+  TopkState& st = per_stream[{(int)x.device().index(), reinterpret_cast<uintptr_t>(stream)}];
   if (!st.counters.defined() || st.counters.numel() < rows)
     st.counters = at::zeros({std::max<long long>(rows, 4096)}, x.options().dtype(at::kInt));
   const auto shape = std::make_tuple(rows, cols, dtype, k);
@@ -311,7 +325,7 @@ TopkLaunchArgs topk_plan(const at::Tensor& x, int k) {
     st.work = at::empty({nchunks > 1 ? rows * nchunks * k : 1}, x.options().dtype(at::kLong));
     st.shape = shape;
   }
-  return {st.chunk, st.work.data_ptr(), st.counters.data_ptr()};
+  return {st.chunk, st.work.data_ptr(), st.counters.data_ptr(), stream};
 }
 
 void topk_checks(const at::Tensor& x, int64_t k, const char* what) {
@@ -331,7 +345,7 @@ std::tuple<at::Tensor, at::Tensor> topk_gpu(const at::Tensor& x_in, int64_t k) {
   const TopkLaunchArgs a = topk_plan(x, (int)k);
   static const auto fn = entry<TopkLaunch>("topk", "launch");
   launched(fn(x.data_ptr(), values.data_ptr(), indices.data_ptr(), a.work, a.counters, x.size(0), x.size(1), (int)k,
-              x.scalar_type() == at::kFloat ? 0 : 1, 256, 4, a.chunk, current_stream(x)),
+              x.scalar_type() == at::kFloat ? 0 : 1, 256, 4, a.chunk, a.stream),
            "topk");
   return {values, indices};
 }
@@ -356,7 +370,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> topk_and_sample_gpu(const at::Ten
   static const auto fn = entry<TopkLaunchSample>("topk", "topk_launch_sample");
   launched(fn(x.data_ptr(), values.data_ptr(), indices.data_ptr(), a.work, a.counters, x.size(0), x.size(1), (int)k,
               x.scalar_type() == at::kFloat ? 0 : 1, 256, 4, a.chunk, u.data_ptr<float>(), drawn.data_ptr(),
-              (float)temperature, (float)top_p, current_stream(x)),
+              (float)temperature, (float)top_p, a.stream),
            "topk_and_sample");
   return {values, indices, drawn};
 }

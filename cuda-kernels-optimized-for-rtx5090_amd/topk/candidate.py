@@ -8,8 +8,8 @@ as in the reference, unless inputs["k"] says otherwise (this build takes 1 <= k 
 Launch protocol, as the reference's: `plan` gives the columns each workgroup scans; when a row spans several chunks,
 the chunks hand their results over through a caller-owned int64 workspace of rows * nchunks * k entries and a
 caller-owned array of int32 per-row counters that starts at zero and that the kernel leaves at zero. This wrapper
-owns both: the workspace of the most recent shape is kept for the next call of that shape, and the counters are one
-zeroed array per device of at least 4096 entries, grown when a call has more rows.
+owns both, per (device, stream): the workspace of the most recent shape is kept for the next call of that shape, and
+the counters are one zeroed array of at least 4096 entries, grown when a call has more rows.
 
 Additions of this build (no counterpart in the reference): sample() draws one index per row from a top-k list, and
 run_and_sample() does the top-k and that draw in one launch.
@@ -80,31 +80,35 @@ _lib.topk_launch_sample.restype = ctypes.c_int
 
 
 class _Buffers:
-    """The caller-side state of the launch protocol: per device one zeroed counter array, and the plan and workspace of
-    the most recent shape. Calls of one shape are queued on one stream, and each split chunk rewrites its workspace
-    slots before its row's merge reads them, so one workspace serves them all."""
+    """The caller-side state of the launch protocol, kept per (device, stream): one zeroed counter array, and the plan
+    and workspace of the most recent shape. Calls on one stream are ordered, and each split chunk rewrites its
+    workspace slots before its row's merge reads them, so one workspace serves a stream's calls; two streams with calls
+    in flight at once must not count arrivals on the same counters, so each stream has its own."""
 
     def __init__(self):
-        self.counters = {}   # device -> int32 zeros
-        self.recent = None   # (key, chunk, work)
+        self.counters = {}   # (device, stream) -> int32 zeros
+        self.recent = {}     # (device, stream) -> (key, chunk, work)
 
-    def counters_for(self, device, rows):
-        c = self.counters.get(device)
+    def counters_for(self, where, device, rows):
+        c = self.counters.get(where)
         if c is None or c.numel() < rows:
             c = torch.zeros(max(rows, 4096), dtype=torch.int32, device=device)
-            self.counters[device] = c
+            self.counters[where] = c
         return c
 
     def plan(self, x, rows, cols, dtype, k):
-        key = (x.device, rows, cols, dtype, k)
-        if self.recent is None or self.recent[0] != key:
-            self.recent = None  # drop the old workspace before making the new one
+        where = (x.device, torch.cuda.current_stream(x.device).cuda_stream)
+        key = (rows, cols, dtype, k)
+        recent = self.recent.get(where)
+        if recent is None or recent[0] != key:
+            self.recent.pop(where, None)  # drop the old workspace before making the new one
             # k > 64 asks for chunks of at least 16k columns (a useful bound per chunk, fewer lists to merge)
             chunk = _lib.plan(rows, cols, dtype, _THREADS, _DEPTH, max(_MIN_CHUNK, 16 * k) if k > 64 else _MIN_CHUNK)
             nchunks = -(-cols // chunk)
             work = torch.empty(rows * nchunks * k if nchunks > 1 else 1, dtype=torch.int64, device=x.device)
-            self.recent = (key, chunk, work)
-        return self.recent[1], self.recent[2], self.counters_for(x.device, rows)
+            recent = (key, chunk, work)
+            self.recent[where] = recent
+        return recent[1], recent[2], self.counters_for(where, x.device, rows)
 
 
 _buffers = _Buffers()

@@ -37,9 +37,10 @@ int launch(const void* x, void* values, void* indices, void* work, void* counter
  * capture, tight serving loops, harnesses that forbid hipMalloc). The same arguments and checks without work and
  * counters, which live in a static scratch of the library, one per GPU, held until the process ends: 256 KiB of row
  * counters and 16 MiB of chunk results. Each call zeroes its counters with a small kernel first (no memset node) and
- * allocates nothing. -1 also when a split row's results would not fit (rows * nchunks * k * 8 bytes above 16 MiB,
- * nchunks = ceil(cols / chunk)). All calls on one GPU share that GPU's scratch: calls that overlap on one GPU (two
- * streams, two host threads) race and must be ordered by the caller. */
+ * allocates nothing. -1 also when a split row's results would not fit: rows * nchunks * k u64 slots (rows * nchunks
+ * for k = 1) above 16 MiB, counted over the chunks the launch runs (k > 64 lengthens chunks shorter than 16k columns,
+ * k <= 64 may fold a short last chunk into the one before). All calls on one GPU share that GPU's scratch: calls that
+ * overlap on one GPU (two streams, two host threads) race and must be ordered by the caller. */
 int topk_launch_noalloc(const void* x, void* values, void* indices, long long rows, long long cols, int k, int dtype,
                         int threads, int depth, long long chunk, hipStream_t stream);
 

@@ -101,6 +101,9 @@ ROPE = [
     ("freq_d24", 9, 3, 1, 24, 1, 3, 0, 8),
     ("cache_d24_in_place", 9, 3, 1, 24, 1, 0, 1, 9),
     ("kv_d256", 5, 2, 2, 256, 1, 4, 0, 10),
+    ("cache_d256_few_heads", 7, 2, 1, 256, 1, 0, 0, 11),     # 128 cache vectors per token over 48 items
+    ("cache_d1024_bf16_cache", 5, 2, 1, 1024, 2, 1, 1, 12),  # the largest vector-path head, a 16-bit cache
+    ("cache_d1040_scalar", 3, 1, 1, 1040, 1, 0, 0, 13),      # beyond it: the scalar kernel
 ]
 
 

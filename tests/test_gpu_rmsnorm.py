@@ -72,16 +72,11 @@ def test_config_rmsnorm_16384x4096(pkg, oracle, dev):
     inp = pkg.workloads.rmsnorm_16384x4096()
     x, w = inp["x"], inp["weight"]
     y = check(pkg, oracle, dev, x, w, inp["eps"], "rmsnorm_16384x4096")
-    # against the reference's torch expression: identical where the rounded inv agrees
+    # against the reference's torch expression (rmsnorm/candidate.py:3-4, weighted as w * y) on the CPU: bit for bit
+    # over all 67M outputs (the oracle equals it there, tests/test_oracle.py)
     from oracle import torch_paths
     ref = bits16(torch_paths.rmsnorm(x, w, inp["eps"]))
-    tinv = bits16(torch.rsqrt(x.float().pow(2).mean(-1) + inp["eps"]).bfloat16())
-    _, inv = oracle.rmsnorm(bits16(x), None, inp["eps"], "bf16", return_inv=True)
-    same = bits16(torch.from_numpy(inv).bfloat16()) == tinv
-    got = bits16(y)
-    assert np.array_equal(got[same], ref[same])
-    assert (~same).mean() < 0.01
-    assert ulp16(got, ref).max() <= 2
+    assert np.array_equal(bits16(y), ref)
 
 
 def test_tuning_overrides_keep_results(pkg, oracle, dev):

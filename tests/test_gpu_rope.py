@@ -107,20 +107,17 @@ def test_config_rope_4x4096_32q_8kv_128(pkg, oracle, dev):
     pkg.rope(qd, kd, pos.to(dev), inv_freq=inv_freq.to(dev), inplace=True)
     rq, rk = oracle.rope_freq(flat(q), flat(k), pos.view(-1).numpy(), inv_freq.numpy())
     assert np.array_equal(flat(qd), rq) and np.array_equal(flat(kd), rk)
-    # against the reference path with a cache built by torch, whose cos/sin may be an fp32 ulp off the correctly
-    # rounded values: identical almost everywhere; where a * cos and b * sin nearly cancel, that fp32 ulp can move
-    # the result by a few bf16 ulps, so the bound is on the absolute error it can cause
+    # The reference's own path: its ABI `launch` with a cos/sin cache built by torch (HF's formula, fp32), against
+    # torch eager's rotation with that cache (rope/candidate.py:3-5) on the CPU, over all 84M outputs of q and k: bit
+    # for bit. (The on-the-fly form above uses correctly rounded cos/sin, which torch's are not everywhere; it differs
+    # from this path in 349 outputs, 21 of them by more than one bf16 ulp, all on near-cancellations:
+    # tests/test_oracle.py pins those counts on the CPU.)
     from oracle import torch_paths
     cos, sin = torch_paths.rope_cache(4096, 128)
-    tq = bits16(torch_paths.rope(q[:1, :1024], cos, sin, pos[:1, :1024]))
-    got = bits16(qd.cpu()[:1, :1024])
-    d = ulp16(got, tq)
-    assert (d == 0).mean() > 0.99
-    gf = torch.from_numpy(got.view(np.int16)).view(torch.bfloat16).float()
-    tf = torch.from_numpy(tq.view(np.int16)).view(torch.bfloat16).float()
-    xa = q[:1, :1024].float().abs()
-    pair = xa + torch.cat((xa[..., 64:], xa[..., :64]), -1)
-    assert ((gf - tf).abs() <= tf.abs() * 2 ** -7 + pair * 2 ** -22).all()
+    print("[rope] config, reference ABI with torch's fp32 cache, against torch eager", flush=True)
+    qo, ko = pkg.rope(q.to(dev), k.to(dev), pos.to(dev), cos=cos.to(dev), sin=sin.to(dev))
+    assert np.array_equal(bits16(qo), bits16(torch_paths.rope(q, cos, sin, pos)))
+    assert np.array_equal(bits16(ko), bits16(torch_paths.rope(k, cos, sin, pos)))
     # the cache form of the same call agrees with the on-the-fly form over the oracle's table
     ct, st = oracle.rope_table(inv_freq.numpy(), 4096, 128)
     qo, ko = pkg.rope(q.to(dev), k.to(dev), pos.to(dev), cos=torch.from_numpy(ct).to(dev),

@@ -238,7 +238,7 @@ def test_workspace_reuse_and_wrapper(pkg, oracle, dev):
         v, ix = pkg.topk(x.to(dev), 50)
         rv, ri = oracle.topk(x.numpy(), 50)
         assert np.array_equal(ix.cpu().numpy(), ri) and np.array_equal(v.cpu().numpy(), rv)
-    counters = pkg.candidate("topk")._buffers.counters[dev]
+    counters = pkg.candidate("topk")._buffers.counters[(dev, torch.cuda.current_stream(dev).cuda_stream)]
     assert (counters == 0).all()
     assert lib(pkg).topk_reset(counters.data_ptr(), counters.numel(), torch.cuda.current_stream().cuda_stream) == 0
 

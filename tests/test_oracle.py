@@ -109,6 +109,17 @@ def test_rmsnorm_matches_torch_path(oracle, dtype):
     _check_rms_against_torch(oracle, x, w, name)
 
 
+def test_rmsnorm_c2_whole_config_equals_torch(oracle, pkg):
+    """The whole C2 config (x [16384, 4096] bf16, w [4096], eps 1e-6): the oracle equals the reference's torch
+    expression (rmsnorm/candidate.py:3-4, weighted as torch's w * y) bit for bit on all 67,108,864 outputs, weighted
+    and plain."""
+    from oracle import torch_paths
+    inp = pkg.workloads.rmsnorm_16384x4096()
+    x, w, eps = inp["x"], inp["weight"], inp["eps"]
+    assert np.array_equal(oracle.rmsnorm(bits16(x), bits16(w), eps, "bf16"), bits16(torch_paths.rmsnorm(x, w, eps)))
+    assert np.array_equal(oracle.rmsnorm(bits16(x), None, eps, "bf16"), bits16(torch_paths.rmsnorm(x, None, eps)))
+
+
 def test_rmsnorm_closed_forms(oracle):
     # constant row a: sum = n a^2 exactly, so every step is one fp32 rounding of a known value
     n, eps = 64, np.float32(1e-6)
@@ -246,6 +257,39 @@ def test_rope_freq_vs_torch_cache(oracle):
     xa = q.float().abs()
     pair = xa + torch.cat((xa[..., 64:], xa[..., :64]), -1)
     assert ((of - tf).abs() <= tf.abs() * 2 ** -7 + pair * 2 ** -22).all()
+
+
+def test_rope_c3_on_the_fly_vs_torch_cache_whole_config(oracle, pkg):
+    """The whole C3 config (q [4, 4096, 32, 128] and k [4, 4096, 8, 128] bf16, positions 0..4095, theta 1e4): the
+    on-the-fly form (cos/sin of the fp32 angle, correctly rounded from fp64) against the reference's PyTorch path with
+    a cos/sin cache built by torch, over all 83,886,080 outputs. torch's cos/sin differ from the correctly rounded
+    values by one fp32 ulp in about 5% of the cache's entries. That moves 349 outputs (274 of q, 75 of k) by at least
+    one bf16 ulp. 21 move by more than one ulp (15 of q, at most 32 ulp; 6 of k, at most 26,112 ulp), each where
+    a * cos and b * sin nearly cancel, so the difference is tiny in absolute terms: the bound below is the error an
+    fp32 ulp of cos or sin can cause, plus the output's own rounding."""
+    from oracle import torch_paths
+    inp = pkg.workloads.rope_4x4096_32q_8kv_128()
+    q, k, pos, inv = inp["q"], inp["k"], inp["position_ids"], inp["inv_freq"]
+    assert torch.equal(inv, torch_paths.inv_freq(128))
+    oq, ok = oracle.rope_freq(bits16(q).reshape(-1, 32, 128), bits16(k).reshape(-1, 8, 128), pos.view(-1).numpy(),
+                              inv.numpy())
+    cos, sin = torch_paths.rope_cache(4096, 128)
+    ct, st = oracle.rope_table(inv.numpy(), 4096, 128)
+    off = (ct != cos.numpy()).mean(), (st != sin.numpy()).mean()
+    assert 0.03 < off[0] < 0.08 and 0.03 < off[1] < 0.08, off
+    total_beyond = 0
+    for x, o, name, n1, nmax in ((q, oq, "q", 274, 32), (k, ok, "k", 75, 26112)):
+        t = torch_paths.rope(x, cos, sin, pos)
+        d = ulp16(o.reshape(-1), bits16(t).reshape(-1))
+        assert (d > 0).sum() == n1, (name, int((d > 0).sum()))
+        assert d.max() == nmax, (name, int(d.max()))
+        total_beyond += int((d > 1).sum())
+        of = torch.from_numpy(o.reshape(t.shape).view(np.int16)).view(torch.bfloat16).float()
+        tf = t.float()
+        xa = x.float().abs()
+        pair = xa + torch.cat((xa[..., 64:], xa[..., :64]), -1)
+        assert ((of - tf).abs() <= tf.abs() * 2 ** -7 + pair * 2 ** -22).all(), name
+    assert total_beyond == 21
 
 
 def test_rope_kv_scatter_semantics(oracle):

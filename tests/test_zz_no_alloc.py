@@ -50,6 +50,13 @@ def test_noalloc_rejects_beyond_its_scratch(pkg, dev):
     out = torch.empty(128, 1024, device=dev)
     idx = torch.empty(128, 1024, dtype=torch.int64, device=dev)
     s = torch.cuda.current_stream().cuda_stream
-    # 32 chunks per row: 128 * 32 * 1024 * 8 bytes = 32 MiB of chunk results, beyond the 16 MiB scratch
-    assert fn(x.data_ptr(), out.data_ptr(), idx.data_ptr(), 128, 128256, 1024, 0, 256, 4, 4096, s) == -1
+    # k > 64 lengthens the caller's 4096-column chunks to 16384 (16k): 8 chunks per row. 128 rows need 128 * 8 * 1024
+    # u64 slots = 8 MiB, within the 16 MiB scratch; 512 rows need 32 MiB, beyond it
+    xl = torch.zeros(512, 128256, device=dev)
+    outl = torch.empty(512, 1024, device=dev)
+    idxl = torch.empty(512, 1024, dtype=torch.int64, device=dev)
+    assert fn(xl.data_ptr(), outl.data_ptr(), idxl.data_ptr(), 512, 128256, 1024, 0, 256, 4, 4096, s) == -1
+    assert fn(x.data_ptr(), out.data_ptr(), idx.data_ptr(), 128, 128256, 1024, 0, 256, 4, 4096, s) == 0
+    torch.cuda.synchronize()
+    assert (idx == torch.arange(1024, device=dev)).all(), "all-zero rows: indices 0..k-1"
     assert fn(x.data_ptr(), out.data_ptr(), idx.data_ptr(), 0, 128256, 1024, 0, 256, 4, 4096, s) == 0
