@@ -54,7 +54,7 @@ KERNELS = {"rmsnorm_16384x4096": "rmsnorm_rows", "softmax_4096x4096": "softmax_r
            "softmax_64x262144": "softmax_coop", "rope_4x4096_32q_8kv_128": "rope_vec",
            "topk_128x128256_k1": "topk_one", "topk_128x128256_k50": "topk_tile",
            "topk_128x128256_k1024": "topk_wide", "rmsnorm_add_16384x4096": "rmsnorm_rows",
-           "rope_kv_4x4096_32q_8kv_128": "rope_vec"}
+           "rope_kv_4x4096_32q_8kv_128": "rope_vec", "rope_cache_4x4096_32q_8kv_128": "rope_vec"}
 
 
 def parse():
@@ -160,6 +160,19 @@ class Case:
                                                   inv.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
                                                   slots.data_ptr(), B * S, Hq, Hk, D, 1, stream())
             footprint = (inp["q"].numel() + 4 * inp["k"].numel()) * 2
+        elif name.startswith("rope_cache"):
+            lib = pkg.candidate("rope")._lib
+            B, S, Hq, D = inp["q"].shape
+            Hk = inp["k"].shape[2]
+            pos, cos, sin = inp["position_ids"].to(dev), inp["cos"].to(dev), inp["sin"].to(dev)
+            self.dtype = "bf16"
+
+            def make():
+                # the reference's ABI: cos/sin read from the fp32 cache; in place
+                q, kk = inp["q"].to(dev), inp["k"].to(dev)
+                return lambda: lib.launch(q.data_ptr(), kk.data_ptr(), cos.data_ptr(), sin.data_ptr(), pos.data_ptr(),
+                                          q.data_ptr(), kk.data_ptr(), B * S, Hq, Hk, D, 1, 0, 40, 1, stream())
+            footprint = 2 * (inp["q"].numel() + inp["k"].numel()) * 2
         elif name.startswith("rope"):
             lib = pkg.candidate("rope")._lib
             B, S, Hq, D = inp["q"].shape
@@ -314,6 +327,11 @@ def cpu_paths(pkg, name, k):
                 vc.index_copy_(0, slots, v.reshape(tokens, 8, 128))
                 return qo
             return "cos/sin, rotation of q and k, cache scatter of k and v over 16384 tokens", rope_kv
+        if name.startswith("rope_cache"):
+            cos, sin = inp["cos"], inp["sin"]
+            return "the rotation of q[4, 4096, 32, 128] and k[4, 4096, 8, 128] bf16 with cos/sin gathered from the " \
+                   "fp32 cache [4096, 128]", lambda: (torch_paths.rope(q, cos, sin, pos),
+                                                      torch_paths.rope(kk, cos, sin, pos))
         return "cos/sin and the rotation of q[4, 4096, 32, 128] and k[4, 4096, 8, 128] bf16", rope
     if name == "topk_sample_128x128256":
         x, u = inp["x"], inp["uniforms"]

@@ -302,8 +302,12 @@ static_assert(kTileSort == kThreads, "the rank sort and the merge heads use one 
 
 typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
 
+constexpr int kStageGroups = 64;  // each wave's staged 8-element groups in a filter pass (Tile::filter_groups)
+
 struct TileSmem {
   u64 seg[kWaves][kTileSeg + 2];  // (+ a spare slot for a batch's writes past the end, padded to 16 bytes)
+  u32x4 stage[kWaves][2 * kStageGroups];  // filter_groups: each wave's staged groups, 8 fp32 elements each
+  uint32_t stage_at[kWaves][kStageGroups];  // and the index of each staged group's first element
   alignas(16) u64 sorted[kTileSort];
   u64 top[kSeedMaxK];  // an output row's composites in order (for the fused draw)
   uint32_t red[2][kWaves];
@@ -711,8 +715,15 @@ __device__ __forceinline__ void stage_stamp(int slot) {
   } while (0)
 #endif
 
-// A register tile: thread t of the workgroup's NT holds vectors v * NT + t (v < NV) of elements [b0, b1) of a row, W
-// each, as raw bits; an element outside [b0, b1) holds the sentinel (all ones: the -NaN whose key is the smallest of
+// Orders one wave's LDS writes before its later LDS reads of other lanes' entries (a wave's LDS operations execute in
+// order; this keeps the compiler from moving them across).
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// A register tile: thread t of the workgroup's NT holds vectors v * NT + t (v < NV = EPL / W) of elements [b0, b1) of a
+// row, W each, as raw bits; an element outside [b0, b1) holds the sentinel (all ones: the -NaN whose key is the smallest of
 // its format), read from g_sentinel_vec by a vector load past the end. load() only issues the loads.
 //
 // The raw bits are ordered without forming keys: over non-negative values key order is the signed order of the bits
@@ -721,10 +732,10 @@ __device__ __forceinline__ void stage_stamp(int slot) {
 // integer, is the largest negative one: it never moves the minimum of a set holding a real element); and for a
 // threshold key K with bits t, key(u) >= K iff (int)u >= (int)t when K is a non-negative value, iff u <= t (unsigned)
 // when K is negative.
-template <typename T, bool VEC, int NT = kThreads>
+template <typename T, bool VEC, int NT = kThreads, int EPL = kTileE>
 struct Tile {
   static constexpr int W = Fmt<T>::W;
-  static constexpr int NV = kTileE / W;
+  static constexpr int NV = EPL / W;
   static constexpr uint32_t kSentinelKey = sizeof(T) == 4 ? 0u : 0xffffu;  // key of the sentinel
   u32x4 r[NV];
   int b0, b1;
@@ -745,7 +756,7 @@ struct Tile {
 
   __device__ __forceinline__ void load(const T* row, int t0, int end) {
     b0 = t0;
-    b1 = end - t0 > NT * kTileE ? t0 + NT * kTileE : end;
+    b1 = end - t0 > NT * EPL ? t0 + NT * EPL : end;
     lane0 = b0 + (int)threadIdx.x * W;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
@@ -859,6 +870,59 @@ struct Tile {
           if constexpr (NEG) return comp(v, j);
           return ((u64)(bits(v, j) | 0x80000000u) << 32) | (u64)(nl - (uint32_t)(v * NT * W + j));
         });
+    }
+  }
+
+  // filter() for a non-negative threshold key K over fp32 tiles, by groups of 8 elements (two vectors): a group whose
+  // signed maximum of the raw bits is below K's bits holds no element with key >= K (over a non-negative threshold
+  // the key order is the signed order of the bits, and a negative element's bits are negative), so only the groups
+  // reaching it are staged, each by its lane, into the wave's LDS area (two 16-byte writes and the group's first index;
+  // positions from a ballot per group), and the wave then tests the staged elements exactly, 64 at a time, pushing
+  // the admitted ones. A group reaching K holds about one admitted element: per wave a compare per group and a push
+  // per 64 staged elements, instead of a compare per element and a push per element position that any lane admits. A
+  // wave with more than kStageGroups groups to stage (ties, adversarial orders) takes the per-element filter.
+  template <typename Lst>
+  __device__ __forceinline__ void filter_groups(Lst& L, uint32_t K, u32x4* stage, uint32_t* stage_at) {
+    static_assert(sizeof(T) == 4, "fp32 tiles: two vectors per group");
+    constexpr int NG = NV / 2;
+    const int t = (int)bits_of(K);  // >= 0
+    const int lane = lane_id();
+    int n = 0;  // wave-uniform
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      int gm = INT_MIN;
+#pragma unroll
+      for (int v = 2 * g; v < 2 * g + 2; ++v)
+#pragma unroll
+        for (int j = 0; j < W; ++j) gm = (int)r[v][j] > gm ? (int)r[v][j] : gm;
+      const bool c = gm >= t;
+      const u64 m = __ballot(c);
+      if (m) {
+        if (c) {
+          const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)n));
+          if (pos < kStageGroups) {
+            stage[2 * pos] = r[2 * g];
+            stage[2 * pos + 1] = r[2 * g + 1];
+            stage_at[pos] = (uint32_t)first(2 * g);
+          }
+        }
+        n += __popcll(m);
+      }
+    }
+    if (n > kStageGroups) {
+      filter<false>(L, K);
+      return;
+    }
+    wave_lds_sync();  // the wave's staging writes before its reads of other lanes' entries
+    const uint32_t* su = reinterpret_cast<const uint32_t*>(stage);
+    for (int b = 0; b < 8 * n; b += kWave) {  // wave-uniform trip count
+      const int i = b + lane, slot = i >> 3, e = i & 7;
+      const bool ok = i < 8 * n;
+      const uint32_t u = su[ok ? i : 0];
+      const uint32_t at = stage_at[ok ? slot : 0] + (uint32_t)((e >> 2) * NT * W + (e & 3));
+      // over a non-negative threshold the key of an admitted element is its bits with the top bit set
+      L.push(((u64)(u | 0x80000000u) << 32) | (u64)(~at), ok && (int)u >= t);
     }
   }
 
@@ -1008,13 +1072,6 @@ struct Tile {
     asm volatile("" : "+v"(lane0));
   }
 };
-
-// Orders one wave's LDS writes before its later LDS reads of other lanes' entries (a wave's LDS operations execute in
-// order; this keeps the compiler from moving them across).
-__device__ __forceinline__ void wave_lds_sync() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_wave_barrier();
-}
 
 // k <= 64 merge of a split row (the row's last workgroup). Every chunk list holds its chunk's k largest, descending,
 // so the first h = ceil(k / nchunks) entries of the lists give nchunks * h >= k distinct composites: the k-th largest
@@ -1273,19 +1330,21 @@ __device__ __forceinline__ void sample_top(const SampleArgs& sa, float u, const 
 
 // ---- the k = 1 kernel ----------------------------------------------------------------------------------------------
 
-constexpr int kOneThreads = 1024;                   // threads of a k = 1 workgroup
-constexpr int kOneChunks = kOneThreads / kThreads;  // consecutive chunks of the caller's chunking per k = 1 workgroup
+constexpr int kOneThreads = 1024;  // threads of a k = 1 workgroup
+constexpr int kOneE = 32;          // elements per lane of its register tile (32768 per workgroup)
+constexpr int kOneChunks = 2;      // consecutive chunks of the caller's chunking per k = 1 workgroup
 
 // k = 1: one 1024-thread workgroup per kOneChunks consecutive chunks of a row (the result does not depend on the
-// chunking), in register tiles of 65536 elements, all of a tile's loads in flight at once. Each lane's largest
+// chunking), in register tiles of 32768 elements, all of a tile's loads in flight at once. Each lane's largest
 // composite comes straight from its registers (no bound, list or block reduction per tile), then the wave's and,
 // through LDS, the workgroup's. A row split over several workgroups hands over as topk_tile's chunks do: each stores
 // its best in the work slot of its group (work[row * nchunks + group], inside the caller's [rows, nchunks] slots),
 // waits for the store and counts its arrival on counters[row]; the row's last arrival takes the largest slot and
 // zeroes the counter.
-// A workgroup of four chunks makes a quarter of the arrivals of one per chunk (the caller's counters pack 32 rows
-// into a 128-byte line, whose device-scope adds are performed one after another) and leaves the merge a quarter of
-// the slots.
+// The shape is measured (interleaved runs on one MI355X, 128 x 128256 fp32): eight 16-byte loads per lane in two
+// resident workgroups of sixteen waves per CU, 13.49 us, against sixteen loads per lane in one (65536-element tiles
+// over four chunks) 13.95 us, 512 threads over one chunk 13.82 us, 1024 threads with four loads per lane over one
+// chunk 14.77 us.
 template <typename T, bool VEC, bool DRAW>
 __global__ void __launch_bounds__(kOneThreads)
     topk_one(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
@@ -1299,8 +1358,8 @@ __global__ void __launch_bounds__(kOneThreads)
   const int end = (int)(group == groups - 1 ? cols : begin + kOneChunks * chunk);  // the last group ends the row
   const T* xr = x + row * cols;
   TOPK_STAGE(0);
-  using TL = Tile<T, VEC, kOneThreads>;
-  constexpr int TE = kOneThreads * kTileE;
+  using TL = Tile<T, VEC, kOneThreads, kOneE>;
+  constexpr int TE = kOneThreads * kOneE;
   u64 best = 0;
   for (int t0 = begin; t0 < end; t0 += TE) {
     TL tile;
@@ -1387,8 +1446,12 @@ __global__ void __launch_bounds__(kThreads)
     const int cnt0 = L.cnt;
     tile.opaque();
     if (thr > TL::kSentinelKey) {
-      if (thr & 0x80000000u) tile.template filter<false>(L, thr);
-      else tile.template filter<true>(L, thr);
+      if (thr & 0x80000000u) {
+        if constexpr (sizeof(T) == 4) tile.filter_groups(L, thr, s.stage[wave_id()], s.stage_at[wave_id()]);
+        else tile.template filter<false>(L, thr);
+      } else {
+        tile.template filter<true>(L, thr);
+      }
     } else {
       L.cnt = kTileSeg + 1;  // no usable bound: every element may pass, so the tile takes the exact re-push path
     }

@@ -2,7 +2,8 @@
 
 Inputs are drawn on the CPU from a seeded torch.Generator (so every run and every machine sees the same values) and
 moved to the device by the caller. `algorithmic_bytes` is the minimum HBM traffic of one call: every input element
-read once and every output element written once (cos/sin are computed on the fly for RoPE; workspaces excluded).
+read once and every output element written once (cos/sin are computed on the fly for RoPE, except in the cache
+workload, which reads each cache entry once; workspaces excluded).
 """
 
 import torch
@@ -63,6 +64,17 @@ def rope_kv_4x4096_32q_8kv_128():
     return inp
 
 
+def rope_cache_4x4096_32q_8kv_128():
+    """RoPE bf16 in place through the reference's ABI `launch`, cos/sin read from an fp32 cache [4096, 128] built by
+    HF's formula (emb = cat(outer(pos, inv_freq)) twice, cos and sin in fp32), over the rope_4x4096_32q_8kv_128
+    inputs."""
+    inp = rope_4x4096_32q_8kv_128()
+    freqs = torch.outer(torch.arange(4096, dtype=torch.int64).float(), inp["inv_freq"])
+    emb = torch.cat((freqs, freqs), dim=-1)
+    inp["cos"], inp["sin"] = emb.cos(), emb.sin()
+    return inp
+
+
 def softmax_64x262144():
     """Long-row softmax fp32: x[64, 262144] ~ N(0, 5^2) with exactly 1% of the entries set to +20, seed 1."""
     g = torch.Generator().manual_seed(1)
@@ -102,6 +114,9 @@ def algorithmic_bytes(name, k=50):
         return 2 * (4 * 4096 * 32 * 128 + 2 * 4 * 4096 * 8 * 128) * 2 + 2 * 4 * 4096 * 8
     if name == "rope_4x4096_32q_8kv_128":
         return 2 * (4 * 4096 * 32 * 128 + 4 * 4096 * 8 * 128) * 2 + 4 * 4096 * 8
+    if name == "rope_cache_4x4096_32q_8kv_128":
+        # the on-the-fly workload's bytes plus the fp32 cos and sin caches [4096, 128], each read once
+        return algorithmic_bytes("rope_4x4096_32q_8kv_128") + 2 * 4096 * 128 * 4
     if name == "topk_sample_128x128256":
         # the logits read once, the uniforms read, the top-k list (fp32 values, int64 indices) and the drawn int64
         # indices written; the draw reads the list from the launch's own LDS or L2, not from HBM
@@ -119,5 +134,6 @@ WORKLOADS = {
     "topk_128x128256": topk_128x128256,
     "rmsnorm_add_16384x4096": rmsnorm_add_16384x4096,
     "rope_kv_4x4096_32q_8kv_128": rope_kv_4x4096_32q_8kv_128,
+    "rope_cache_4x4096_32q_8kv_128": rope_cache_4x4096_32q_8kv_128,
     "topk_sample_128x128256": topk_sample_128x128256,
 }

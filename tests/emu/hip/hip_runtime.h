@@ -61,6 +61,29 @@ struct float2 {
   float x, y;
 };
 inline float2 make_float2(float a, float b) { return float2{a, b}; }
+// Raw buffer resources: a base and a byte extent; a load returns zeros for the dwords at or past the extent.
+struct __amdgpu_buffer_rsrc_t {
+  const char* base;
+  long long bytes;
+};
+inline __amdgpu_buffer_rsrc_t emu_make_buffer_rsrc(void* base, short, int bytes, int) {
+  return __amdgpu_buffer_rsrc_t{static_cast<const char*>(base), (long long)(unsigned)bytes};
+}
+#define __builtin_amdgcn_make_buffer_rsrc(b, s, n, f) emu_make_buffer_rsrc((b), (s), (n), (f))
+typedef unsigned emu_u32x4 __attribute__((ext_vector_type(4)));
+inline emu_u32x4 emu_raw_buffer_load_b128(const __amdgpu_buffer_rsrc_t& r, int voff, int soff, int) {
+  const long long off = (long long)(unsigned)voff + (long long)(unsigned)soff;
+  emu_u32x4 v = {0u, 0u, 0u, 0u};
+  for (int i = 0; i < 4; ++i) {
+    if (off + 4 * i + 4 <= r.bytes) {
+      unsigned u;
+      std::memcpy(&u, r.base + off + 4 * i, 4);
+      v[i] = u;
+    }
+  }
+  return v;
+}
+#define __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, aux) emu_raw_buffer_load_b128((r), (vo), (so), (aux))
 struct alignas(16) float4 {
   float x, y, z, w;
 };
@@ -116,6 +139,7 @@ struct State {
   unsigned long long switches = 0, inactive_reads = 0;
   int shuffle_seed = -1;
   std::mt19937 rng{1};
+  char* stacks = nullptr;  // the fibers' stacks, kStack each
 };
 // The calling OS thread's state (a workgroup's thread in concurrent mode takes one from a pool).
 inline State*& tls_state() {
@@ -349,10 +373,16 @@ inline void run_block() {
   for (int i = 0; i < s.n; ++i) {
     Fiber& f = s.fib[i];
     if (!f.stack) {
-      char* base = (char*)mmap(nullptr, kStack + 4096, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS, -1, 0);
-      if (base == MAP_FAILED) fail("stack mmap", 0);
-      mprotect(base, 4096, PROT_NONE);
-      f.stack = base + 4096;
+      // the stacks of a workgroup's fibers in one mapping (one mapping each would pass the process's mapping limit
+      // with a few dozen 1024-thread workgroups at once), a guard page below the lowest
+      if (!s.stacks) {
+        char* base = (char*)mmap(nullptr, kMaxThreads * kStack + 4096, PROT_READ | PROT_WRITE,
+                                 MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
+        if (base == MAP_FAILED) fail("stack mmap", 0);
+        mprotect(base, 4096, PROT_NONE);
+        s.stacks = base + 4096;
+      }
+      f.stack = s.stacks + (size_t)i * kStack;
     }
     f.done = false;
     f.started = false;
