@@ -491,7 +491,9 @@ def build_topk_stages():
 TOPK_STAGES = {
     "topk_one": [(0, "start"), (1, "loads landed (wave 0)"), (2, "workgroup's best"), (3, "arrival counted"),
                  (8, "row written")],
-    "topk_tile": [(0, "start"), (1, "loads landed (wave 0)"), (2, "threshold"), (3, "tile filtered and settled"),
+    "topk_tile": [(0, "start"), (1, "loads landed (wave 0)"), (11, "wave 0's bound"), (2, "threshold"),
+                  (9, "tile filtered"),
+                  (10, "list settled"), (3, "chunk's tiles done"),
                   (4, "chunk list published"), (5, "arrival counted"), (6, "merge: floor, candidates counted"),
                   (7, "merge: candidates compacted"), (8, "row written")],
     "topk_wide": [(0, "start"), (1, "loads landed (wave 0)"), (2, "bounds"), (3, "tile appended"), (4, "cut to k"),

@@ -690,28 +690,42 @@ __device__ u32x4 g_sentinel_vec = {~0u, ~0u, ~0u, ~0u};
 // into its own library; the op library is built without it, and there TOPK_STAGE and TOPK_WAVE_STAGE compile to
 // nothing). Thread 0 of each workgroup records the 100 MHz s_memrealtime clock at stage i of its kernel in slot i of
 // the workgroup's row of stamps, and lane 0 of each wave the moment its tile's loads have landed in slot 16 + wave.
+// The clock is read by an asm statement after the LDS operations before it have completed; a stamp that follows
+// register work (TOPK_STAGE_AT, TOPK_WAVE_STAGE_AT) first takes that work's result as an asm operand, so the compiler
+// cannot read the clock before the work is done (it may move the clock builtin freely).
 #ifdef ROWKERN_TOPK_STAGES
 constexpr long long kStageWGs = 4096;  // workgroups with stamps (blockIdx.y * gridDim.x + blockIdx.x below this)
 constexpr int kStageSlots = 32;
 __device__ unsigned long long g_stage_stamps[kStageWGs * kStageSlots];
 __device__ __forceinline__ void stage_stamp(int slot) {
   const long long wg = (long long)blockIdx.y * gridDim.x + blockIdx.x;
-  if (wg < kStageWGs) g_stage_stamps[wg * kStageSlots + slot] = __builtin_amdgcn_s_memrealtime();
+  unsigned long long t;
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t) : : "memory");
+  if (wg < kStageWGs) g_stage_stamps[wg * kStageSlots + slot] = t;
 }
 #define TOPK_STAGE(i) \
   do {                              \
     if (threadIdx.x == 0) stage_stamp(i); \
   } while (0)
-#define TOPK_WAVE_STAGE()                                                                       \
+#define TOPK_STAGE_AT(i, v)                \
+  do {                                     \
+    asm volatile("" : : "v"(v) : "memory"); \
+    TOPK_STAGE(i);                         \
+  } while (0)
+#define TOPK_WAVE_STAGE_AT(v)                                                                   \
   do {                                                                                          \
+    asm volatile("" : : "v"(v) : "memory");                                                     \
     if ((threadIdx.x & 63) == 0 && (threadIdx.x >> 6) < 16) stage_stamp(16 + (int)(threadIdx.x >> 6)); \
   } while (0)
 #else
 #define TOPK_STAGE(i) \
   do {                \
   } while (0)
-#define TOPK_WAVE_STAGE() \
-  do {                    \
+#define TOPK_STAGE_AT(i, v) \
+  do {                      \
+  } while (0)
+#define TOPK_WAVE_STAGE_AT(v) \
+  do {                        \
   } while (0)
 #endif
 
@@ -1367,8 +1381,8 @@ __global__ void __launch_bounds__(kOneThreads)
     const u64 c = tile.best_composite();
     best = c > best ? c : best;
   }
-  TOPK_STAGE(1);
-  TOPK_WAVE_STAGE();
+  TOPK_STAGE_AT(1, best);
+  TOPK_WAVE_STAGE_AT(best);
   best = wave_ext64<true>(best);
   if (lane_id() == 0) best_of[wave_id()] = best;
   __syncthreads();
@@ -1436,9 +1450,10 @@ __global__ void __launch_bounds__(kThreads)
   auto process = [&](TL& tile, bool more) __attribute__((always_inline)) {
     const bool has = tile.lane0 < tile.b1;
     const uint32_t m = tile.max_key();  // vector by vector as the loads complete
-    TOPK_STAGE(1);
-    TOPK_WAVE_STAGE();
+    TOPK_STAGE_AT(1, m);
+    TOPK_WAVE_STAGE_AT(m);
     const uint32_t tw = __popcll(__ballot(has)) >= kw ? wave_kth32(m, has, kw) : 0u;
+    TOPK_STAGE_AT(11, tw);
     const uint32_t tb = red.min(tw);
     TOPK_STAGE(2);
     thr = tb > thr ? tb : thr;
@@ -1455,10 +1470,12 @@ __global__ void __launch_bounds__(kThreads)
     } else {
       L.cnt = kTileSeg + 1;  // no usable bound: every element may pass, so the tile takes the exact re-push path
     }
+    TOPK_STAGE_AT(9, L.cnt);
     int total = 0;
     u64 kth = L.settle(
         red, k, cnt0, TL::NV, (u64)thr << 32,
         [&](int v, const u64& floor, const auto& check) { tile.push_first(L, v, floor, check); }, total);
+    TOPK_STAGE(10);
     // before another tile, keep the list near k so that it admits less: the list's k-th raises the admission key
     if (more && total > 2 * k) kth = prune_ranked(s, L, k);
     const uint32_t kk = (uint32_t)(kth >> 32);
@@ -1936,8 +1953,8 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     const int cnt0 = s.count;  // block-uniform: the buffer is settled between tiles
     uint32_t g[kWideGroups];
     tile.group_keys(g);
-    TOPK_STAGE(1);
-    TOPK_WAVE_STAGE();
+    TOPK_STAGE_AT(1, g[0]);
+    TOPK_WAVE_STAGE_AT(g[0]);
     const bool last_tile = end - t0 <= TE;
     if (last_tile && nchunks > 1) {
       // the cut's counters, zeroed ahead of the bounds' barriers while no wave appends (the buffer holds at most
