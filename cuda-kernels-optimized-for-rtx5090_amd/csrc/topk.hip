@@ -42,6 +42,7 @@ struct Smem {
   u64 red[kWaves];
   u64 red2[kWaves];  // reductions of two values at one barrier (with red), and of a second pair (with wsum)
   u64 red3[kWaves];
+  u64 red4[kWaves];
   u64 thr;       // admit composites >= thr (>= 1: composite 0 is never admitted)
   int count;     // composites in buf
   int bin;       // narrowing: the bin holding the wanted rank
@@ -1040,10 +1041,23 @@ struct Tile {
         }
   }
 
-  // Appends the elements of vector v, held in r[0], with composites >= floor to s.buf (exact validity; the caller
-  // keeps room for them); then moves the later vectors down one place (as push_first).
+  // The lane's elements with composites in [lo, hi].
+  __device__ __forceinline__ int count_range(u64 lo, u64 hi) const {
+    int n = 0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        const u64 c = comp(v, j);
+        n += (VEC ? first(v) < b1 : first(v) + j < b1) && c >= lo && c <= hi ? 1 : 0;
+      }
+    return n;
+  }
+
+  // Appends the elements of vector v, held in r[0], with composites in [floor, top] to s.buf (exact validity; the
+  // caller keeps room for them); then moves the later vectors down one place (as push_first).
   template <typename S>
-  __device__ __forceinline__ void append_first(S& s, int v, u64 floor) {
+  __device__ __forceinline__ void append_first(S& s, int v, u64 floor, u64 top = ~0ull) {
     const int e0 = first(v);
     u64 c[W];
     bool keep[W];
@@ -1051,7 +1065,7 @@ struct Tile {
 #pragma unroll
     for (int j = 0; j < W; ++j) {
       c[j] = ((u64)key_of(bits(0, j)) << 32) | (u64)(~(uint32_t)(e0 + j));
-      keep[j] = (VEC ? e0 < b1 : e0 + j < b1) && c[j] >= floor;
+      keep[j] = (VEC ? e0 < b1 : e0 + j < b1) && c[j] >= floor && c[j] <= top;
       any |= keep[j];
     }
     if (__ballot(any)) append<W>(s, c, keep);
@@ -1516,6 +1530,8 @@ __global__ void __launch_bounds__(kThreads)
 constexpr int kWideCap = 4096;    // the wide kernel's candidate buffer (composites)
 constexpr int kWideList = 2048;   // the most candidates ranked at once (write_ranked)
 constexpr int kWideMaxChunks = 256;
+constexpr int kListSlack = 64;  // a split row's chunk publishes twice its share of k and kListSlack more (at most k)
+constexpr int kAgainE = 32;     // elements per lane of the merger's tiles when it reads chunks again from x
 
 constexpr int kRankBuckets = 4096;  // buckets of write_ranked (16-bit counters and first positions)
 
@@ -1650,16 +1666,17 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
 }
 
 // Writes the k largest of a chunk's m candidates s.buf[0, m) (k < m <= kWideList) to list[0, k) with device-coherent
-// stores, in no particular order, and returns (a lower bound of) the k-th largest, block-uniform: the candidates stay
-// in registers from one read. Their keys are counted in kRankBuckets 16-bit LDS counters, bucket (hi - key) >> sh,
+// stores, in no particular order, and returns the k-th largest (the smallest written), block-uniform: the candidates
+// stay in registers from one read. Their keys are counted in kRankBuckets 16-bit LDS counters, bucket (hi - key) >> sh,
 // with [lo, hi] the caller's range of the keys (hi the chunk's largest, lo its admission key; a candidate below lo,
 // kept from an earlier tile, counts in the last bucket) and sh set so that it fills them. A scan finds the bucket B
 // holding the k-th. When B is kept whole (the usual case: about m / kRankBuckets members), everything in buckets up to
-// B is kept and B's lower edge is returned; otherwise B's members are gathered and ranked among themselves for the
-// k-th. Each thread stores its kept candidates at positions from a block scan of the kept counts. A bucket of more than
-// kThreads members (values clustered far below an outlier) takes the general prune (histogram narrowing) and stores the
-// buffer. `zeroed`: the caller has zeroed the counters (s.buf[kWideList, kWideList + kRankBuckets / 4)) and s.members
-// behind a barrier. Every thread calls it; the block is synchronized on entry (the caller's) and on return.
+// B is kept and the k-th is the smallest of B, from a reduction over the kept candidates; otherwise B's members are
+// gathered and ranked among themselves for the k-th. Each thread stores its kept candidates at positions from a block
+// scan of the kept counts. A bucket of more than kThreads members (values clustered far below an outlier) takes the
+// general prune (histogram narrowing) and stores the buffer. `zeroed`: the caller has zeroed the counters
+// (s.buf[kWideList, kWideList + kRankBuckets / 4)) and s.members behind a barrier. Every thread calls it; the block is
+// synchronized on entry (the caller's) and on return.
 template <typename S>
 __device__ __forceinline__ u64 cut_publish(S& s, int m, int k, u64* list, uint32_t lo, uint32_t hi, bool zeroed) {
   constexpr int P = kWideList / kThreads;
@@ -1725,12 +1742,9 @@ __device__ __forceinline__ u64 cut_publish(S& s, int m, int k, u64* list, uint32
   }
   __syncthreads();
   const int B = s.bin, rb = k - s.above, pop = (int)s.hist[0];  // the k-th is the rb-th largest of bucket B's pop
-  u64 kth, least;  // the returned bound; the smallest composite kept from bucket B
-  if (rb == pop && B < kRankBuckets - 1) {  // B kept whole: its lower edge bounds the k-th (B's members are above it)
-    const u64 below = (u64)(B + 1) << sh;
-    kth = (u64)(below >= (u64)hi ? 1u : hi - (uint32_t)below + 1u) << 32;
-    least = 0;
-  } else {
+  u64 kth = 0, least = 0;  // the k-th (found below when B is kept whole); the smallest composite kept from bucket B
+  const bool whole = rb == pop && B < kRankBuckets - 1;  // B kept whole: every member of B is at or above the k-th
+  if (!whole) {
     if (pop > kThreads) {
       prune(s, k);
       for (int i = t; i < k; i += kThreads)
@@ -1756,13 +1770,24 @@ __device__ __forceinline__ u64 cut_publish(S& s, int m, int k, u64* list, uint32
   bool keep[P];
   u64 km[P];
   unsigned* per = s.hist + 64;  // [P][kWaves] kept counts (s.hist[0] holds pop, read above without a barrier since)
+  u64 mn = ~0ull;               // B kept whole: the smallest kept
 #pragma unroll
   for (int i = 0; i < P; ++i) {
     keep[i] = bk[i] < B || (bk[i] == B && c[i] >= least);
     km[i] = __ballot(keep[i]);
     if (lane == 0) per[i * kWaves + wave] = (unsigned)__popcll(km[i]);
+    if (whole) mn = keep[i] && c[i] < mn ? c[i] : mn;
+  }
+  if (whole) {
+    mn = wave_ext64<false>(mn);
+    if (lane == 0) s.red2[wave] = mn;
   }
   __syncthreads();
+  if (whole) {
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mn = s.red2[w] < mn ? s.red2[w] : mn;
+    kth = mn;
+  }
   unsigned base = 0;
 #pragma unroll
   for (int i = 0; i < P; ++i) {
@@ -1831,12 +1856,13 @@ constexpr uint32_t kBoundWindow = (1u << 24) - 1u;  // two binades of fp32 keys 
 // it, and it lies within 2^sh of the k-th (q-th) largest. One count per group instead of a ballot per group and
 // candidate bit. Returns false, with no bounds, when fewer than k group maxima lie in the window (group maxima spread
 // over more than two binades; the caller then searches each wave's whole range). q = 0 asks for no q-bound (bq = 0).
+// A third count, k2 (0: none), gives bk2 the same way, or 0 when fewer than k2 group maxima lie in the window.
 // Uses the last kRankBuckets / 4 entries of s.buf (the buffer holds at most kWideCap - kWideList candidates between
 // tiles). M is set to the largest group maximum (the tile's largest key) in every case. Every thread calls it; the
 // result is block-uniform.
 template <typename S>
 __device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t (&g)[kWideGroups], int k, int q,
-                                            uint32_t& bk, uint32_t& bq, uint32_t& M) {
+                                            int k2, uint32_t& bk, uint32_t& bq, uint32_t& bk2, uint32_t& M) {
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan (BPT / 4 u64 words of counters)
   static_assert(kRankBuckets / 4 <= kWideList && BPT % 4 == 0 && kThreads * kWideGroups < 65536,
                 "the counters lie past the candidates kept between tiles; counts fit 16 bits");
@@ -1884,15 +1910,17 @@ __device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t 
   // the thread whose buckets hold the k-th (q-th) from the top records the bucket: the last one whose count from the
   // top before it is short of k (q)
   uint32_t acc = run;
-  int atk = 0, atq = 0;
+  int atk = 0, atq = 0, atk2 = 0;
 #pragma unroll
   for (int i = 0; i < BPT; ++i) {
     atk = acc < (uint32_t)k ? i : atk;
     atq = acc < (uint32_t)q ? i : atq;
+    atk2 = acc < (uint32_t)k2 ? i : atk2;
     acc += (uint32_t)(w4[i >> 2] >> (16 * (i & 3))) & 0xffffu;
   }
   if (run < (uint32_t)k && (uint32_t)k <= run + sum) s.hist[0] = (unsigned)(t * BPT + atk);
   if (run < (uint32_t)q && (uint32_t)q <= run + sum) s.hist[1] = (unsigned)(t * BPT + atq);
+  if (run < (uint32_t)k2 && (uint32_t)k2 <= run + sum) s.hist[2] = (unsigned)(t * BPT + atk2);
   __syncthreads();
   auto edge = [&](unsigned b) {
     const u64 below = (u64)(b + 1) << sh;
@@ -1900,24 +1928,32 @@ __device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t 
   };
   bk = edge(s.hist[0]);
   bq = q > 0 ? edge(s.hist[1]) : 0u;
+  bk2 = k2 > 0 && (uint32_t)k2 <= total ? edge(s.hist[2]) : 0u;
   return true;
 }
 
-// 64 < k <= 1024: one 256-thread workgroup per (chunk, row), the chunk in register tiles as topk_tile. Per tile: each
-// lane's 64 elements form kWideGroups groups; a group's largest element has the group behind it, so each wave's ceil(k
-// / 4)-th largest group maximum has that many distinct elements at or above it and the smallest of the four waves' has
-// at least k: with the k-th of the earlier tiles it is the admission key (about k * 1.4 admitted per tile on continuous
-// data). The same bound for q = ceil(k / nchunks) gives a q-bound. Admitted elements are appended to an LDS buffer (one
-// LDS atomic per wave and 16 elements per lane); a tile that overflows it (ties, adversarial orders) is appended again
-// vector by vector from the buffer's k-th, pruning to k (histogram narrowing) whenever a vector might not fit. An
-// unsplit row ranks its candidates (write_ranked) and writes the first k. A split row's chunk keeps its k largest
-// (pruned to exactly k when it holds more), writes them to its k slots of the caller's work [rows, nchunks, k] (0 past
-// the end of a shorter list) and its k- and q-bound keys to indices[row * k + part] (the row's output, not yet written:
-// nchunks <= k), all with device-coherent stores, and counts its arrival on counters[row] (block_hand_off). The row's
-// last arrival merges: every chunk has k elements at or above its k-bound and q at or above its q-bound, so the largest
-// k-bound and, when every chunk has one, the smallest q-bound (nchunks * q >= k elements at or above it) bound the
-// row's k-th from below; the lists' entries at or above that floor (about k * 1.4) are gathered, ranked and the first
-// k written out, and the counter is zeroed for the next launch.
+// 64 < k <= 1024: one 256-thread workgroup per (chunk, row), the chunk in register tiles as topk_tile. A split row's
+// chunk keeps only its m = min(k, 2 ceil(k * chunk / cols) + kListSlack) largest: twice a full chunk's share of the
+// row's k and a margin (C5 at k = 1024: 326 of 16384), so that rows whose largest values cluster in one chunk at up to
+// about twice the density elsewhere need no second look at x. Per tile: each lane's 64 elements form kWideGroups groups; a group's
+// largest element has the group behind it, so the m-th largest of the block's group maxima has m distinct elements at
+// or above it: with the m-th of the earlier tiles it is the admission key (about 1.3 m admitted per tile on continuous
+// data). The q-th largest, q = ceil(k / nchunks), gives a q-bound the same way. Admitted elements are appended to an
+// LDS buffer (one LDS atomic per wave and 16 elements per lane); a tile that overflows it (ties, adversarial orders) is
+// appended again vector by vector from the buffer's m-th, pruning to m (histogram narrowing) whenever a vector might
+// not fit. An unsplit row keeps k, ranks its candidates (write_ranked) and writes the first k.
+//
+// A split row's chunk writes its m largest to its list in the caller's work (the row's [nchunks, k] slots hold the
+// nchunks lists of m, then, when m < k, each chunk's separator: the smallest entry of its list, 0 when the list holds
+// every element of the chunk), its header (k-bound key << 32 | q-bound key; when m < k the k-bound comes from a third
+// count of the group maxima, or is 0) to indices[row * k + part] (the row's output, not yet written: nchunks <= k), all
+// with device-coherent stores, and counts its arrival on counters[row] (block_hand_off). The row's last arrival merges.
+// The smallest q-bound (nchunks * q >= k elements at or above it) and the largest k-bound bound the row's k-th largest
+// T from below: the floor. Every element a chunk left out lies below its separator; so when at least k list entries lie at or above the
+// largest separator S (then T >= S), every element at or above T is in the lists, and the lists' entries at or above
+// the floor (about 1.4 k) are gathered, ranked and the first k written out. Otherwise (a chunk holding more than m of
+// the row's k largest: sorted rows, ties, values clustered by index) the merger reads the row again from x and takes
+// every element at or above the floor. The counter is zeroed for the next launch either way.
 template <typename T, bool VEC, bool DRAW>
 __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPRs, four workgroups per CU
     topk_wide(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
@@ -1934,16 +1970,23 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   BlockRed red;
   red.slot = redslots;
   red.phase = 0;
+  const int q = (k + nchunks - 1) / nchunks;
+  // entries each chunk publishes: twice a full chunk's share of the row's k (the last chunk may be shorter) and a
+  // margin, at most k
+  const long long share = ((long long)k * chunk + cols - 1) / cols;
+  const int m = nchunks > 1 && 2 * share + kListSlack < k ? 2 * (int)share + kListSlack : k;
+  const bool split = nchunks > 1;
+  const int kt = split ? m : k;  // the buffer's target: the chunk's m largest, or the row's k
+  uint32_t thr = 0, thq = 0, cmax = 0;  // the admission key, the q-bound, the chunk's largest key
+  uint32_t thk = 0;                     // m < k: a k-bound (k distinct elements of the chunk at or above it), or 0
   if (threadIdx.x == 0) {
     s.count = 0;
     s.thr = 1;
   }
   __syncthreads();
   TOPK_STAGE(0);
-  uint32_t thr = 0, thq = 0, cmax = 0;  // the admission key, the q-bound, the chunk's largest key
   bool cut_zeroed = false;
-  const int q = (k + nchunks - 1) / nchunks;
-  const int kw = (k + kWaves - 1) / kWaves, kwq = (q + kWaves - 1) / kWaves;
+  const int kw = (kt + kWaves - 1) / kWaves, kwq = (q + kWaves - 1) / kWaves;
   using TL = Tile<T, VEC>;
   constexpr int TE = kThreads * kTileE;
   constexpr int kStep = kThreads * TL::W;  // what one vector of a tile may append
@@ -1956,7 +1999,7 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     TOPK_STAGE_AT(1, g[0]);
     TOPK_WAVE_STAGE_AT(g[0]);
     const bool last_tile = end - t0 <= TE;
-    if (last_tile && nchunks > 1) {
+    if (last_tile && split) {
       // the cut's counters, zeroed ahead of the bounds' barriers while no wave appends (the buffer holds at most
       // kWideList candidates between tiles); kept zero unless this tile's appends pass kWideList
       u64* cz = s.buf + kWideList + (int)threadIdx.x * (kRankBuckets / 4 / kThreads);
@@ -1964,17 +2007,18 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
       for (int i = 0; i < kRankBuckets / 4 / kThreads; ++i) cz[i] = 0ull;
       if (threadIdx.x == 0) s.members = 0;
     }
-    uint32_t tb, qb, tm;
-    if (!hist_bounds(s, red, g, k, nchunks > 1 ? q : 0, tb, qb, tm)) {
+    uint32_t tb, qb, kb2 = 0, tm;
+    if (!hist_bounds(s, red, g, kt, split ? q : 0, kt < k ? k : 0, tb, qb, kb2, tm)) {
       // the group maxima spread over more than the window: each wave's bound from a search over its whole range
       const uint32_t tw = wave_kth_multi<kWideGroups>(g, kw, 0u);
       tb = red.min(tw);
-      // q <= k, so the wave's q-th largest group maximum is at or above its k-bound: the search starts there (the
+      // q <= kt, so the wave's q-th largest group maximum is at or above its kt-bound: the search starts there (the
       // groups' smallest maximum is often negative, and 12 bits over that range resolve the bound to about 0.5)
-      qb = nchunks > 1 ? red.min(wave_kth_multi<kWideGroups>(g, kwq, tw)) : 0u;
+      qb = split ? red.min(wave_kth_multi<kWideGroups>(g, kwq, tw)) : 0u;
     }
     thr = tb > thr ? tb : thr;
     thq = qb > thq ? qb : thq;
+    thk = kb2 > thk ? kb2 : thk;
     cmax = tm > cmax ? tm : cmax;
     TOPK_STAGE(2);
     tile.opaque();
@@ -1986,25 +2030,25 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
       redo = s.count > kWideCap;
     }
     cut_zeroed = last_tile && !redo && s.count <= kWideList;  // (the appends left the counters alone)
-    if (redo) {  // every element may pass, or the buffer overflowed: append again vector by vector, pruning to k
+    if (redo) {  // every element may pass, or the buffer overflowed: append again vector by vector, pruning to kt
       __syncthreads();
       if (threadIdx.x == 0) s.count = cnt0;
       __syncthreads();
       const u64 bound = thr > TL::kSentinelKey ? (u64)thr << 32 : 0ull;
       for (int v = 0; v < TL::NV; ++v) {
-        if (prune_due(s, kWideCap - kStep)) prune(s, k);
+        if (prune_due(s, kWideCap - kStep)) prune(s, kt);
         const u64 floor = s.thr > bound ? s.thr : bound;
         tile.append_first(s, v, floor);
         __syncthreads();
       }
     }
     if (end - t0 > TE && s.count > kWideCap - kWideList) {  // before another tile: room for a tile's candidates
-      prune(s, k);
+      prune(s, kt);
       const uint32_t kk = (uint32_t)(s.thr >> 32);
       thr = kk > thr ? kk : thr;
     }
   }
-  if (nchunks == 1) {
+  if (!split) {
     const float u = sa.uniform(row);
     if (s.count > kWideList) prune(s, k);
     write_ranked<T>(s, s.count, k, values, indices, row, 0ull);
@@ -2012,24 +2056,31 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     return;
   }
   TOPK_STAGE(3);
-  // publish: the chunk's k largest (the list, zero-padded to k when it holds fewer) and the header (k-bound key << 32 |
-  // q-bound key) in the row's output
+  // publish: the chunk's m largest (the list, zero-padded to m when it holds fewer), its separator (m < k) and the
+  // header (k-bound key << 32 | q-bound key) in the row's output
   u64* wr = work + row * (long long)nchunks * k;
-  u64* mine = wr + (long long)part * k;
-  if (s.count > kWideList) prune(s, k);
+  u64* mine = wr + (long long)part * m;
+  if (s.count > kWideList) prune(s, m);
   const int n = s.count;
-  u64 kth = s.thr;
-  if (n > k) {
-    kth = cut_publish(s, n, k, mine, thr, cmax, cut_zeroed);
+  u64 kth = 0;  // the chunk's m-th largest, the smallest entry of its list (0: the list holds fewer than m)
+  if (n > m) {
+    kth = cut_publish(s, n, m, mine, thr, cmax, cut_zeroed);
   } else {
-    for (int i = threadIdx.x; i < k; i += kThreads)
+    if (n == m) {  // (block-uniform)
+      u64 mn = ~0ull;
+      for (int i = threadIdx.x; i < n; i += kThreads) mn = s.buf[i] < mn ? s.buf[i] : mn;
+      kth = block_ext64<false>(mn, s);
+    }
+    for (int i = threadIdx.x; i < m; i += kThreads)
       __hip_atomic_store(mine + i, i < n ? s.buf[i] : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   TOPK_STAGE(4);
   u64* heads = reinterpret_cast<u64*>(indices + row * k);
+  u64* seps = wr + (long long)nchunks * m;  // m < k: nchunks * (m + 1) <= nchunks * k slots of the row
   if (threadIdx.x == 0) {
-    const uint32_t kb = (uint32_t)(kth >> 32) > thr ? (uint32_t)(kth >> 32) : thr;
+    const uint32_t kb = m < k ? thk : (uint32_t)(kth >> 32) > thr ? (uint32_t)(kth >> 32) : thr;
     __hip_atomic_store(heads + part, ((u64)kb << 32) | thq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (m < k) __hip_atomic_store(seps + part, kth, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   const bool last = block_hand_off(s, counters + row, nchunks);
   TOPK_STAGE(5);
@@ -2038,14 +2089,15 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   // merge (the row's last arrival): the floor from the headers, then every list's entries at or above it
   auto ld = [&](const u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   const int t = (int)threadIdx.x, lane = lane_id(), wave = wave_id();
-  // Rows whose lists fit the registers (C5: 8 x 1024 entries) read them all at once, right after the headers: the
-  // floor's reduction runs while the lists' loads are in flight (loads return in order), and one block scan places the
-  // entries at or above it.
-  constexpr int kGatherAll = 8192;  // list entries the merger reads in one batch
+  // Rows whose lists fit the registers (C5: 8 x 326 entries) read them all at once, right after the headers: the
+  // floor's reduction runs while the lists' loads are in flight (loads return in order), and one block scan places
+  // the entries at or above it.
+  constexpr int kGatherAll = 2816;  // list entries the merger reads in one batch
   constexpr int PB = kGatherAll / kThreads;
-  const int entries = nchunks * k;  // the row's lists, contiguous in wr
-  u64 kmax = 0, qmn = ~0ull;
-  u64 h0 = t < nchunks ? ld(heads + t) : 0ull;
+  const int entries = nchunks * m;  // the row's lists, contiguous in wr
+  u64 kmax = 0, qmn = ~0ull, smax = 0;
+  const u64 h0 = t < nchunks ? ld(heads + t) : 0ull;
+  const u64 s0 = m < k && t < nchunks ? ld(seps + t) : 0ull;
   u64 e[PB];
   if (entries <= kGatherAll) {
 #pragma unroll
@@ -2056,116 +2108,187 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   }
   for (int c = t; c < nchunks; c += kThreads) {
     const u64 h = c == t ? h0 : ld(heads + c);
+    const u64 sp = m == k ? 0ull : c == t ? s0 : ld(seps + c);
     const u64 kb = h & 0xffffffff00000000ull, qb = h << 32;
     kmax = kb > kmax ? kb : kmax;
     qmn = qb < qmn ? qb : qmn;
+    smax = sp > smax ? sp : smax;
   }
   kmax = wave_ext64<true>(kmax);
   qmn = wave_ext64<false>(qmn);
+  smax = wave_ext64<true>(smax);
   if (lane == 0) {
     s.red[wave] = kmax;
     s.red2[wave] = qmn;
+    s.red4[wave] = smax;
   }
   __syncthreads();
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
     kmax = s.red[w] > kmax ? s.red[w] : kmax;
     qmn = s.red2[w] < qmn ? s.red2[w] : qmn;  // 0 when a chunk has no q-bound
+    smax = s.red4[w] > smax ? s.red4[w] : smax;
   }
   u64 floor = kmax > qmn ? kmax : qmn;
   floor = floor > 1 ? floor : 1;
   TOPK_STAGE(6);
+  bool whole = true;      // every element at or above T is in the lists
+  bool gathered = false;  // the buffer holds the lists' entries at or above the floor
   if (entries <= kGatherAll) {
-    unsigned n = 0;
+    unsigned n = 0, ns = 0;
     u64 mx = 0;
 #pragma unroll
     for (int i = 0; i < PB; ++i) {
       const bool keep = e[i] >= floor;
       n += keep ? 1u : 0u;
+      ns += e[i] >= smax ? 1u : 0u;
       mx = keep && e[i] > mx ? e[i] : mx;
     }
     const unsigned incl = wave_incl_u32(n);
+    const unsigned wns = (unsigned)wave_sum((float)ns);  // exact: at most kGatherAll
     mx = wave_ext64<true>(mx);
     if (lane == kWave - 1) s.wsum[wave] = incl;
-    if (lane == 0) s.red3[wave] = mx;
+    if (lane == 0) {
+      s.red3[wave] = mx;
+      s.hist[wave] = wns;
+    }
     // the ordering's counters, zeroed behind the barrier below (they stay zero unless more than kWideList are kept)
     u64* cz = s.buf + kWideList + t * (kRankBuckets / 4 / kThreads);
 #pragma unroll
     for (int i = 0; i < kRankBuckets / 4 / kThreads; ++i) cz[i] = 0ull;
     __syncthreads();
-    unsigned m = 0, pos = incl - n;
+    unsigned nm = 0, pos = incl - n, above = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      m += s.wsum[w];
+      nm += s.wsum[w];
       pos += w < wave ? s.wsum[w] : 0u;
       mx = s.red3[w] > mx ? s.red3[w] : mx;
+      above += s.hist[w];
     }
-    if (m <= (unsigned)kWideCap) {  // (block-uniform) all of them fit the buffer: one write, then the ordering
+    whole = smax == 0 || above >= (unsigned)k;
+    if (nm <= (unsigned)kWideCap) {  // (block-uniform) all of them fit the buffer: one write
 #pragma unroll
       for (int i = 0; i < PB; ++i)
         if (e[i] >= floor) s.buf[pos++] = e[i];
       if (t == 0) {
-        s.count = (int)m;
+        s.count = (int)nm;
         s.thr = floor;
       }
       __syncthreads();
-      TOPK_STAGE(7);
-      if (m > (unsigned)kWideList) prune(s, k);
-      write_ranked<T>(s, s.count, k, values, indices, row, floor, mx, m <= (unsigned)kWideList);
-      TOPK_STAGE(8);
-      if (t == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sample_list<T>(sa, u, values, indices, row, k);
-      return;
+      if (whole) {
+        TOPK_STAGE(7);
+        if (nm > (unsigned)kWideList) prune(s, k);
+        write_ranked<T>(s, s.count, k, values, indices, row, floor, mx, nm <= (unsigned)kWideList);
+        TOPK_STAGE(8);
+        if (t == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sample_list<T>(sa, u, values, indices, row, k);
+        return;
+      }
+      gathered = true;
     }
   }
-  // longer rows (or more entries at the floor than the buffer holds): the lists in turn, pruning as they come
-  if (t == 0) {
-    s.count = 0;
-    s.thr = floor;
-  }
-  __syncthreads();
-  constexpr int PER = kMaxK / kThreads;  // list entries per thread (k <= kMaxK)
-  constexpr int kInFlight = 2;           // lists whose loads are in flight while one is taken (4 measured no faster)
-  static_assert(PER * kThreads <= kWideCap - kWideList, "room for a whole list above a buffer of kWideList");
-  u64 cv[kInFlight][PER];
-  auto load = [&](int c, u64 (&v)[PER]) {
-    const u64* list = wr + (long long)c * k;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int at = i * kThreads + (int)threadIdx.x;
-      v[i] = at < k ? ld(list + at) : 0ull;
+  if (!gathered) {
+    // longer rows (or more entries at the floor than the buffer holds): the lists in turn, pruning as they come
+    if (t == 0) {
+      s.count = 0;
+      s.thr = floor;
     }
-  };
-  auto take = [&](const u64 (&v)[PER]) {  // appends the entries at or above the floor (room for a list is kept)
-    if (prune_due(s, kWideCap - kWideList)) prune(s, k);
-    const u64 f = s.thr;
-    bool keep[PER];
-    bool any = false;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      keep[i] = v[i] >= f;
-      any |= keep[i];
-    }
-    if (__ballot(any)) append<PER>(s, v, keep);
     __syncthreads();
-  };
+    constexpr int PER = kMaxK / kThreads;  // list entries per thread (m <= kMaxK)
+    constexpr int kInFlight = 2;           // lists whose loads are in flight while one is taken (4 measured no faster)
+    static_assert(PER * kThreads <= kWideCap - kWideList, "room for a whole list above a buffer of kWideList");
+    u64 cv[kInFlight][PER];
+    unsigned ns = 0;  // entries at or above the largest separator
+    auto load = [&](int c, u64 (&v)[PER]) {
+      const u64* list = wr + (long long)c * m;
 #pragma unroll
-  for (int j = 0; j < kInFlight; ++j)
-    if (j < nchunks) load(j, cv[j]);
-  for (int c = 0; c < nchunks; c += kInFlight) {
+      for (int i = 0; i < PER; ++i) {
+        const int at = i * kThreads + (int)threadIdx.x;
+        v[i] = at < m ? ld(list + at) : 0ull;
+      }
+    };
+    auto take = [&](const u64 (&v)[PER]) {  // appends the entries at or above the floor (room for a list is kept)
+      if (prune_due(s, kWideCap - kWideList)) prune(s, k);
+      const u64 f = s.thr;
+      bool keep[PER];
+      bool any = false;
 #pragma unroll
-    for (int j = 0; j < kInFlight; ++j) {
-      if (c + j < nchunks) {
-        take(cv[j]);
-        if (c + j + kInFlight < nchunks) load(c + j + kInFlight, cv[j]);
+      for (int i = 0; i < PER; ++i) {
+        keep[i] = v[i] >= f;
+        any |= keep[i];
+        ns += v[i] >= smax ? 1u : 0u;
+      }
+      if (__ballot(any)) append<PER>(s, v, keep);
+      __syncthreads();
+    };
+#pragma unroll
+    for (int j = 0; j < kInFlight; ++j)
+      if (j < nchunks) load(j, cv[j]);
+    for (int c = 0; c < nchunks; c += kInFlight) {
+#pragma unroll
+      for (int j = 0; j < kInFlight; ++j) {
+        if (c + j < nchunks) {
+          take(cv[j]);
+          if (c + j + kInFlight < nchunks) load(c + j + kInFlight, cv[j]);
+        }
       }
     }
+    whole = smax == 0 || block_count((int)ns, s) >= k;
+  }
+  if (!whole) {
+    // A chunk may hold more than m of the row's k largest. The buffer holds every list entry at or above the floor
+    // (less entries pruned below its k-th), so its k-th largest L bounds T from below. The elements a chunk left out
+    // lie below its separator: the chunks whose separator exceeds L are read again from x, and their elements in
+    // [L, separator) appended, a tile at a time when the tile's count fits the buffer, else vector by vector, pruning
+    // to k whenever a vector might not fit.
+    const int n = s.count;
+    u64 L = n >= k ? kth_largest(s, n, k) : floor;
+    L = L > floor ? L : floor;
+    TOPK_STAGE(9);
+    const u64 again = __ballot(t < nchunks && s0 > L);  // (thread c holds chunk c's separator)
+    if (lane == 0) s.red3[wave] = again;
+    __syncthreads();
+    using TR = Tile<T, VEC, kThreads, kAgainE>;
+    for (int w = 0; w < kWaves; ++w) {
+      u64 mask = s.red3[w];
+      mask = (u64)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(mask >> 32)) << 32 |
+             (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)mask);
+      while (mask) {
+        const int c = w * kWave + __builtin_ctzll(mask);
+        mask &= mask - 1;
+        const u64 sep = ld(seps + c);
+        const u64 top = ((u64)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(sep >> 32)) << 32 |
+                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)sep)) - 1u;  // (sep > L >= 1)
+        const int c0 = (int)((long long)c * chunk), c1 = (int)(c0 + chunk < cols ? c0 + chunk : cols);
+        for (int t0 = c0; t0 < c1; t0 += kThreads * kAgainE) {
+          TR tile;
+          tile.load(xr, t0, c1);
+          // (s.thr and s.count are settled: the last step ended with a barrier; the count is read before the
+          // barriers of block_count, so that no wave reads it after another wave's appends)
+          const u64 f = s.thr > L ? s.thr : L;
+          const int held = s.count;
+          const int add = block_count(tile.count_range(f, top), s);
+          tile.opaque();  // the composites are formed again below, not held from the count
+          if (held + add <= kWideCap) {
+            for (int v = 0; v < TR::NV; ++v) tile.append_first(s, v, f, top);
+            __syncthreads();
+          } else {
+            for (int v = 0; v < TR::NV; ++v) {
+              if (prune_due(s, kWideCap - kStep)) prune(s, k);
+              tile.append_first(s, v, s.thr > L ? s.thr : L, top);
+              __syncthreads();
+            }
+          }
+        }
+      }
+    }
+    TOPK_STAGE(10);
   }
   TOPK_STAGE(7);
   if (s.count > kWideList) prune(s, k);
   write_ranked<T>(s, s.count, k, values, indices, row, floor);  // every candidate kept is at or above the floor
   TOPK_STAGE(8);
-  if (threadIdx.x == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (t == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   sample_list<T>(sa, u, values, indices, row, k);
 }
 

@@ -11,7 +11,8 @@
 //   wrapper); reps launches per k on the same buffers; shuffle_seed >= 0 shuffles the workgroup order and each
 //   round of the lane schedule; pattern: randn (N(0, 2)), ints (0..5: ties), ascending, descending, negative (all
 //   values below -1), allones (rows of the all-ones NaN with a few real values), outlier (randn and one value of 1e30
-//   per row), binades (randn scaled over 24 binades).
+//   per row), binades (randn scaled over 24 binades), clustered (randn raised inside one eighth of each row, by 4 on
+//   even rows and by 0.6 on odd rows, so that one or two chunks hold most of the row's largest values).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -81,6 +82,10 @@ int main(int argc, char** argv) {
     else if (pattern == "allones") ones = r % 3 == 0 ? c % 7 == 0 : r % 3 == 1 ? c != 5 : c < cols - 10;
     else if (pattern == "outlier") f = c == (r * 7919) % cols ? 1e30f : f;  // one value far above the rest
     else if (pattern == "binades") f = std::ldexp(f, (int)(c % 24) - 12);  // magnitudes over 24 binades
+    else if (pattern == "clustered") {
+      const long long w = cols / 8, at = (r * 3 % 8) * w + (r * 101) % (w + 1);
+      f += c >= at && c < at + w ? (r % 2 ? 0.6f : 4.0f) : 0.0f;
+    }
     else if (pattern != "randn") {
       std::fprintf(stderr, "unknown pattern %s\n", pattern.c_str());
       return 2;

@@ -5,7 +5,8 @@ Each workgroup thread is a cooperative fiber and each cross-lane operation an ex
 live lanes. Every buffer the kernels touch (input, outputs, the caller's work and counters) lies between guard pages,
 so an out-of-bounds access ends the run with a fault, and a launch that allocates device memory fails the case. The
 cases cover single- and split-chunk rows, every k class (1, the lane-maxima bound up to 64, the wide path up to
-1024), short last tiles, ties, monotone and all-negative rows, the all-ones NaN, repeated launches on the same buffers
+1024), short last tiles, ties, monotone and all-negative rows, the all-ones NaN, rows whose largest values cluster
+in one chunk (the wide merger's second pass over the row), repeated launches on the same buffers
 (the arrival counters' self-reset), and shuffled workgroup and lane schedules. The concurrent cases run every
 workgroup of a launch on an OS thread of its own, so chunks publish and count their arrivals while the row's other
 chunks and merger run. The waves-ahead cases let each wave run on to the next block barrier before the next wave
@@ -63,6 +64,10 @@ CASES = [
     ("wide_outlier", 2, 3 * 16384 + 500, 0, "65,300,1024", 16384, 2048, 1, 20, -1, "outlier"),
     ("wide_binades", 2, 3 * 16384 + 500, 1, "65,300,1024", 16384, 2048, 1, 21, -1, "binades"),
     ("wide_binades_fp32", 2, 40000, 0, "65,1024", 40000, 2048, 1, 22, -1, "binades"),
+    # the largest values clustered in one eighth of each row: a chunk holds more than the m entries it publishes, and
+    # the merger takes the row again from x (as do the ascending, descending and ties rows above)
+    ("wide_clustered", 4, 128256, 0, "65,300,1024", 0, 16384, 1, 24, -1, "clustered"),
+    ("wide_clustered_bf16", 4, 128256, 1, "300,1024", 0, 16384, 1, 25, 3, "clustered"),
 ]
 
 
@@ -78,6 +83,7 @@ CONCURRENT = [
     ("split_bf16_ties", 4, 40000, 1, "1,13,64,65,300", 4096, 2048, 3, 32, 6, "ints"),
     # 59 workgroups (their fiber stacks stay within the host's limit on memory mappings)
     ("many_chunks", 1, 60000, 0, "7,65", 1024, 2048, 2, 33, -1, "randn"),
+    ("clustered_rows", 4, 128256, 0, "300,1024", 0, 16384, 2, 34, 5, "clustered"),
 ]
 
 
@@ -111,6 +117,7 @@ WEAK = [
     ("c5_rows_fp32", 8, 128256, 0, "1,50,1024", 0, 16384, 2, 41, -1, "randn"),
     ("split_every_k", 4, 40000, 0, ALL_K, 4096, 2048, 3, 42, -1, "randn"),
     ("split_bf16_ties", 4, 40000, 1, "1,13,64,65,300", 4096, 2048, 2, 43, 3, "ints"),
+    ("clustered_rows", 4, 128256, 0, "1024", 0, 16384, 2, 44, -1, "clustered"),
 ]
 
 
@@ -134,7 +141,7 @@ def test_weak_mode_exposes_a_missing_wait(emu_topk, concurrent):
 # barriers with the others' other barriers): rows with ties, monotone and all-ones NaN rows take the prune-heavy paths
 # (the k > 64 tile's re-append loop, the merge's pruning gather).
 AHEAD = ["ties", "ascending", "descending", "negative", "all_ones_nan", "all_ones_nan_bf16", "shuffled_bf16",
-         "split_fp32", "wide_outlier", "wide_binades"]
+         "split_fp32", "wide_outlier", "wide_binades", "wide_clustered"]
 
 
 @pytest.mark.parametrize("name", AHEAD)
