@@ -102,17 +102,20 @@ __device__ __forceinline__ void* head_dst(void* q_out, void* k_out, const Cache&
 template <int IPT>
 struct Items {
   u32x4 a[IPT], b[IPT];
-  u32x4 trig;  // cache entry: this thread's 16-byte vector of the token's cos and sin rows (see load_trig)
+  u32x4 trig;    // cache entry: this thread's 16-byte vector of the token's cos and sin rows (see load_trig)
+  long long pos;  // on the fly: the token's position
 };
 
-// Loads the IPT items of lane j for `token` (an out-of-range item is clamped to the token's last item, never stored).
+// Loads the IPT items of lane j of nt for `token` (an out-of-range item is clamped to the token's last item, never
+// stored).
 template <bool KV, int IPT>
 __device__ __forceinline__ void load_items(Items<IPT>& r, const void* q, const void* k, const Cache& kv,
-                                           long long token, const Shape& s, int items, int lanes_per_head, int j) {
+                                           long long token, const Shape& s, int items, int lanes_per_head, int j,
+                                           int nt) {
   const int half = s.head_dim >> 1;
 #pragma unroll
   for (int u = 0; u < IPT; ++u) {
-    int it = j + u * (int)blockDim.x;
+    int it = j + u * nt;
     it = it < items ? it : items - 1;
     const int h = it / lanes_per_head, c = it - h * lanes_per_head;
     long long o;
@@ -152,24 +155,32 @@ __device__ __forceinline__ void store_trig(const u32x4& v, float* tab, int head_
   }
 }
 
-// Rotates and stores the items; cs(i) gives (cos[i], sin[i], cos[i + h], sin[i + h]) for 8 consecutive i.
+// Rotates the items into w and then stores them, every store after every rotation: a register that a store still
+// reads is written again only later (with all of a step's stores issued together, no rotation waits for a store
+// issued after the next token's loads). cs(i) gives (cos[i], sin[i], cos[i + h], sin[i + h]) for 8 consecutive i.
 template <typename T, bool KV, int IPT, typename Trig>
-__device__ __forceinline__ void rotate_items(const Items<IPT>& r, void* q_out, void* k_out, const Cache& kv,
-                                             long long token, long long slot, const Shape& s, int items,
-                                             int lanes_per_head, int j, bool active, const Trig& trig) {
+__device__ __forceinline__ void rotate_items(const Items<IPT>& r, Items<IPT>& w, void* q_out, void* k_out,
+                                             const Cache& kv, long long token, long long slot, const Shape& s,
+                                             int items, int lanes_per_head, int j, int nt, bool active,
+                                             const Trig& trig) {
   const int half = s.head_dim >> 1;
+  void* dst[IPT];
+  long long off[IPT];
 #pragma unroll
   for (int u = 0; u < IPT; ++u) {
-    const int it = j + u * (int)blockDim.x;
+    dst[u] = nullptr;
+    off[u] = 0;
+    const int it = j + u * nt;
     if (!active || it >= items) continue;
     const int h = it / lanes_per_head, c = it - h * lanes_per_head;
     long long o;
     void* out = head_dst<KV>(q_out, k_out, kv, token, slot, h, s, o);
     if (KV && !out) continue;
-    o += 8 * c;
+    dst[u] = out;
+    off[u] = o + 8 * c;
     if (KV && h >= s.q_heads + s.kv_heads) {  // a fused write's V head: copied as it is
-      store16<true>(out, o / 8, r.a[u]);
-      store16<true>(out, (o + half) / 8, r.b[u]);
+      w.a[u] = r.a[u];
+      w.b[u] = r.b[u];
       continue;
     }
     float c1[8], s1[8], c2[8], s2[8];
@@ -182,8 +193,14 @@ __device__ __forceinline__ void rotate_items(const Items<IPT>& r, void* q_out, v
       oa[e] = a[e] * c1[e] - b[e] * s1[e];
       ob[e] = b[e] * c2[e] + a[e] * s2[e];
     }
-    store16<true>(out, o / 8, pack<T>(oa));
-    store16<true>(out, (o + half) / 8, pack<T>(ob));
+    w.a[u] = pack<T>(oa);
+    w.b[u] = pack<T>(ob);
+  }
+#pragma unroll
+  for (int u = 0; u < IPT; ++u) {
+    if (!dst[u]) continue;
+    store16<true>(dst[u], off[u] / 8, w.a[u]);
+    store16<true>(dst[u], (off[u] + half) / 8, w.b[u]);
   }
 }
 
@@ -228,61 +245,99 @@ __device__ __forceinline__ float2 freq_trig(long long pos, float inv_freq) {
   return make_float2((float)cn, (float)sn);
 }
 
+// On the fly: the LDS table of a token at position pos, (cos, sin) of pair i at float2 freq_slot(i) (threads j, j + nt,
+// ... each fill the pairs of the inv_freq entries they copied).
+__device__ __forceinline__ void fill_table(float* tab, long long pos, const float* invf, int half, int j, int nt) {
+  float2* cs = reinterpret_cast<float2*>(tab);
+  for (int i = j; i < half; i += nt) cs[freq_slot(i)] = freq_trig(pos, invf[i]);
+}
+
+// One token: on the fly, the token's table (tab, filled during the step before) is complete after the barrier, and the
+// next token's table is filled into `next` after the rotation (every thread is past the step before, which read that
+// buffer, once it has passed the barrier); from the cache, the token's cos/sin vectors (loaded with its items) are
+// stored into tab first.
 template <typename T, typename C, bool FREQ, bool KV, int IPT>
-__device__ __forceinline__ void token_step(const Items<IPT>& r, const float* inv_freq, const long long* ids,
-                                           void* q_out, void* k_out, const Cache& kv, long long token, const Shape& s,
-                                           int items, int lanes_per_head, int j, float* tab) {
+__device__ __forceinline__ void token_step(const Items<IPT>& r, Items<IPT>& w, const float* invf, void* q_out,
+                                           void* k_out, const Cache& kv, long long token, const Shape& s, int items,
+                                           int lanes_per_head, int j, int nt, float* tab, float* next,
+                                           long long next_pos) {
   const bool active = token < s.tokens;
   const long long tok = active ? token : s.tokens - 1;
   const long long slot = KV ? kv.slots[tok] : tok;  // the k output row: the token's cache slot when fused
   const int half = s.head_dim >> 1;
   if constexpr (FREQ) {
-    const long long pos = ids[tok];
-    float2* cs = reinterpret_cast<float2*>(tab);
-    for (int i = j; i < half; i += blockDim.x) cs[freq_slot(i)] = freq_trig(pos, inv_freq[i]);
     __syncthreads();
-    rotate_items<T, KV, IPT>(r, q_out, k_out, kv, tok, slot, s, items, lanes_per_head, j, active, LdsTrig{cs});
+    rotate_items<T, KV, IPT>(r, w, q_out, k_out, kv, tok, slot, s, items, lanes_per_head, j, nt, active,
+                             LdsTrig{reinterpret_cast<const float2*>(tab)});
+    fill_table(next, next_pos, invf, half, j, nt);
   } else {
     store_trig<C>(r.trig, tab, s.head_dim, j);
     __syncthreads();
-    rotate_items<T, KV, IPT>(r, q_out, k_out, kv, tok, slot, s, items, lanes_per_head, j, active,
+    rotate_items<T, KV, IPT>(r, w, q_out, k_out, kv, tok, slot, s, items, lanes_per_head, j, nt, active,
                              LdsCacheTrig{tab, half});
   }
 }
 
 // Persistent vector kernel: block b takes tokens b, b + grid, ... with a uniform trip count (a block past the last
 // token loads an in-bounds token and stores nothing), two register sets of items (and, for the cache entry, of the
-// token's cos/sin vectors) alternating between tokens. The LDS table is double-buffered by token parity: a buffer is
-// written again two tokens later, after the barrier of the token in between, which every thread passes only once it
-// has read the buffer.
-template <typename T, typename C, bool FREQ, bool KV, int IPT>
-__global__ void __launch_bounds__(1024)
+// token's cos/sin vectors; on the fly, of its position) alternating between tokens. The LDS table is double-buffered
+// by token parity: a buffer is written again two tokens later, after the barrier of the token in between, which every
+// thread passes only once it has read the buffer.
+//
+// Inside the token loop no value is read from memory with a vector load that a step must wait for: the vector memory
+// counter retires loads and stores in order, so such a wait also waits for the next token's items, issued just before,
+// and the two register sets no longer overlap. So the block size is read once (blockDim.x is a 16-bit load from the
+// dispatch's arguments, which the compiler repeats after stores), inv_freq is copied into LDS once (each thread keeps
+// the entries it computes), positions are uniform loads through the scalar cache, a step issues its stores after all
+// of its rotations, and those stores' registers stay untouched until the next token's loads are issued (keep below):
+// a register written while a store still reads it waits for that store and so for every load issued before it.
+// WIDE: blocks of more than 256 threads (at most 128 registers per thread); otherwise at most 256 threads, which
+// leaves the compiler room for the register sets without spilling.
+template <typename T, typename C, bool FREQ, bool KV, int IPT, bool WIDE>
+__global__ void __launch_bounds__(WIDE ? 1024 : 256)
     rope_vec(const void* q, const void* k, const void* __restrict__ cos_rows, const void* __restrict__ sin_rows,
              const float* __restrict__ inv_freq, const long long* __restrict__ ids, void* q_out, void* k_out,
              Cache kv, Shape s) {
   constexpr int TABLE = FREQ ? kFreqTable : kCacheTable;
   __shared__ __align__(16) float tab[2][TABLE];
+  __shared__ float invf[FREQ ? kMaxHalf : 1];
   const int lanes_per_head = s.head_dim >> 4;
   const int items = (s.q_heads + s.kv_heads + (KV ? s.v_heads : 0)) * lanes_per_head;
   const int j = threadIdx.x;
+  const int nt = __builtin_amdgcn_readfirstlane((int)blockDim.x);
   long long t = blockIdx.x;
   if (t >= s.tokens) return;
   const long long last = s.tokens - 1;
-  Items<IPT> a, b;
+  Items<IPT> a, b, w;  // w: the rotated items of the last step, which its stores read
+#pragma unroll
+  for (int u = 0; u < IPT; ++u) w.a[u] = w.b[u] = (u32x4){0u, 0u, 0u, 0u};
   auto load = [&](Items<IPT>& r, long long tok) __attribute__((always_inline)) {
-    load_items<KV, IPT>(r, q, k, kv, tok, s, items, lanes_per_head, j);
-    if constexpr (!FREQ) load_trig<C>(r.trig, cos_rows, sin_rows, ids[tok], s.head_dim, j);
+    load_items<KV, IPT>(r, q, k, kv, tok, s, items, lanes_per_head, j, nt);
+    if constexpr (FREQ) r.pos = ids[tok];
+    else load_trig<C>(r.trig, cos_rows, sin_rows, ids[tok], s.head_dim, j);
+  };
+  auto keep = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < IPT; ++u) asm volatile("" ::"v"(w.a[u]), "v"(w.b[u]));
   };
   load(a, t);
+  if constexpr (FREQ) {  // the entries i = j, j + nt, ...: those whose pairs this thread computes
+    for (int i = j; i < (s.head_dim >> 1); i += nt) invf[i] = inv_freq[i];
+    fill_table(tab[0], a.pos, invf, s.head_dim >> 1, j, nt);
+  }
   while (true) {
     const long long tb = t + gridDim.x;
     load(b, tb < s.tokens ? tb : last);
-    token_step<T, C, FREQ, KV, IPT>(a, inv_freq, ids, q_out, k_out, kv, t, s, items, lanes_per_head, j, tab[0]);
+    keep();
+    token_step<T, C, FREQ, KV, IPT>(a, w, invf, q_out, k_out, kv, t, s, items, lanes_per_head, j, nt, tab[0], tab[1],
+                                    b.pos);
     t = tb;
     if (t >= s.tokens) break;
     const long long tc = t + gridDim.x;
     load(a, tc < s.tokens ? tc : last);
-    token_step<T, C, FREQ, KV, IPT>(b, inv_freq, ids, q_out, k_out, kv, t, s, items, lanes_per_head, j, tab[1]);
+    keep();
+    token_step<T, C, FREQ, KV, IPT>(b, w, invf, q_out, k_out, kv, t, s, items, lanes_per_head, j, nt, tab[1], tab[0],
+                                    a.pos);
     t = tc;
     if (t >= s.tokens) break;
   }
@@ -359,7 +414,7 @@ struct Ptrs {
 
 template <typename T, typename C, bool FREQ, bool KV, int IPT>
 int launch_vec_k(const Ptrs& p, const Shape& s, int threads, hipStream_t stream) {
-  auto kern = rope_vec<T, C, FREQ, KV, IPT>;
+  auto kern = threads > 256 ? rope_vec<T, C, FREQ, KV, IPT, true> : rope_vec<T, C, FREQ, KV, IPT, false>;
   int occ = blocks_per_cu(kern, threads);
   int per_cu = rw_host::tune_get(kTuneBlocksPerCu);
   if (per_cu <= 0) per_cu = 8;  // 8 resident token blocks per CU by default (measured on MI355X)

@@ -217,4 +217,11 @@ __device__ __forceinline__ F group_reduce(F v, Op op, F* slots, int wave, int fi
 __device__ __forceinline__ int wave_id() { return (int)(threadIdx.x >> 6); }
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// Orders one wave's LDS writes before its later LDS reads of other lanes' entries (a wave's LDS operations execute in
+// order; this keeps the compiler from moving them across).
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
+
 }  // namespace rw

@@ -730,13 +730,6 @@ __device__ __forceinline__ void stage_stamp(int slot) {
   } while (0)
 #endif
 
-// Orders one wave's LDS writes before its later LDS reads of other lanes' entries (a wave's LDS operations execute in
-// order; this keeps the compiler from moving them across).
-__device__ __forceinline__ void wave_lds_sync() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_wave_barrier();
-}
-
 // A register tile: thread t of the workgroup's NT holds vectors v * NT + t (v < NV = EPL / W) of elements [b0, b1) of a
 // row, W each, as raw bits; an element outside [b0, b1) holds the sentinel (all ones: the -NaN whose key is the smallest of
 // its format), read from g_sentinel_vec by a vector load past the end. load() only issues the loads.

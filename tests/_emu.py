@@ -38,15 +38,22 @@ def build(tmpdir, source, driver):
         subprocess.run(["gcc", "-O2", "-c", src, "-o", obj], check=True)
     exe = os.path.join(str(tmpdir), "emu_" + stem)
     proc = subprocess.run([clang, "-std=c++17", "-O1", "-U_FORTIFY_SOURCE", "-D_FORTIFY_SOURCE=0",
-                           "-fno-strict-aliasing", "-w", "-pthread", "-I", EMU, "-I", CSRC, kern,
+                           "-fno-strict-aliasing", "-w", "-pthread", "-I", EMU, "-I", str(tmpdir), "-I", CSRC, kern,
                            os.path.join(EMU, driver), obj, "-o", exe, "-lm"], capture_output=True, text=True)
     assert proc.returncode == 0, proc.stderr[-4000:]
     return exe
 
 
 def kernel_source(tmpdir, source):
-    """csrc/<source> with its inline asm statements routed to the emulation's hook; returns the path of the copy."""
+    """csrc/<source> with its inline asm statements routed to the emulation's hook; returns the path of the copy. The
+    csrc headers are copied beside it the same way (the copy's directory comes first on the include path)."""
     stem = os.path.splitext(source)[0]
+    for name in os.listdir(CSRC):
+        if name.endswith(".hpp"):
+            with open(os.path.join(CSRC, name)) as f:
+                text = f.read().replace("asm volatile(", "EMU_ASM(")
+            with open(os.path.join(str(tmpdir), name), "w") as f:
+                f.write(text)
     with open(os.path.join(CSRC, source)) as f:
         src = f.read().replace("asm volatile(", "EMU_ASM(")
     kern = os.path.join(str(tmpdir), stem + "_emu.cpp")
@@ -62,7 +69,7 @@ def build_shared(tmpdir, source, name):
         pytest.skip("clang++ (for the kernels' vector extensions on the host) is missing")
     out = os.path.join(str(tmpdir), name)
     proc = subprocess.run([clang, "-std=c++17", "-O1", "-fPIC", "-shared", "-U_FORTIFY_SOURCE", "-D_FORTIFY_SOURCE=0",
-                           "-fno-strict-aliasing", "-w", "-pthread", "-I", EMU, "-I", CSRC,
+                           "-fno-strict-aliasing", "-w", "-pthread", "-I", EMU, "-I", str(tmpdir), "-I", CSRC,
                            kernel_source(tmpdir, source), "-o", out], capture_output=True, text=True)
     assert proc.returncode == 0, proc.stderr[-4000:]
     return out
