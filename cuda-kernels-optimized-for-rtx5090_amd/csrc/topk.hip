@@ -1688,10 +1688,18 @@ __device__ __forceinline__ u64 cut_publish(S& s, int m, int k, u64* list, uint32
   lo = lo < hi ? lo : hi;
   const uint32_t D = hi - lo;
   const int sh = (D >> 12) ? (32 - __builtin_clz(D)) - 12 : 0;  // D >> sh < kRankBuckets
+  // the candidate slots in use (block-uniform): the rest are skipped as a block (C5 at k = 1024: 2 of 8)
+  const int used = (m + kThreads - 1) / kThreads;
   u64 c[P];
   int bk[P];
 #pragma unroll
   for (int r = 0; r < P; ++r) {
+    c[r] = 0ull;
+    bk[r] = kRankBuckets;
+  }
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    if (r >= used) break;
     const int i = r * kThreads + t;
     c[r] = i < m ? s.buf[i] : 0ull;
     const uint32_t d = (hi - (uint32_t)(c[r] >> 32)) >> sh;
@@ -1745,8 +1753,10 @@ __device__ __forceinline__ u64 cut_publish(S& s, int m, int k, u64* list, uint32
       return s.thr;
     }
 #pragma unroll
-    for (int i = 0; i < P; ++i)
+    for (int i = 0; i < P; ++i) {
+      if (i >= used) break;
       if (bk[i] == B) members[atomicAdd(&s.members, 1)] = c[i];
+    }
     __syncthreads();
     if (t < pop) {
       const u64 mem = members[t];
@@ -1766,6 +1776,12 @@ __device__ __forceinline__ u64 cut_publish(S& s, int m, int k, u64* list, uint32
   u64 mn = ~0ull;               // B kept whole: the smallest kept
 #pragma unroll
   for (int i = 0; i < P; ++i) {
+    keep[i] = false;
+    km[i] = 0ull;
+  }
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    if (i >= used) break;
     keep[i] = bk[i] < B || (bk[i] == B && c[i] >= least);
     km[i] = __ballot(keep[i]);
     if (lane == 0) per[i * kWaves + wave] = (unsigned)__popcll(km[i]);
@@ -1784,6 +1800,7 @@ __device__ __forceinline__ u64 cut_publish(S& s, int m, int k, u64* list, uint32
   unsigned base = 0;
 #pragma unroll
   for (int i = 0; i < P; ++i) {
+    if (i >= used) break;
     unsigned before = 0, all = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
