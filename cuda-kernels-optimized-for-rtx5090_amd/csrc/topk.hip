@@ -1876,7 +1876,8 @@ __device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t 
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan (BPT / 4 u64 words of counters)
   static_assert(kRankBuckets / 4 <= kWideList && BPT % 4 == 0 && kThreads * kWideGroups < 65536,
                 "the counters lie past the candidates kept between tiles; counts fit 16 bits");
-  unsigned* cnt2 = reinterpret_cast<unsigned*>(s.buf + kWideCap - kRankBuckets / 4);  // bucket b: half b & 1 of word b >> 1
+  // bucket b: half b & 1 of word b >> 1
+  unsigned* cnt2 = reinterpret_cast<unsigned*>(s.buf + kWideCap - kRankBuckets / 4);
   const int t = (int)threadIdx.x;
   u64* mine = reinterpret_cast<u64*>(cnt2) + t * (BPT / 4);
 #pragma unroll
@@ -1945,25 +1946,27 @@ __device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t 
 // 64 < k <= 1024: one 256-thread workgroup per (chunk, row), the chunk in register tiles as topk_tile. A split row's
 // chunk keeps only its m = min(k, 2 ceil(k * chunk / cols) + kListSlack) largest: twice a full chunk's share of the
 // row's k and a margin (C5 at k = 1024: 326 of 16384), so that rows whose largest values cluster in one chunk at up to
-// about twice the density elsewhere need no second look at x. Per tile: each lane's 64 elements form kWideGroups groups; a group's
-// largest element has the group behind it, so the m-th largest of the block's group maxima has m distinct elements at
-// or above it: with the m-th of the earlier tiles it is the admission key (about 1.3 m admitted per tile on continuous
-// data). The q-th largest, q = ceil(k / nchunks), gives a q-bound the same way. Admitted elements are appended to an
-// LDS buffer (one LDS atomic per wave and 16 elements per lane); a tile that overflows it (ties, adversarial orders) is
-// appended again vector by vector from the buffer's m-th, pruning to m (histogram narrowing) whenever a vector might
-// not fit. An unsplit row keeps k, ranks its candidates (write_ranked) and writes the first k.
+// about twice the density elsewhere need no second look at x. Per tile: each lane's 64 elements form kWideGroups
+// groups; a group's largest element has the group behind it, so the m-th largest of the block's group maxima has m
+// distinct elements at or above it: with the m-th of the earlier tiles it is the admission key (about 1.3 m admitted
+// per tile on continuous data). The q-th largest, q = ceil(k / nchunks), gives a q-bound the same way. Admitted
+// elements are appended to an LDS buffer (one LDS atomic per wave and 16 elements per lane); a tile that overflows it
+// (ties, adversarial orders) is appended again vector by vector from the buffer's m-th, pruning to m (histogram
+// narrowing) whenever a vector might not fit. An unsplit row keeps k, ranks its candidates (write_ranked) and writes
+// the first k.
 //
 // A split row's chunk writes its m largest to its list in the caller's work (the row's [nchunks, k] slots hold the
 // nchunks lists of m, then, when m < k, each chunk's separator: the smallest entry of its list, 0 when the list holds
 // every element of the chunk), its header (k-bound key << 32 | q-bound key; when m < k the k-bound comes from a third
-// count of the group maxima, or is 0) to indices[row * k + part] (the row's output, not yet written: nchunks <= k), all
-// with device-coherent stores, and counts its arrival on counters[row] (block_hand_off). The row's last arrival merges.
-// The smallest q-bound (nchunks * q >= k elements at or above it) and the largest k-bound bound the row's k-th largest
-// T from below: the floor. Every element a chunk left out lies below its separator; so when at least k list entries lie at or above the
-// largest separator S (then T >= S), every element at or above T is in the lists, and the lists' entries at or above
-// the floor (about 1.4 k) are gathered, ranked and the first k written out. Otherwise (a chunk holding more than m of
-// the row's k largest: sorted rows, ties, values clustered by index) the merger reads the row again from x and takes
-// every element at or above the floor. The counter is zeroed for the next launch either way.
+// count of the group maxima, or is 0) to indices[row * k + part] (the row's output, not yet written: nchunks <= k),
+// all with device-coherent stores, and counts its arrival on counters[row] (block_hand_off). The row's last arrival
+// merges. The smallest q-bound (nchunks * q >= k elements at or above it) and the largest k-bound bound the row's k-th
+// largest T from below: the floor. Every element a chunk left out lies below its separator; so when at least k list
+// entries lie at or above the largest separator S (then T >= S), every element at or above T is in the lists, and
+// the lists' entries at or above the floor (about 1.4 k) are gathered, ranked and the first k written out. Otherwise
+// (a chunk holding more than m of the row's k largest: sorted rows, ties, values clustered by index) the merger reads
+// again from x the chunks that may have left out part of the row's k largest (below). The counter is zeroed for the
+// next launch either way.
 template <typename T, bool VEC, bool DRAW>
 __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPRs, four workgroups per CU
     topk_wide(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,

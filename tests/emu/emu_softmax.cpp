@@ -12,9 +12,9 @@
 //   an all -inf row, a row of one huge value); reps: launches on the same buffers, each checked (the co-resident
 //   tier's pair table is reused by the next launch, under fresh tags); wait_ticks bounds the co-resident tier's wait
 //   (1 makes its workgroups stop waiting and take the row's statistics from x).
-// EMU_GRAPH set: after an eager launch, the launch is recorded as a graph (the emulation's capture) and every rep replays it, each with
-// new values in x (seed + rep); odd reps first run an eager launch of the same shape on other values and buffers,
-// which leaves its own pairs in the table. Every replay is checked against the oracle of its own x.
+// EMU_GRAPH set: after an eager launch, the launch is recorded as a graph (the emulation's capture) and every rep
+// replays it, each with new values in x (seed + rep); odd reps first run an eager launch of the same shape on other
+// values and buffers, which leaves its own pairs in the table. Every replay is checked against the oracle of its x.
 #include <hip/hip_runtime.h>
 
 #include <cmath>

@@ -18,9 +18,9 @@
 //    at the lane's later atomic operations, ballots, sleeps and barriers (so a lane that keeps running sees its
 //    stores complete in the end, as the hardware's do), all of the lane's drain at `s_waitcnt vmcnt(0)` (the wait
 //    that orders them before a later arrival count), and what a lane left pending when it ended drains one store at a
-//    time, now and then, while other lanes run, and wholly when the launch completes. A lane reads its own pending stores (same-address order is
-//    kept); atomic read-modify-writes act on memory at once. With EMU_DROP_VMCNT set as well, `s_waitcnt vmcnt(0)`
-//    drains nothing: the planted mistake that the weak mode must expose.
+//    time, now and then, while other lanes run, and wholly when the launch completes. A lane reads its own pending
+//    stores (same-address order is kept); atomic read-modify-writes act on memory at once. With EMU_DROP_VMCNT set as
+//    well, `s_waitcnt vmcnt(0)` drains nothing: the planted mistake that the weak mode must expose.
 //  - hipMalloc calls are counted (emu::mallocs()), so a driver can show that a launch allocates nothing.
 #pragma once
 #include <sched.h>
