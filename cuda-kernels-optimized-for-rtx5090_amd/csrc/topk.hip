@@ -989,9 +989,9 @@ struct Tile {
   // wave (a ballot per bit of the counts) and one LDS atomic per wave reserve the wave's positions, and each lane
   // writes its elements in order. This needs no ballot per element, which at the wide kernel's admission rate (an
   // admitted lane in nearly every 64-lane column) cost as many scalar instructions as the compares. Appends past the
-  // buffer's end are counted in s.count and not stored.
+  // buffer's first `lim` entries are counted in s.count and not stored.
   template <bool NEG, typename S>
-  __device__ __forceinline__ void filter_append(S& s, uint32_t K) {
+  __device__ __forceinline__ void filter_append(S& s, uint32_t K, int lim) {
     const uint32_t t = bits_of(K);
     int n = 0;
 #pragma unroll
@@ -1004,8 +1004,7 @@ struct Tile {
     int base = 0;
     if (lane_id() == 0) base = atomicAdd(&s.count, total);
     base = __builtin_amdgcn_readfirstlane(base);
-    constexpr int kCap = (int)(sizeof(s.buf) / sizeof(u64));
-    if (base + total <= kCap) {
+    if (base + total <= lim) {
       // every element of the wave fits: no bound check per element. Over a non-negative threshold every admitted
       // element is non-negative, and its key is its bits with the top bit set.
       u64* at = s.buf + base + excl;
@@ -1029,9 +1028,66 @@ struct Tile {
 #pragma unroll
       for (int j = 0; j < W; ++j)
         if (admits<NEG>(v, j, t)) {
-          if (pos < kCap) s.buf[pos] = comp(v, j);
+          if (pos < lim) s.buf[pos] = comp(v, j);
           ++pos;
         }
+  }
+
+  // filter_append<false> for fp32 tiles by way of the wave's LDS staging area (CAPW vectors, then their first indices):
+  // a vector whose signed maximum of the raw bits is below t = bits_of(K) holds no element with key >= K (as in
+  // filter_groups), so each lane stages only its vectors reaching t, and the wave then tests the staged elements 64 at
+  // a time, appending the admitted ones (one LDS atomic per batch of 64; positions from the batch's ballot). At the
+  // wide kernel's admission rate a staged vector holds about one admitted element, so this replaces a compare and a
+  // masked write per element position with a compare per vector and a few instructions per 64 staged elements.
+  // Appends at or past `lim` are counted in s.count and not stored. Returns false, having appended nothing, when the
+  // wave has more than CAPW vectors to stage (ties, clustered values); its lanes then take filter_append.
+  template <int CAPW, typename S>
+  __device__ __forceinline__ bool stage_append(S& s, uint32_t K, u32x4* stage, uint32_t* stage_at, int lim) {
+    static_assert(sizeof(T) == 4, "fp32 tiles");
+    const int t = (int)bits_of(K);  // >= 0
+    int n = 0;                      // wave-uniform
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int a = (int)r[v][0], b = (int)r[v][1], c = (int)r[v][2], d = (int)r[v][3];
+      const int ab = a > b ? a : b, cd = c > d ? c : d;
+      const bool hit = (ab > cd ? ab : cd) >= t;
+      const u64 m = __ballot(hit);
+      int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                               __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)n));
+      pos = pos < CAPW - 1 ? pos : CAPW - 1;  // past the area: the last slot (the wave then returns false)
+      if (hit) {
+        stage[pos] = r[v];
+        stage_at[pos] = (uint32_t)first(v);
+      }
+      n += __popcll(m);
+    }
+    if (n > CAPW) return false;
+    wave_lds_sync();  // the wave's staging writes before its reads of other lanes' entries
+    const int lane = lane_id();
+    const uint32_t* su = reinterpret_cast<const uint32_t*>(stage);
+    // two batches of 64 staged elements per step, all four reads issued together, one LDS atomic for both
+    for (int b = 0; b < 4 * n; b += 2 * kWave) {  // wave-uniform trip count
+      const int i0 = b + lane, i1 = i0 + kWave;
+      const bool ok0 = i0 < 4 * n, ok1 = i1 < 4 * n;
+      const int a0 = ok0 ? i0 : 0, a1 = ok1 ? i1 : 0;
+      const uint32_t u0 = su[a0], u1 = su[a1];
+      const uint32_t x0 = stage_at[a0 >> 2] + (uint32_t)(a0 & 3), x1 = stage_at[a1 >> 2] + (uint32_t)(a1 & 3);
+      const bool k0 = ok0 && (int)u0 >= t, k1 = ok1 && (int)u1 >= t;
+      const u64 m0 = __ballot(k0), m1 = __ballot(k1);
+      const int c0 = __popcll(m0), c = c0 + __popcll(m1);
+      if (c == 0) continue;
+      int base = 0;
+      if (lane == 0) base = atomicAdd(&s.count, c);
+      base = __builtin_amdgcn_readfirstlane(base);
+      const int p0 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m0 >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)m0, (uint32_t)base));
+      const int p1 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m1 >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)m1, (uint32_t)(base + c0)));
+      // over a non-negative threshold the key of an admitted element is its bits with the top bit set
+      if (k0 && p0 < lim) s.buf[p0] = ((u64)(u0 | 0x80000000u) << 32) | (u64)(~x0);
+      if (k1 && p1 < lim) s.buf[p1] = ((u64)(u1 | 0x80000000u) << 32) | (u64)(~x1);
+    }
+    return true;
   }
 
   // The lane's elements with composites in [lo, hi].
@@ -1525,6 +1581,10 @@ constexpr int kWideList = 2048;   // the most candidates ranked at once (write_r
 constexpr int kWideMaxChunks = 256;
 constexpr int kListSlack = 64;  // a split row's chunk publishes twice its share of k and kListSlack more (at most k)
 constexpr int kAgainE = 32;     // elements per lane of the merger's tiles when it reads chunks again from x
+constexpr int kStageVecs = 192;    // vectors one wave may stage for its appends (Tile::stage_append)
+constexpr int kStageMaxKeep = 512;  // staged appends for buffer targets up to this (about 1.3 / 4 of it per wave)
+static_assert(kStageVecs * 20 <= (kWideCap - kWideList) / kWaves * 8,
+              "a wave's staged vectors and indices fit its area");
 
 constexpr int kRankBuckets = 4096;  // buckets of write_ranked (16-bit counters and first positions)
 
@@ -2037,10 +2097,31 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     tile.opaque();
     bool redo = true;
     if (thr > TL::kSentinelKey) {
-      if (thr & 0x80000000u) tile.template filter_append<false>(s, thr);
-      else tile.template filter_append<true>(s, thr);
+      int lim = kWideCap;
+      if (!(thr & 0x80000000u)) {
+        tile.template filter_append<true>(s, thr, lim);
+      } else if (sizeof(T) == 4 && cnt0 == 0 && kt <= kStageMaxKeep) {
+        // fp32 over a non-negative bound, the tile's candidates into an empty buffer: each wave stages its vectors
+        // reaching the bound in its quarter of s.buf[kWideList, kWideCap) (free after the bounds' last read), and
+        // the appends stay below kWideList meanwhile
+        lim = kWideList;
+        u64* area = s.buf + kWideList + wave_id() * ((kWideCap - kWideList) / kWaves);
+        u32x4* stage = reinterpret_cast<u32x4*>(area);
+        if constexpr (sizeof(T) == 4) {
+          if (!tile.template stage_append<kStageVecs>(s, thr, stage, reinterpret_cast<uint32_t*>(stage + kStageVecs),
+                                                      lim))
+            tile.template filter_append<false>(s, thr, lim);
+        }
+        if (last_tile && split && area < s.buf + kWideList + kRankBuckets / 4) {
+          // the cut's counters this wave's area overlaps, zeroed again (LDS operations of one wave complete in order)
+#pragma unroll
+          for (int i = 0; i < (kWideCap - kWideList) / kWaves / kWave; ++i) area[i * kWave + lane_id()] = 0ull;
+        }
+      } else {
+        tile.template filter_append<false>(s, thr, lim);
+      }
       __syncthreads();
-      redo = s.count > kWideCap;
+      redo = s.count > lim;
     }
     cut_zeroed = last_tile && !redo && s.count <= kWideList;  // (the appends left the counters alone)
     if (redo) {  // every element may pass, or the buffer overflowed: append again vector by vector, pruning to kt
