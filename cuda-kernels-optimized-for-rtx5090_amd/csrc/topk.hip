@@ -2004,29 +2004,31 @@ __device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t 
 }
 
 // 64 < k <= 1024: one 256-thread workgroup per (chunk, row), the chunk in register tiles as topk_tile. A split row's
-// chunk keeps only its m = min(k, 2 ceil(k * chunk / cols) + kListSlack) largest: twice a full chunk's share of the
-// row's k and a margin (C5 at k = 1024: 326 of 16384), so that rows whose largest values cluster in one chunk at up to
-// about twice the density elsewhere need no second look at x. Per tile: each lane's 64 elements form kWideGroups
-// groups; a group's largest element has the group behind it, so the m-th largest of the block's group maxima has m
-// distinct elements at or above it: with the m-th of the earlier tiles it is the admission key (about 1.3 m admitted
-// per tile on continuous data). The q-th largest, q = ceil(k / nchunks), gives a q-bound the same way. Admitted
-// elements are appended to an LDS buffer (one LDS atomic per wave and 16 elements per lane); a tile that overflows it
-// (ties, adversarial orders) is appended again vector by vector from the buffer's m-th, pruning to m (histogram
-// narrowing) whenever a vector might not fit. An unsplit row keeps k, ranks its candidates (write_ranked) and writes
-// the first k.
+// chunk admits its candidates at an m-bound, m = min(k, 2 ceil(k * chunk / cols) + kListSlack): twice a full chunk's
+// share of the row's k and a margin (C5 at k = 1024: 326 of 16384), so that rows whose largest values cluster in one
+// chunk at up to about twice the density elsewhere need no second look at x. Per tile: each lane's 64 elements form
+// kWideGroups groups; a group's largest element has the group behind it, so the m-th largest of the block's group
+// maxima has m distinct elements at or above it: with the m-th of the earlier tiles it is the admission key (about
+// 1.1 m admitted per tile on continuous data). The q-th largest, q = ceil(k / nchunks), gives a q-bound the same way.
+// Admitted elements are appended to an LDS buffer (fp32: through each wave's staging area; else one LDS atomic per
+// wave and 16 elements per lane); a tile that overflows it (ties, adversarial orders) is appended again vector by
+// vector from the buffer's m-th, pruning to m (histogram narrowing) whenever a vector might not fit. An unsplit row
+// keeps k, ranks its candidates (write_ranked) and writes the first k.
 //
-// A split row's chunk writes its m largest to its list in the caller's work (the row's [nchunks, k] slots hold the
-// nchunks lists of m, then, when m < k, each chunk's separator: the smallest entry of its list, 0 when the list holds
-// every element of the chunk), its header (k-bound key << 32 | q-bound key; when m < k the k-bound comes from a third
-// count of the group maxima, or is 0) to indices[row * k + part] (the row's output, not yet written: nchunks <= k),
-// all with device-coherent stores, and counts its arrival on counters[row] (block_hand_off). The row's last arrival
+// A split row's chunk writes its list to the caller's work: the row's [nchunks, k] slots hold the nchunks lists of ls
+// entries (zero-padded), then, when m < k, each chunk's separator. When m < k the list is the chunk's candidates at or
+// above the separator, the larger of the admission key and the prunes' floor, as they are (no cut) when they fit ls;
+// else (and when m = k) its m largest, with the smallest of them as the separator (0: the list holds every element of
+// the chunk). The header (k-bound key << 32 | q-bound key; when m < k the k-bound comes from a third count of the group
+// maxima, or is 0) goes to indices[row * k + part] (the row's output, not yet written: nchunks <= k), all with
+// device-coherent stores, and the chunk counts its arrival on counters[row] (block_hand_off). The row's last arrival
 // merges. The smallest q-bound (nchunks * q >= k elements at or above it) and the largest k-bound bound the row's k-th
-// largest T from below: the floor. Every element a chunk left out lies below its separator; so when at least k list
-// entries lie at or above the largest separator S (then T >= S), every element at or above T is in the lists, and
-// the lists' entries at or above the floor (about 1.4 k) are gathered, ranked and the first k written out. Otherwise
-// (a chunk holding more than m of the row's k largest: sorted rows, ties, values clustered by index) the merger reads
-// again from x the chunks that may have left out part of the row's k largest (below). The counter is zeroed for the
-// next launch either way.
+// largest T from below: the floor. Every element a chunk left out lies below its separator, and every list entry at
+// or above it; so when at least k list entries lie at or above the largest separator S (then T >= S), every element at
+// or above T is in the lists, and the lists' entries at or above the floor (about 1.4 k) are gathered, ranked and the
+// first k written out. Otherwise (a chunk holding more than m of the row's k largest: sorted rows, ties, values
+// clustered by index) the merger reads again from x the chunks that may have left out part of the row's k largest
+// (below). The counter is zeroed for the next launch either way.
 template <typename T, bool VEC, bool DRAW>
 __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPRs, four workgroups per CU
     topk_wide(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
@@ -2048,6 +2050,11 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   // margin, at most k
   const long long share = ((long long)k * chunk + cols - 1) / cols;
   const int m = nchunks > 1 && 2 * share + kListSlack < k ? 2 * (int)share + kListSlack : k;
+  // the lists' stride: when m < k, room for the candidates at or above the admission key, which has m distinct
+  // elements at or above it (about 1.1 m on continuous data), and less than k, so that the separators fit after the
+  // lists in the row's nchunks * k slots of work
+  const int lsr = (m + m / 8 + 16 + 63) / 64 * 64;
+  const int ls = m < k ? (lsr < k ? lsr : k - 1) : m;
   const bool split = nchunks > 1;
   const int kt = split ? m : k;  // the buffer's target: the chunk's m largest, or the row's k
   uint32_t thr = 0, thq = 0, cmax = 0;  // the admission key, the q-bound, the chunk's largest key
@@ -2150,27 +2157,40 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     return;
   }
   TOPK_STAGE(3);
-  // publish: the chunk's m largest (the list, zero-padded to m when it holds fewer), its separator (m < k) and the
-  // header (k-bound key << 32 | q-bound key) in the row's output
+  // publish: the list (zero-padded to ls), its separator (m < k) and the header (k-bound key << 32 | q-bound key) in
+  // the row's output. When m < k the list holds the chunk's candidates as they are when they fit ls (C5 at k = 1024:
+  // about 350 of at most 384), else their m largest (cut_publish).
   u64* wr = work + row * (long long)nchunks * k;
-  u64* mine = wr + (long long)part * m;
+  u64* mine = wr + (long long)part * ls;
   if (s.count > kWideList) prune(s, m);
   const int n = s.count;
-  u64 kth = 0;  // the chunk's m-th largest, the smallest entry of its list (0: the list holds fewer than m)
-  if (n > m) {
-    kth = cut_publish(s, n, m, mine, thr, cmax, cut_zeroed);
+  u64 kth = 0;  // the separator (m < k): every element of the chunk not in its list lies below it (0: none is left out)
+  if (n > ls) {
+    kth = cut_publish(s, n, m, mine, thr, cmax, cut_zeroed);  // the m-th largest, the smallest entry of the list
+    for (int i = m + (int)threadIdx.x; i < ls; i += kThreads)
+      __hip_atomic_store(mine + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
-    if (n == m) {  // (block-uniform)
+    if (m < k) {
+      // Every element left out lies below the last admission key (those of earlier tiles were no higher) or below the
+      // prunes' floor s.thr. Candidates below the separator (admitted by an earlier tile's lower key, or by a 16-bit
+      // compare of the key's upper half) are left out too, so that every list entry lies at or above it (the second
+      // look at x reads a chunk's elements below its separator only). The key has m distinct elements at or above it,
+      // all kept: with fewer than m candidates (no usable bound: every element appended) none is left out.
+      const u64 ak = (u64)thr << 32;
+      kth = n < m ? 0ull : ak > s.thr ? ak : s.thr;
+    } else if (n == m) {  // (block-uniform) the chunk's k largest: their smallest gives the header's k-bound
       u64 mn = ~0ull;
       for (int i = threadIdx.x; i < n; i += kThreads) mn = s.buf[i] < mn ? s.buf[i] : mn;
       kth = block_ext64<false>(mn, s);
     }
-    for (int i = threadIdx.x; i < m; i += kThreads)
-      __hip_atomic_store(mine + i, i < n ? s.buf[i] : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = threadIdx.x; i < ls; i += kThreads) {
+      const u64 e = i < n ? s.buf[i] : 0ull;
+      __hip_atomic_store(mine + i, e >= kth ? e : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   TOPK_STAGE(4);
   u64* heads = reinterpret_cast<u64*>(indices + row * k);
-  u64* seps = wr + (long long)nchunks * m;  // m < k: nchunks * (m + 1) <= nchunks * k slots of the row
+  u64* seps = wr + (long long)nchunks * ls;  // m < k: nchunks * (ls + 1) <= nchunks * k slots of the row
   if (threadIdx.x == 0) {
     const uint32_t kb = m < k ? thk : (uint32_t)(kth >> 32) > thr ? (uint32_t)(kth >> 32) : thr;
     __hip_atomic_store(heads + part, ((u64)kb << 32) | thq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2183,12 +2203,12 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   // merge (the row's last arrival): the floor from the headers, then every list's entries at or above it
   auto ld = [&](const u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   const int t = (int)threadIdx.x, lane = lane_id(), wave = wave_id();
-  // Rows whose lists fit the registers (C5: 8 x 326 entries) read them all at once, right after the headers: the
+  // Rows whose lists fit the registers (C5: 8 x 384 entries) read them all at once, right after the headers: the
   // floor's reduction runs while the lists' loads are in flight (loads return in order), and one block scan places
   // the entries at or above it.
-  constexpr int kGatherAll = 2816;  // list entries the merger reads in one batch
+  constexpr int kGatherAll = 3072;  // list entries the merger reads in one batch
   constexpr int PB = kGatherAll / kThreads;
-  const int entries = nchunks * m;  // the row's lists, contiguous in wr
+  const int entries = nchunks * ls;  // the row's lists, contiguous in wr
   u64 kmax = 0, qmn = ~0ull, smax = 0;
   const u64 h0 = t < nchunks ? ld(heads + t) : 0ull;
   const u64 s0 = m < k && t < nchunks ? ld(seps + t) : 0ull;
@@ -2294,11 +2314,11 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     u64 cv[kInFlight][PER];
     unsigned ns = 0;  // entries at or above the largest separator
     auto load = [&](int c, u64 (&v)[PER]) {
-      const u64* list = wr + (long long)c * m;
+      const u64* list = wr + (long long)c * ls;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int at = i * kThreads + (int)threadIdx.x;
-        v[i] = at < m ? ld(list + at) : 0ull;
+        v[i] = at < ls ? ld(list + at) : 0ull;
       }
     };
     auto take = [&](const u64 (&v)[PER]) {  // appends the entries at or above the floor (room for a list is kept)
