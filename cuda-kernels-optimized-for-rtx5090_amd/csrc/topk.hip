@@ -1968,30 +1968,35 @@ __device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t 
     sum += (lo & 0xffffu) + (lo >> 16) + (hi & 0xffffu) + (hi >> 16);
   }
   const uint32_t incl = wave_incl_u32(sum);
-  if (lane_id() == kWave - 1) s.wsum[wave_id()] = incl;
+  const int wv = __builtin_amdgcn_readfirstlane(wave_id());  // (a scalar: a vector copy was spilled to memory)
+  if (lane_id() == kWave - 1) s.wsum[wv] = incl;
   __syncthreads();
   uint32_t run = incl - sum, total = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
     const uint32_t v = s.wsum[w];
-    run += w < wave_id() ? v : 0u;
+    run += w < wv ? v : 0u;
     total += v;
   }
   if (total < (uint32_t)k) return false;
   // the thread whose buckets hold the k-th (q-th) from the top records the bucket: the last one whose count from the
-  // top before it is short of k (q)
-  uint32_t acc = run;
-  int atk = 0, atq = 0, atk2 = 0;
+  // top before it is short of k (q); only the waves holding such a thread walk their buckets
+  const bool hk = run < (uint32_t)k && (uint32_t)k <= run + sum, hq = run < (uint32_t)q && (uint32_t)q <= run + sum;
+  const bool hk2 = run < (uint32_t)k2 && (uint32_t)k2 <= run + sum;
+  if (hk || hq || hk2) {
+    uint32_t acc = run;
+    int atk = 0, atq = 0, atk2 = 0;
 #pragma unroll
-  for (int i = 0; i < BPT; ++i) {
-    atk = acc < (uint32_t)k ? i : atk;
-    atq = acc < (uint32_t)q ? i : atq;
-    atk2 = acc < (uint32_t)k2 ? i : atk2;
-    acc += (uint32_t)(w4[i >> 2] >> (16 * (i & 3))) & 0xffffu;
+    for (int i = 0; i < BPT; ++i) {
+      atk = acc < (uint32_t)k ? i : atk;
+      atq = acc < (uint32_t)q ? i : atq;
+      atk2 = acc < (uint32_t)k2 ? i : atk2;
+      acc += (uint32_t)(w4[i >> 2] >> (16 * (i & 3))) & 0xffffu;
+    }
+    if (hk) s.hist[0] = (unsigned)(t * BPT + atk);
+    if (hq) s.hist[1] = (unsigned)(t * BPT + atq);
+    if (hk2) s.hist[2] = (unsigned)(t * BPT + atk2);
   }
-  if (run < (uint32_t)k && (uint32_t)k <= run + sum) s.hist[0] = (unsigned)(t * BPT + atk);
-  if (run < (uint32_t)q && (uint32_t)q <= run + sum) s.hist[1] = (unsigned)(t * BPT + atq);
-  if (run < (uint32_t)k2 && (uint32_t)k2 <= run + sum) s.hist[2] = (unsigned)(t * BPT + atk2);
   __syncthreads();
   auto edge = [&](unsigned b) {
     const u64 below = (u64)(b + 1) << sh;
@@ -2065,7 +2070,6 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   }
   __syncthreads();
   TOPK_STAGE(0);
-  bool cut_zeroed = false;
   const int kw = (kt + kWaves - 1) / kWaves, kwq = (q + kWaves - 1) / kWaves;
   using TL = Tile<T, VEC>;
   constexpr int TE = kThreads * kTileE;
@@ -2078,15 +2082,6 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     tile.group_keys(g);
     TOPK_STAGE_AT(1, g[0]);
     TOPK_WAVE_STAGE_AT(g[0]);
-    const bool last_tile = end - t0 <= TE;
-    if (last_tile && split) {
-      // the cut's counters, zeroed ahead of the bounds' barriers while no wave appends (the buffer holds at most
-      // kWideList candidates between tiles); kept zero unless this tile's appends pass kWideList
-      u64* cz = s.buf + kWideList + (int)threadIdx.x * (kRankBuckets / 4 / kThreads);
-#pragma unroll
-      for (int i = 0; i < kRankBuckets / 4 / kThreads; ++i) cz[i] = 0ull;
-      if (threadIdx.x == 0) s.members = 0;
-    }
     uint32_t tb, qb, kb2 = 0, tm;
     if (!hist_bounds(s, red, g, kt, split ? q : 0, kt < k ? k : 0, tb, qb, kb2, tm)) {
       // the group maxima spread over more than the window: each wave's bound from a search over its whole range
@@ -2112,17 +2107,11 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
         // reaching the bound in its quarter of s.buf[kWideList, kWideCap) (free after the bounds' last read), and
         // the appends stay below kWideList meanwhile
         lim = kWideList;
-        u64* area = s.buf + kWideList + wave_id() * ((kWideCap - kWideList) / kWaves);
-        u32x4* stage = reinterpret_cast<u32x4*>(area);
+        u32x4* stage = reinterpret_cast<u32x4*>(s.buf + kWideList + wave_id() * ((kWideCap - kWideList) / kWaves));
         if constexpr (sizeof(T) == 4) {
           if (!tile.template stage_append<kStageVecs>(s, thr, stage, reinterpret_cast<uint32_t*>(stage + kStageVecs),
                                                       lim))
             tile.template filter_append<false>(s, thr, lim);
-        }
-        if (last_tile && split && area < s.buf + kWideList + kRankBuckets / 4) {
-          // the cut's counters this wave's area overlaps, zeroed again (LDS operations of one wave complete in order)
-#pragma unroll
-          for (int i = 0; i < (kWideCap - kWideList) / kWaves / kWave; ++i) area[i * kWave + lane_id()] = 0ull;
         }
       } else {
         tile.template filter_append<false>(s, thr, lim);
@@ -2130,7 +2119,6 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
       __syncthreads();
       redo = s.count > lim;
     }
-    cut_zeroed = last_tile && !redo && s.count <= kWideList;  // (the appends left the counters alone)
     if (redo) {  // every element may pass, or the buffer overflowed: append again vector by vector, pruning to kt
       __syncthreads();
       if (threadIdx.x == 0) s.count = cnt0;
@@ -2166,7 +2154,7 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   const int n = s.count;
   u64 kth = 0;  // the separator (m < k): every element of the chunk not in its list lies below it (0: none is left out)
   if (n > ls) {
-    kth = cut_publish(s, n, m, mine, thr, cmax, cut_zeroed);  // the m-th largest, the smallest entry of the list
+    kth = cut_publish(s, n, m, mine, thr, cmax, false);  // the m-th largest, the smallest entry of the list
     for (int i = m + (int)threadIdx.x; i < ls; i += kThreads)
       __hip_atomic_store(mine + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
