@@ -496,7 +496,7 @@ TOPK_STAGES = {
                   (10, "list settled"), (3, "chunk's tiles done"),
                   (4, "chunk list published"), (5, "arrival counted"), (6, "merge: floor, candidates counted"),
                   (7, "merge: candidates compacted"), (8, "row written")],
-    "topk_wide": [(0, "start"), (1, "loads landed (wave 0)"), (2, "bounds"), (3, "tile appended"), (4, "cut to k"),
+    "topk_wide": [(0, "start"), (1, "loads landed (wave 0)"), (2, "bounds"), (3, "tile appended"), (4, "list published"),
                   (5, "arrival counted"), (6, "merge: floor from the headers"), (7, "merge: lists gathered"),
                   (8, "row written")],
 }
