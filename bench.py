@@ -498,7 +498,8 @@ TOPK_STAGES = {
                   (7, "merge: candidates compacted"), (8, "row written")],
     "topk_wide": [(0, "start"), (1, "loads landed (wave 0)"), (2, "bounds"), (3, "tile appended"), (4, "list published"),
                   (5, "arrival counted"), (6, "merge: floor from the headers"), (7, "merge: lists gathered"),
-                  (8, "row written")],
+                  (12, "ordering: bucket counts"), (13, "ordering: bucket scan"), (14, "ordering: scatter"),
+                  (15, "ordering: positions"), (8, "row written")],
 }
 STAGE_SLOTS, STAGE_WGS = 32, 4096
 STAGE_TICK_US = 0.01  # s_memrealtime runs at 100 MHz

@@ -1647,6 +1647,7 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
     slot[r] = r * kThreads + t < m ? (int)((atomicAdd(&cnt2[bk[r] >> 1], 1u << half) >> half) & 0xffffu) : 0;
   }
   __syncthreads();
+  TOPK_STAGE(12);
   // exclusive scan of the counts, bucket 0 (the largest candidates) first
   unsigned own[BPT], sum = 0;
 #pragma unroll
@@ -1667,10 +1668,12 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
     run += own[i];
   }
   __syncthreads();
+  TOPK_STAGE(13);
 #pragma unroll
   for (int r = 0; r < P; ++r)
     if (r * kThreads + t < m) sorted[first[bk[r]] + slot[r]] = c[r];
   __syncthreads();
+  TOPK_STAGE(14);
   // Ranked in bucket order: lane i takes sorted[i], so neighbouring lanes read the same bucket's members (LDS
   // broadcasts rather than scattered reads) and write neighbouring output positions. Every position first, then the
   // stores. A thread's reads are issued together, stage by stage (its entries, their buckets' ranges, the buckets'
@@ -1707,6 +1710,7 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
       pos[r] += (a > c[r]) + (j + 1 < n[r] && e1 > c[r]) + (j + 2 < n[r] && e2 > c[r]) + (j + 3 < n[r] && e3 > c[r]);
     }
   }
+  TOPK_STAGE_AT(15, pos[0]);
 #pragma unroll
   for (int r = 0; r < P; ++r) {
     if (r * kThreads >= m) break;

@@ -254,6 +254,24 @@ def test_stale_caller_buffers(pkg, oracle, dev, dt):
             check(pkg, oracle, x, k, dev, chunk=chunk, what="stale buffers", poison=True)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_wide_lists_uncut_cut_and_second_look(pkg, oracle, dev, dt):
+    # k > 64 over 8 chunks of 16384, the caller's buffers stale: random rows publish their candidates uncut (lists
+    # zero-padded past them); values from a few dozen integers tie at the admission key, so that a chunk's candidates
+    # overflow its list and are cut to m (the slots past m zeroed); rows whose largest values sit in one chunk take
+    # the second look at x
+    g = torch.Generator().manual_seed(43)
+    x = (torch.randn(4, 8 * 16384, generator=g) * 2).to(dt)
+    ties = torch.randint(0, 50, (4, 8 * 16384), generator=g).float().to(dt)
+    hot = torch.randn(4, 8 * 16384, generator=g) * 2
+    for r in range(4):
+        hot[r, r * 16384:(r + 1) * 16384] += 4.0 if r % 2 == 0 else 0.6
+    hot = hot.to(dt)
+    for k in (300, 1024):
+        for what, t in (("uncut lists", x), ("cut lists", ties), ("one hot chunk", hot)):
+            check(pkg, oracle, t, k, dev, chunk=16384, what=f"wide, {what}", poison=True)
+
+
 def test_invalid_arguments(pkg, dev):
     L = lib(pkg)
     s = torch.cuda.current_stream().cuda_stream
