@@ -1588,45 +1588,21 @@ static_assert(kStageVecs * 20 <= (kWideCap - kWideList) / kWaves * 8,
 
 constexpr int kRankBuckets = 4096;  // buckets of write_ranked (16-bit counters and first positions)
 
-// Writes the k largest of the m candidates s.buf[0, m) (k <= m <= kWideList), in order, as the output row: the
-// candidates are bucketed by their distance below the largest, (max - c) >> sh with sh chosen so that the range fills
-// kRankBuckets buckets, with 16-bit LDS counters (two to a word, so that counters and first positions fit beside the
-// bucketed copy); an exclusive scan of the counts gives each bucket's first output position;
-// the candidates are scattered by bucket into LDS, and each one's position is its bucket's first plus the number of
-// its bucket's members above it. Nearly linear on spread-out values; a bucket holding many candidates (values
-// clustered far below an outlier) costs its size per member. `lo`, when not 0, is a lower bound of the candidates known
-// to the caller, used in place of their minimum (a candidate below it would still be ordered exactly: it lands in the
-// last bucket, below every other bucket's members). `hi`, when not 0 (with lo not 0), is the largest candidate, known
-// to the caller; the block is then not reduced here, and the caller's barrier after its writes of s.buf suffices.
-// `zeroed`: the caller has zeroed the counters (s.buf[kWideList, kWideList + kRankBuckets / 4)) behind that barrier.
-// Every thread calls it.
-template <typename T, typename S>
-__device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, long long* indices, long long row,
-                                             u64 lo, u64 hi = 0, bool zeroed = false) {
+// The ordering of write_ranked (below) over m candidates (k <= m <= kWideList) held in registers: cin[r] where in[r],
+// NS slots per thread, every candidate in [mn, mx] (mx the largest, or mn a lower bound: a candidate below it lands
+// in the last bucket and is still ordered exactly). `zeroed`: the caller has zeroed the counters (s.buf[kWideList,
+// kWideList + kRankBuckets / 4)) behind a barrier. The scatter into s.buf[0, m) follows the barriers of the counts, so
+// the caller's reads of it before the call need no barrier of their own. Every thread calls it.
+template <typename T, int NS, typename S>
+__device__ __forceinline__ void write_ranked_regs(S& s, const u64 (&cin)[NS], const bool (&in)[NS], int m, int k,
+                                                  void* values, long long* indices, long long row, u64 mx, u64 mn,
+                                                  bool zeroed) {
   constexpr int P = kWideList / kThreads;
   constexpr int BPT = kRankBuckets / kThreads;  // buckets per thread in the scan
   static_assert(kWideList * 2 <= kWideCap && kRankBuckets * 2 * sizeof(uint16_t) <= kWideList * sizeof(u64) &&
                     kWideList < 65536 && BPT % 2 == 0,
                 "the bucketed copy, the counters and the first positions share the buffer; counts fit 16 bits");
   const int t = (int)threadIdx.x;
-  u64 c[P];
-  u64 mx = 0, mn = ~0ull;
-#pragma unroll
-  for (int r = 0; r < P; ++r) {
-    const int i = r * kThreads + t;
-    c[r] = i < m ? s.buf[i] : 0ull;
-    if (i < m) {
-      mx = c[r] > mx ? c[r] : mx;
-      mn = c[r] < mn ? c[r] : mn;
-    }
-  }
-  if (hi && lo) {  // the reads above need no barrier before the writes below: the counters lie past s.buf[0, m), and
-    mx = hi;        // the scatter into s.buf[0, m) comes after the barriers of the counts
-    mn = lo;
-  } else {
-    mx = block_ext64<true>(mx, s);  // also orders every read of s.buf above before the writes below
-    mn = lo ? lo : block_ext64<false>(mn, s);
-  }
   const u64 range = mx - mn;
   const int bits = range ? 64 - __clzll(range) : 0;
   const int sh = bits > 12 ? bits - 12 : 0;  // (mx - mn) >> sh < 4096 = kRankBuckets
@@ -1638,13 +1614,13 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
     for (int w = t; w < kRankBuckets / 2; w += kThreads) cnt2[w] = 0;
     __syncthreads();
   }
-  int bk[P], slot[P];
+  int bk[NS], slot[NS];
 #pragma unroll
-  for (int r = 0; r < P; ++r) {
-    const u64 d = (mx - c[r]) >> sh;
+  for (int r = 0; r < NS; ++r) {
+    const u64 d = (mx - cin[r]) >> sh;
     bk[r] = d < (u64)kRankBuckets ? (int)d : kRankBuckets - 1;
     const int half = 16 * (bk[r] & 1);
-    slot[r] = r * kThreads + t < m ? (int)((atomicAdd(&cnt2[bk[r] >> 1], 1u << half) >> half) & 0xffffu) : 0;
+    slot[r] = in[r] ? (int)((atomicAdd(&cnt2[bk[r] >> 1], 1u << half) >> half) & 0xffffu) : 0;
   }
   __syncthreads();
   TOPK_STAGE(12);
@@ -1670,8 +1646,8 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   __syncthreads();
   TOPK_STAGE(13);
 #pragma unroll
-  for (int r = 0; r < P; ++r)
-    if (r * kThreads + t < m) sorted[first[bk[r]] + slot[r]] = c[r];
+  for (int r = 0; r < NS; ++r)
+    if (in[r]) sorted[first[bk[r]] + slot[r]] = cin[r];
   __syncthreads();
   TOPK_STAGE(14);
   // Ranked in bucket order: lane i takes sorted[i], so neighbouring lanes read the same bucket's members (LDS
@@ -1681,6 +1657,7 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
   // r * kThreads >= m (C5 at k = 65 fills one of the eight): every index stays inside the buffer whether or not the
   // entry exists (i < kWideList; f + 3 <= m + 3 < kWideCap), and a missing entry's position is discarded. Buckets of
   // more than four members (rare) are finished after.
+  u64 c[P];
   int pos[P], f[P], n[P];
 #pragma unroll
   for (int r = 0; r < P; ++r) {
@@ -1720,6 +1697,46 @@ __device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, l
       indices[row * k + pos[r]] = composite_index(c[r]);
     }
   }
+}
+
+// Writes the k largest of the m candidates s.buf[0, m) (k <= m <= kWideList), in order, as the output row, by
+// write_ranked_regs: the candidates are bucketed by their distance below the largest, (max - c) >> sh with sh chosen
+// so that the range fills kRankBuckets buckets, with 16-bit LDS counters (two to a word, so that counters and first
+// positions fit beside the bucketed copy); an exclusive scan of the counts gives each bucket's first output position;
+// the candidates are scattered by bucket into LDS, and each one's position is its bucket's first plus the number of
+// its bucket's members above it. Nearly linear on spread-out values; a bucket holding many candidates (values
+// clustered far below an outlier) costs its size per member. `lo`, when not 0, is a lower bound of the candidates known
+// to the caller, used in place of their minimum (a candidate below it would still be ordered exactly: it lands in the
+// last bucket, below every other bucket's members). `hi`, when not 0 (with lo not 0), is the largest candidate, known
+// to the caller; the block is then not reduced here, and the caller's barrier after its writes of s.buf suffices.
+// `zeroed`: the caller has zeroed the counters (s.buf[kWideList, kWideList + kRankBuckets / 4)) behind that barrier.
+// Every thread calls it.
+template <typename T, typename S>
+__device__ __forceinline__ void write_ranked(S& s, int m, int k, void* values, long long* indices, long long row,
+                                             u64 lo, u64 hi = 0, bool zeroed = false) {
+  constexpr int P = kWideList / kThreads;
+  const int t = (int)threadIdx.x;
+  u64 c[P];
+  bool in[P];
+  u64 mx = 0, mn = ~0ull;
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    const int i = r * kThreads + t;
+    in[r] = i < m;
+    c[r] = in[r] ? s.buf[i] : 0ull;
+    if (in[r]) {
+      mx = c[r] > mx ? c[r] : mx;
+      mn = c[r] < mn ? c[r] : mn;
+    }
+  }
+  if (hi && lo) {  // the reads above need no barrier before the writes below: the counters lie past s.buf[0, m), and
+    mx = hi;        // the scatter into s.buf[0, m) comes after the barriers of the counts
+    mn = lo;
+  } else {
+    mx = block_ext64<true>(mx, s);  // also orders every read of s.buf above before the writes below
+    mn = lo ? lo : block_ext64<false>(mn, s);
+  }
+  write_ranked_regs<T>(s, c, in, m, k, values, indices, row, mx, mn, zeroed);
 }
 
 // Writes the k largest of a chunk's m candidates s.buf[0, m) (k < m <= kWideList) to list[0, k) with device-coherent
@@ -2097,7 +2114,7 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
     }
     thr = tb > thr ? tb : thr;
     thq = qb > thq ? qb : thq;
-    thk = kb2 > thk ? kb2 : thk;
+    thk = __builtin_amdgcn_readfirstlane(kb2 > thk ? kb2 : thk);  // (block-uniform: kept in a scalar register)
     cmax = tm > cmax ? tm : cmax;
     TOPK_STAGE(2);
     tile.opaque();
@@ -2243,12 +2260,13 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   if (entries <= kGatherAll) {
     unsigned n = 0, ns = 0;
     u64 mx = 0;
+    bool keep[PB];
 #pragma unroll
     for (int i = 0; i < PB; ++i) {
-      const bool keep = e[i] >= floor;
-      n += keep ? 1u : 0u;
+      keep[i] = e[i] >= floor;
+      n += keep[i] ? 1u : 0u;
       ns += e[i] >= smax ? 1u : 0u;
-      mx = keep && e[i] > mx ? e[i] : mx;
+      mx = keep[i] && e[i] > mx ? e[i] : mx;
     }
     const unsigned incl = wave_incl_u32(n);
     const unsigned wns = (unsigned)wave_sum((float)ns);  // exact: at most kGatherAll
@@ -2272,6 +2290,15 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
       above += s.hist[w];
     }
     whole = smax == 0 || above >= (unsigned)k;
+    if (whole && nm <= (unsigned)kWideList) {
+      // (block-uniform) ordered straight from the registers: the counters were zeroed behind the barrier above
+      TOPK_STAGE(7);
+      write_ranked_regs<T>(s, e, keep, (int)nm, k, values, indices, row, mx, floor, true);
+      TOPK_STAGE(8);
+      if (t == 0) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sample_list<T>(sa, u, values, indices, row, k);
+      return;
+    }
     if (nm <= (unsigned)kWideCap) {  // (block-uniform) all of them fit the buffer: one write
 #pragma unroll
       for (int i = 0; i < PB; ++i)
