@@ -272,6 +272,33 @@ def test_wide_lists_uncut_cut_and_second_look(pkg, oracle, dev, dt):
             check(pkg, oracle, t, k, dev, chunk=16384, what=f"wide, {what}", poison=True)
 
 
+def test_random_shapes_and_chunkings(pkg, oracle, dev):
+    # seeded random shapes, k (every class up to 1024) and chunkings (the plan's and explicit ones, split and unsplit),
+    # fp32 and bf16, stale caller buffers: each against the oracle
+    rng = np.random.default_rng(2024)
+    g = torch.Generator().manual_seed(2024)
+    for case in range(160):
+        rows = int(rng.integers(1, 9))
+        cols = int(rng.integers(70, 140000))
+        k = int(min(cols, rng.choice([1, 2, 13, 50, 64, 65, 100, 150, 257, 300, 600, 1000, 1024])))
+        dt = torch.float32 if case % 3 else torch.bfloat16
+        pattern = case % 4
+        if pattern == 0:
+            x = torch.randn(rows, cols, generator=g) * 3
+        elif pattern == 1:  # few distinct values: ties everywhere
+            x = torch.randint(0, 40, (rows, cols), generator=g).float()
+        elif pattern == 2:  # negative rows (log-probabilities)
+            x = -torch.rand(rows, cols, generator=g) * 20
+        else:  # one hot region per row
+            x = torch.randn(rows, cols, generator=g)
+            at = int(rng.integers(0, cols))
+            x[:, at:at + 3000] += 3.0
+        chunk = None if case % 2 else int(rng.choice([2048, 4096, 16384, 32768])) // 8 * 8
+        if chunk is not None and chunk >= cols:
+            chunk = None
+        check(pkg, oracle, x.to(dt), k, dev, chunk=chunk, what=f"random case {case}", poison=bool(case % 2))
+
+
 def test_invalid_arguments(pkg, dev):
     L = lib(pkg)
     s = torch.cuda.current_stream().cuda_stream
