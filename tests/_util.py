@@ -35,17 +35,17 @@ def is_nan16(a, fp16=False):
     return ((a & 0x7F80) == 0x7F80) & ((a & 0x007F) != 0)
 
 
-def assert_rel(got, ref, rtol=1e-5, what=""):
-    """|got - ref| <= rtol * |ref| elementwise (NaN must match NaN)."""
+def assert_rel(got, ref, rtol=1e-5, what="", atol=0.0):
+    """|got - ref| <= rtol * |ref| + atol elementwise (NaN must match NaN)."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     nan_g, nan_r = np.isnan(got), np.isnan(ref)
     assert np.array_equal(nan_g, nan_r), f"{what}: NaN positions differ"
-    ok = nan_r | (np.abs(got - ref) <= rtol * np.abs(ref))
+    ok = nan_r | (np.abs(got - ref) <= rtol * np.abs(ref) + atol)
     if not ok.all():
         i = np.argwhere(~ok)[0]
-        raise AssertionError(f"{what}: {int((~ok).sum())} elements beyond rtol {rtol}; first at {tuple(i)}: "
-                             f"got {got[tuple(i)]!r} ref {ref[tuple(i)]!r}")
+        raise AssertionError(f"{what}: {int((~ok).sum())} elements beyond rtol {rtol} + atol {atol}; first at "
+                             f"{tuple(i)}: got {got[tuple(i)]!r} ref {ref[tuple(i)]!r}")
 
 
 def assert_ulp(got_bits, ref_bits, max_ulp=1, what=""):

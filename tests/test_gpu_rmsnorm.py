@@ -39,6 +39,20 @@ def test_shapes(pkg, oracle, dev, dtype, rows, cols):
     check(pkg, oracle, dev, x, w, what=f"{rows}x{cols} weighted")
 
 
+def test_random_shapes(pkg, oracle, dev):
+    # seeded random shapes (odd lengths included), both dtypes, with and without the weight, several eps
+    rng = np.random.default_rng(78)
+    g = torch.Generator().manual_seed(78)
+    for case in range(60):
+        cols = int(np.exp(rng.uniform(0, np.log(100000))))
+        rows = int(rng.integers(1, max(2, min(300, 2_000_000 // cols))))
+        dtype = torch.bfloat16 if case % 2 else torch.float16
+        x = (torch.randn(rows, cols, generator=g) * float(rng.choice([0.01, 1.0, 20.0]))).to(dtype)
+        w = (torch.rand(cols, generator=g) + 0.5).to(dtype) if case % 3 else None
+        eps = float(rng.choice([1e-6, 1e-5, 1e-3]))
+        check(pkg, oracle, dev, x, w, eps, what=f"random case {case}")
+
+
 def test_many_rows_and_eps(pkg, oracle, dev):
     g = torch.Generator().manual_seed(3)
     x = torch.randn(10000, 1024, generator=g).bfloat16()

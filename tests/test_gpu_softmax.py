@@ -1,6 +1,11 @@
 """GPU parity of softmax (build/softmax/libkernel.so through the reference ABI `launch`) against the oracle.
 
-fp32: |y - oracle| <= 1e-5 |oracle| elementwise (the oracle is the fp64 softmax rounded once); bf16: within 1 ulp.
+fp32: |y - oracle| <= 1e-5 |oracle| + 2^-147 elementwise (the oracle is the fp64 softmax rounded once); bf16: within
+1 ulp. The absolute term is four ulps of the fp32 subnormal range (2^-149 each), where a relative bound cannot hold for
+any computation that rounds more than once: exp(x - max) rounded to a subnormal, then scaled by the row's 1 / sum, is
+off by up to about 1.5 ulps there, and the reference's own PyTorch path (torch.softmax, fp32 on the CPU) is off by up
+to 33 ulps from the oracle on rows whose outputs reach that range (checked in tests/test_oracle.py). Outputs of
+normal magnitude keep the relative bound alone.
 Shapes cover every tier: wave-per-row and workgroup-per-row rows (full and ragged), the single-pass co-resident tier
 for long rows (one row per workgroup, and row groups walking several rows when the rows' chunks do not all fit at
 once), the two-pass stream tier for rows beyond it, and the generic tier for lengths that are not a multiple of the
@@ -19,12 +24,13 @@ from _util import assert_rel, assert_ulp, bits16
 pytestmark = pytest.mark.gpu
 
 FP32_TOL = 1e-5
+FP32_SUBNORMAL_ATOL = 2.0 ** -147
 
 
 def run_fp32(pkg, oracle, dev, x, what):
     print(f"[softmax fp32] {what} shape={tuple(x.shape)}", flush=True)
     y = pkg.softmax(x.to(dev)).cpu()
-    assert_rel(y.numpy(), oracle.softmax(x.numpy(), "fp32"), FP32_TOL, what)
+    assert_rel(y.numpy(), oracle.softmax(x.numpy(), "fp32"), FP32_TOL, what, FP32_SUBNORMAL_ATOL)
     return y
 
 
@@ -45,6 +51,25 @@ def test_bf16_shapes(pkg, oracle, dev, rows, cols):
     assert_ulp(bits16(y), oracle.softmax(bits16(x), "bf16"), 1, f"bf16 {rows}x{cols}")
 
 
+def test_random_shapes(pkg, oracle, dev):
+    # seeded random shapes across every tier (short rows to rows of 2^18 and beyond), fp32 and bf16, with spreads from
+    # flat to peaked rows
+    rng = np.random.default_rng(77)
+    g = torch.Generator().manual_seed(77)
+    for case in range(60):
+        cols = int(np.exp(rng.uniform(0, np.log(300000))))
+        rows = int(rng.integers(1, max(2, min(300, 2_000_000 // cols))))
+        scale = float(rng.choice([0.1, 1.0, 3.0, 30.0]))
+        x = torch.randn(rows, cols, generator=g) * scale
+        if case % 2:
+            run_fp32(pkg, oracle, dev, x, f"random case {case}")
+        else:
+            xb = x.bfloat16()
+            print(f"[softmax bf16] random case {case} {rows}x{cols}", flush=True)
+            y = pkg.softmax(xb.to(dev))
+            assert_ulp(bits16(y), oracle.softmax(bits16(xb), "bf16"), 1, f"bf16 random case {case} {rows}x{cols}")
+
+
 def test_many_rows_persistent(pkg, oracle, dev):
     # more rows than resident workgroups: every workgroup walks several rows
     g = torch.Generator().manual_seed(5)
@@ -59,7 +84,8 @@ def test_misaligned_and_special_values(pkg, oracle, dev):
     y = torch.empty_like(x)
     lib = pkg.candidate("softmax")._lib
     assert lib.launch(x.data_ptr(), y.data_ptr(), 4, 1024, 0, 256, 1024, torch.cuda.current_stream().cuda_stream) == 0
-    assert_rel(y.cpu().numpy(), oracle.softmax(x.cpu().numpy(), "fp32"), FP32_TOL, "misaligned")
+    assert_rel(y.cpu().numpy(), oracle.softmax(x.cpu().numpy(), "fp32"), FP32_TOL, "misaligned",
+               FP32_SUBNORMAL_ATOL)
     s = torch.randn(4, 1024, generator=g)
     s[0, 10] = float("-inf")
     s[1, :] = float("-inf")
@@ -68,7 +94,7 @@ def test_misaligned_and_special_values(pkg, oracle, dev):
     y = pkg.softmax(s.to(dev)).cpu()
     assert y[0, 10] == 0 and torch.isnan(y[1]).all() and torch.isnan(y[2]).all() and (y[3, ::3] == 0).all()
     ref = oracle.softmax(s.numpy(), "fp32")
-    assert_rel(y[[0, 3]].numpy(), ref[[0, 3]], FP32_TOL, "special values")
+    assert_rel(y[[0, 3]].numpy(), ref[[0, 3]], FP32_TOL, "special values", FP32_SUBNORMAL_ATOL)
 
 
 def test_long_rows_with_infinite_chunks(pkg, oracle, dev):
@@ -79,7 +105,7 @@ def test_long_rows_with_infinite_chunks(pkg, oracle, dev):
     y = pkg.softmax(x.to(dev)).cpu()
     assert torch.isnan(y[1]).all()
     ref = oracle.softmax(x.numpy(), "fp32")
-    assert_rel(y[[0, 2]].numpy(), ref[[0, 2]], FP32_TOL, "long rows")
+    assert_rel(y[[0, 2]].numpy(), ref[[0, 2]], FP32_TOL, "long rows", FP32_SUBNORMAL_ATOL)
 
 
 @pytest.mark.parametrize("rows,cols,dtype", [(64, 262144, "fp32"), (3, 70000, "fp32"), (1, 1 << 20, "fp32"),
@@ -104,7 +130,7 @@ def test_long_rows_single_pass_and_stream(pkg, oracle, dev, rows, cols, dtype):
             if dtype == "bf16":
                 assert_ulp(bits16(y), ref, 1, f"tier {tier}")
             else:
-                assert_rel(y.cpu().numpy(), ref, FP32_TOL, f"tier {tier}")
+                assert_rel(y.cpu().numpy(), ref, FP32_TOL, f"tier {tier}", FP32_SUBNORMAL_ATOL)
     finally:
         lib.softmax_tune(5, 0)
 
@@ -133,7 +159,7 @@ def test_coresident_graph_replay(pkg, oracle, dev, dtype):
         if dtype == "bf16":
             assert_ulp(bits16(y), ref(x), 1, what)
         else:
-            assert_rel(y.cpu().numpy(), ref(x), FP32_TOL, what)
+            assert_rel(y.cpu().numpy(), ref(x), FP32_TOL, what, FP32_SUBNORMAL_ATOL)
 
     xd, yd = xs[0].to(dev), torch.empty(rows, cols, dtype=xs[0].dtype, device=dev)
     x2, y2 = torch.empty_like(xd), torch.empty_like(yd)
@@ -199,7 +225,7 @@ def test_single_pass_fallback_when_the_wait_ends(pkg, oracle, dev, dtype):
             if dtype == "bf16":
                 assert_ulp(bits16(y), ref, 1, f"launch {rep}")
             else:
-                assert_rel(y.cpu().numpy(), ref, FP32_TOL, f"launch {rep}")
+                assert_rel(y.cpu().numpy(), ref, FP32_TOL, f"launch {rep}", FP32_SUBNORMAL_ATOL)
     finally:
         lib.softmax_tune(7, 0)
         lib.softmax_tune(5, 0)
@@ -208,7 +234,7 @@ def test_single_pass_fallback_when_the_wait_ends(pkg, oracle, dev, dtype):
     if dtype == "bf16":
         assert_ulp(bits16(y), ref, 1, "after")
     else:
-        assert_rel(y.cpu().numpy(), ref, FP32_TOL, "after")
+        assert_rel(y.cpu().numpy(), ref, FP32_TOL, "after", FP32_SUBNORMAL_ATOL)
 
 
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])
@@ -230,7 +256,7 @@ def test_single_pass_rows_beyond_one_wave(pkg, oracle, dev, dtype):
     if dtype == "bf16":
         assert_ulp(bits16(y), ref, 1, "256x262144")
     else:
-        assert_rel(y.cpu().numpy(), ref, FP32_TOL, "256x262144")
+        assert_rel(y.cpu().numpy(), ref, FP32_TOL, "256x262144", FP32_SUBNORMAL_ATOL)
     xs = x[:13, :70000].contiguous()
     refs = oracle.softmax(bits16(xs), "bf16") if dtype == "bf16" else oracle.softmax(xs.numpy(), "fp32")
     xd = xs.to(dev)
@@ -244,7 +270,7 @@ def test_single_pass_rows_beyond_one_wave(pkg, oracle, dev, dtype):
                 if dtype == "bf16":
                     assert_ulp(bits16(y), refs, 1, f"groups {groups}")
                 else:
-                    assert_rel(y.cpu().numpy(), refs, FP32_TOL, f"groups {groups}")
+                    assert_rel(y.cpu().numpy(), refs, FP32_TOL, f"groups {groups}", FP32_SUBNORMAL_ATOL)
     finally:
         lib.softmax_tune(4, 0)
         lib.softmax_tune(5, 0)
@@ -265,7 +291,8 @@ def test_single_pass_back_to_back_shapes(pkg, oracle, dev):
     ys = [pkg.softmax(d) for d in ds + ds]  # queued back to back, then checked
     for i, y in enumerate(ys):
         print(f"[softmax back-to-back] launch {i} shape={tuple(xs[i % 4].shape)}", flush=True)
-        assert_rel(y.cpu().numpy(), oracle.softmax(xs[i % 4].numpy(), "fp32"), FP32_TOL, f"launch {i}")
+        assert_rel(y.cpu().numpy(), oracle.softmax(xs[i % 4].numpy(), "fp32"), FP32_TOL, f"launch {i}",
+                   FP32_SUBNORMAL_ATOL)
 
 
 def test_empty_is_noop(pkg, dev):
@@ -288,7 +315,7 @@ def test_config_softmax_64x262144(pkg, oracle, dev):
     x = pkg.workloads.softmax_64x262144()["x"]
     y = run_fp32(pkg, oracle, dev, x, "softmax_64x262144")
     # the reference's own path (torch fp32) agrees within the same tolerance
-    assert_rel(y.numpy(), torch.softmax(x, -1).numpy(), 2 * FP32_TOL, "vs torch fp32")
+    assert_rel(y.numpy(), torch.softmax(x, -1).numpy(), 2 * FP32_TOL, "vs torch fp32", FP32_SUBNORMAL_ATOL)
 
 
 def test_tuning_overrides_keep_results(pkg, oracle, dev):
@@ -305,12 +332,12 @@ def test_tuning_overrides_keep_results(pkg, oracle, dev):
             for per_cu in (1, 2):
                 lib.softmax_tune(2, per_cu)
                 print(f"[softmax tune] waves={waves} nv={nv} per_cu={per_cu}", flush=True)
-                assert_rel(pkg.softmax(xd).cpu().numpy(), ref, FP32_TOL, f"w{waves} nv{nv}")
+                assert_rel(pkg.softmax(xd).cpu().numpy(), ref, FP32_TOL, f"w{waves} nv{nv}", FP32_SUBNORMAL_ATOL)
         lib.softmax_tune(0, 0), lib.softmax_tune(1, 0), lib.softmax_tune(2, 0)
         for tier in (2, 3):
             lib.softmax_tune(5, tier)
             print(f"[softmax tune] tier={tier}", flush=True)
-            assert_rel(pkg.softmax(xd).cpu().numpy(), ref, FP32_TOL, f"tier {tier}")
+            assert_rel(pkg.softmax(xd).cpu().numpy(), ref, FP32_TOL, f"tier {tier}", FP32_SUBNORMAL_ATOL)
     finally:
         for slot in range(8):
             lib.softmax_tune(slot, 0)

@@ -37,6 +37,21 @@ def test_softmax_fp32_matches_torch_fp64_and_fp32(oracle):
     assert_rel(torch.softmax(x, -1).numpy(), y, 1e-5, "torch fp32 softmax vs oracle")
 
 
+def test_softmax_subnormal_outputs_of_the_reference_path(oracle):
+    # rows whose outputs reach the fp32 subnormal range (x ~ N(0, 30^2)): there the reference's own PyTorch path
+    # (torch.softmax in fp32) differs from the oracle by more than 1e-5 relative on many elements, by up to 33
+    # subnormal ulps (2^-149 each; the GPU tests allow the kernels 4, 2^-147); normal outputs stay within 1e-5
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(15, 58817, generator=g) * 30
+    ref = oracle.softmax(x.numpy(), "fp32").astype(np.float64)
+    t = torch.softmax(x, dim=-1).numpy().astype(np.float64)
+    err = np.abs(t - ref)
+    sub = np.abs(ref) < 2.0 ** -126
+    assert ((err > 1e-5 * np.abs(ref)) & sub).sum() > 1000  # the relative bound alone fails the reference path
+    assert 4 * 2.0 ** -149 < err[sub].max() <= 64 * 2.0 ** -149
+    assert (err[~sub] <= 1e-5 * np.abs(ref[~sub])).all()
+
+
 def test_softmax_invariants(oracle):
     g = torch.Generator().manual_seed(12)
     x = torch.randint(-40, 40, (9, 300), generator=g).float()
