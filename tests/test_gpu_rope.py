@@ -64,6 +64,33 @@ def test_freq_path_inplace(pkg, oracle, dev, dtype, shape):
     assert np.array_equal(flat(qd), rq) and np.array_equal(flat(kd), rk)
 
 
+def test_random_shapes(pkg, oracle, dev):
+    # seeded random token counts, head counts and head sizes (the vector path for D % 16 == 0, the scalar path else),
+    # positions up to 2^20, both 16-bit dtypes, the cache path (three cache dtypes) and the on-the-fly path, bit for bit
+    from oracle import torch_paths
+    rng = np.random.default_rng(79)
+    for case in range(40):
+        D = int(rng.choice([16, 32, 48, 64, 80, 96, 128, 160, 256, 512, 2, 6, 40, 72, 200]))
+        B, S = int(rng.integers(1, 3)), int(rng.integers(1, 300))
+        Hq, Hk = int(rng.integers(1, 40)), int(rng.integers(1, 9))
+        dtype = torch.bfloat16 if case % 2 else torch.float16
+        far = case % 4 < 2 and case % 3 == 0  # on the fly only: a cache of 2^20 rows would not be small
+        q, k, pos = inputs(B, S, Hq, Hk, D, dtype, 1000 + case, max_pos=1 << 20 if far else 8192)
+        print(f"[rope random] case {case} {(B, S, Hq, Hk, D)} {dtype}", flush=True)
+        if case % 4 < 2:
+            inv_freq = pkg.workloads.rope_inv_freq(D)
+            qo, ko = pkg.rope(q.to(dev), k.to(dev), pos.to(dev), inv_freq=inv_freq.to(dev))
+            rq, rk = oracle.rope_freq(flat(q), flat(k), pos.view(-1).numpy(), inv_freq.numpy(), DT[dtype])
+        else:
+            cdtype = [torch.float32, torch.bfloat16, torch.float16][case % 3]
+            P = int(pos.max()) + 1
+            cos, sin = torch_paths.rope_cache(P, D, dtype=cdtype)
+            qo, ko = pkg.rope(q.to(dev), k.to(dev), pos.to(dev), cos=cos.to(dev), sin=sin.to(dev))
+            rq, rk = oracle.rope_cache(flat(q), flat(k), cache_np(cos), cache_np(sin), pos.view(-1).numpy(),
+                                       DT[dtype], CDT[cdtype])
+        assert np.array_equal(flat(qo), rq) and np.array_equal(flat(ko), rk), f"random case {case}"
+
+
 def test_cache_path_inplace_through_abi(pkg, oracle, dev):
     from oracle import torch_paths
     q, k, pos = inputs(2, 17, 8, 2, 128, torch.bfloat16, 99)
