@@ -2488,6 +2488,9 @@ enum { kTuneBlocksPerCu = 0, kTuneSeed = 1 };
 //  - k <= 64: a last chunk too short to give each of the four waves a vector would leave a wave without a bound, and
 //    the tile would take the exact re-push path; when the previous chunk can take it within one register tile, it
 //    does. k = 1 uses one slot per chunk (its workgroups take four chunks each and use the first slots of the row).
+//  - 1 < k <= 64: a row of two chunks within two register tiles is taken whole by one workgroup, tile after tile,
+//    when there are at least as many rows as CUs (512 x 32000 fp32 at k = 50: 19.2 -> 17.6 us on MI355X; the chunks'
+//    hand-off and merge cost more than the second tile's wait, while one workgroup per row still fills the GPU).
 //  - k > 64: chunks long enough for a useful bound (16k elements: a tile holds the 4 * ceil(k / 4) group maxima the
 //    bound needs) and few enough for the merge: at most kWideMaxChunks, and at most k, so that the chunks' bound
 //    headers fit the row's output indices.
@@ -2500,6 +2503,10 @@ Chunking chunking(long long rows, long long cols, long long chunk, int nchunks, 
   if (k <= kSeedMaxK) {
     const long long tail = cols - (long long)(nchunks - 1) * chunk;
     if (nchunks > 1 && tail < (long long)kThreads * width && chunk + tail <= (long long)kThreads * kTileE) --nchunks;
+    if (k > 1 && nchunks == 2 && cols <= 2LL * kThreads * kTileE && rows >= rw_host::device_cus()) {
+      chunk = cols;
+      nchunks = 1;
+    }
   } else {
     const long long most = k < kWideMaxChunks ? k : kWideMaxChunks;
     long long want = 16LL * k;

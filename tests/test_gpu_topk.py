@@ -299,6 +299,17 @@ def test_random_shapes_and_chunkings(pkg, oracle, dev):
         check(pkg, oracle, x.to(dt), k, dev, chunk=chunk, what=f"random case {case}", poison=bool(case % 2))
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_many_short_rows_taken_whole(pkg, oracle, dev, dt):
+    # as many rows as CUs or more, two chunks of a row within two register tiles: one workgroup takes the row whole
+    # (the plan's chunking at 512 x 32000 and 400 x 30000), next to k = 1 and k > 64 on the same shapes
+    g = torch.Generator().manual_seed(45)
+    for rows, cols in ((512, 32000), (400, 30000)):
+        x = (torch.randn(rows, cols, generator=g) * 2).to(dt)
+        for k in (1, 2, 50, 64, 65):
+            check(pkg, oracle, x, k, dev, what=f"short rows {rows}x{cols}", poison=True)
+
+
 def test_invalid_arguments(pkg, dev):
     L = lib(pkg)
     s = torch.cuda.current_stream().cuda_stream
