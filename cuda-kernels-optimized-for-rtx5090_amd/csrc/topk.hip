@@ -2488,6 +2488,11 @@ enum { kTuneBlocksPerCu = 0, kTuneSeed = 1 };
 //  - k <= 64: a last chunk too short to give each of the four waves a vector would leave a wave without a bound, and
 //    the tile would take the exact re-push path; when the previous chunk can take it within one register tile, it
 //    does. k = 1 uses one slot per chunk (its workgroups take four chunks each and use the first slots of the row).
+//  - 1 < k <= 64: chunks shorter than kShortChunk are joined into chunks of one register tile (16384 elements), or of
+//    half of one when that grid would have fewer than 64 workgroups: a chunk's chain after its loads costs about the
+//    same at any length up to a tile, and every chunk adds a list to its row's merge (on MI355X, the plan's chunks
+//    of 2048 or 4008 columns at k = 50: 1 x 128256 11.3 -> 9.4 us, 8 x 128256 16.8 -> 10.3 us, 32 x 128256
+//    19.6 -> 12.2 us, 16 x 32000 11.5 -> 9.9 us).
 //  - 1 < k <= 64: a row of two chunks within two register tiles is taken whole by one workgroup, tile after tile,
 //    when there are at least as many rows as CUs (512 x 32000 fp32 at k = 50: 19.2 -> 17.6 us on MI355X; the chunks'
 //    hand-off and merge cost more than the second tile's wait, while one workgroup per row still fills the GPU).
@@ -2499,8 +2504,18 @@ struct Chunking {
   int nchunks;
   long long slots;
 };
+constexpr long long kShortChunk = 8192;
+
 Chunking chunking(long long rows, long long cols, long long chunk, int nchunks, int k, int width) {
   if (k <= kSeedMaxK) {
+    const long long tile = (long long)kThreads * kTileE;
+    if (k > 1 && nchunks > 1 && chunk < kShortChunk) {
+      const long long want = rows * ((cols + tile - 1) / tile) >= 64 ? tile : tile / 2;  // a multiple of 8
+      if (want > chunk) {
+        chunk = want < cols ? want : cols;
+        nchunks = (int)((cols + chunk - 1) / chunk);  // fewer than the caller's: its work holds them
+      }
+    }
     const long long tail = cols - (long long)(nchunks - 1) * chunk;
     if (nchunks > 1 && tail < (long long)kThreads * width && chunk + tail <= (long long)kThreads * kTileE) --nchunks;
     if (k > 1 && nchunks == 2 && cols <= 2LL * kThreads * kTileE && rows >= rw_host::device_cus()) {

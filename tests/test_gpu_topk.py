@@ -310,6 +310,16 @@ def test_many_short_rows_taken_whole(pkg, oracle, dev, dt):
             check(pkg, oracle, x, k, dev, what=f"short rows {rows}x{cols}", poison=True)
 
 
+def test_joined_short_chunks(pkg, oracle, dev):
+    # the caller's short chunks joined to 8192 or 16384 columns: 80 chunks per row (more heads than a wave holds and
+    # more list entries than one batch: the merge's block floor and streamed lists), a few rows, one row
+    g = torch.Generator().manual_seed(46)
+    for rows, cols in ((2, 40 * 16384), (8, 128256), (1, 128256)):
+        x = torch.randn(rows, cols, generator=g) * 2
+        for k in (7, 13, 50, 64):
+            check(pkg, oracle, x, k, dev, chunk=2048, what=f"joined chunks {rows}x{cols}", poison=True)
+
+
 def test_invalid_arguments(pkg, dev):
     L = lib(pkg)
     s = torch.cuda.current_stream().cuda_stream
