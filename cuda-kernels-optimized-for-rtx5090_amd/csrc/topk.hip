@@ -2488,11 +2488,13 @@ enum { kTuneBlocksPerCu = 0, kTuneSeed = 1 };
 //  - k <= 64: a last chunk too short to give each of the four waves a vector would leave a wave without a bound, and
 //    the tile would take the exact re-push path; when the previous chunk can take it within one register tile, it
 //    does. k = 1 uses one slot per chunk (its workgroups take four chunks each and use the first slots of the row).
-//  - 1 < k <= 64: chunks shorter than kShortChunk are joined into chunks of one register tile (16384 elements), or of
-//    half of one when that grid would have fewer than 64 workgroups: a chunk's chain after its loads costs about the
-//    same at any length up to a tile, and every chunk adds a list to its row's merge (on MI355X, the plan's chunks
-//    of 2048 or 4008 columns at k = 50: 1 x 128256 11.3 -> 9.4 us, 8 x 128256 16.8 -> 10.3 us, 32 x 128256
-//    19.6 -> 12.2 us, 16 x 32000 11.5 -> 9.9 us).
+//  - chunks shorter than kShortChunk are joined into chunks of one register tile (16384 elements), or of half of one
+//    when that grid would have fewer than 64 workgroups (for k = 1 unless a row fits two tiles): a chunk's chain
+//    after its loads costs about the same at any length up to a tile, and every chunk adds a list to its row's merge.
+//    On MI355X, from the plan's chunks of 2048 or 4008 columns at k = 50: 1 x 128256 11.3 -> 9.4 us, 8 x 128256
+//    16.8 -> 10.3 us, 32 x 128256 19.6 -> 12.2 us, 16 x 32000 11.5 -> 9.9 us; at k = 1: 32 x 128256 10.2 -> 6.9 us,
+//    4 x 128256 6.3 -> 5.4 us, 16 x 32000 6.4 -> 4.8 us; at k = 300, from chunks of 16 k = 4800 columns: 8 x 128256
+//    26.8 -> 13.1 us, 32 x 128256 33.6 -> 15.2 us.
 //  - 1 < k <= 64: a row of two chunks within two register tiles is taken whole by one workgroup, tile after tile,
 //    when there are at least as many rows as CUs (512 x 32000 fp32 at k = 50: 19.2 -> 17.6 us on MI355X; the chunks'
 //    hand-off and merge cost more than the second tile's wait, while one workgroup per row still fills the GPU).
@@ -2507,10 +2509,14 @@ struct Chunking {
 constexpr long long kShortChunk = 8192;
 
 Chunking chunking(long long rows, long long cols, long long chunk, int nchunks, int k, int width) {
+  const long long tile = (long long)kThreads * kTileE;
+  // the length short chunks are joined to (a multiple of 8); k = 1 takes a row of up to two tiles whole (its
+  // workgroups take two chunks each)
+  const bool whole_tiles = rows * ((cols + tile - 1) / tile) >= 64 || (k == 1 && cols <= 2 * tile);
+  const long long joined = whole_tiles ? tile : tile / 2;
   if (k <= kSeedMaxK) {
-    const long long tile = (long long)kThreads * kTileE;
-    if (k > 1 && nchunks > 1 && chunk < kShortChunk) {
-      const long long want = rows * ((cols + tile - 1) / tile) >= 64 ? tile : tile / 2;  // a multiple of 8
+    if (nchunks > 1 && chunk < kShortChunk) {
+      const long long want = joined;
       if (want > chunk) {
         chunk = want < cols ? want : cols;
         nchunks = (int)((cols + chunk - 1) / chunk);  // fewer than the caller's: its work holds them
@@ -2525,6 +2531,7 @@ Chunking chunking(long long rows, long long cols, long long chunk, int nchunks, 
   } else {
     const long long most = k < kWideMaxChunks ? k : kWideMaxChunks;
     long long want = 16LL * k;
+    if (chunk < kShortChunk && want < joined) want = joined;
     if (want < (cols + most - 1) / most) want = (cols + most - 1) / most;
     if (chunk < want && nchunks > 1) {
       chunk = want < cols ? (want + 7) / 8 * 8 : cols;

@@ -52,7 +52,8 @@ CASES = [
     ("k_equals_cols", 2, 1024, 0, "1024", 0, 2048, 1, 14, -1, "randn"),
     ("shuffled", 2, 20000, 0, ALL_K, 4096, 2048, 2, 15, 99, "randn"),
     ("shuffled_bf16", 2, 20000, 1, "1,50,1024", 2052, 2048, 2, 16, 7, "ints"),
-    ("many_chunks_wide", 2, 100000, 0, "65", 1024, 2048, 1, 17, -1, "randn"),
+    # 65 chunks of a k = 65 row (at most k lists; short chunks are joined to 8192 or more columns)
+    ("many_chunks_wide", 1, 65 * 16384, 0, "65", 1024, 2048, 1, 17, -1, "randn"),
     # k <= 64 over 80 chunks (short chunks are joined to 8192 columns): more heads than a wave holds and more list
     # entries than one batch, so the merge finds its floor over the block and streams the lists
     ("many_chunks_joined", 1, 40 * 16384, 0, "7,13,64", 2048, 2048, 1, 26, -1, "randn"),
