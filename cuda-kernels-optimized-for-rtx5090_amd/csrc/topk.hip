@@ -2499,8 +2499,10 @@ enum { kTuneBlocksPerCu = 0, kTuneSeed = 1 };
 //    when there are at least as many rows as CUs (512 x 32000 fp32 at k = 50: 19.2 -> 17.6 us on MI355X; the chunks'
 //    hand-off and merge cost more than the second tile's wait, while one workgroup per row still fills the GPU).
 //  - k > 64: chunks long enough for a useful bound (16k elements: a tile holds the 4 * ceil(k / 4) group maxima the
-//    bound needs) and few enough for the merge: at most kWideMaxChunks, and at most k, so that the chunks' bound
-//    headers fit the row's output indices.
+//    bound needs), and at least as long as the joined chunks above (from the plan's 9496 columns at 64 x 151936:
+//    k = 65 20.8 -> 19.1 us, k = 300 21.3 -> 19.7 us; 32 x 262144: k = 65 23.9 -> 18.3 us, k = 300 39.7 -> 19.4 us),
+//    and few enough for the merge: at most kWideMaxChunks, and at most k, so that the chunks' bound headers fit the
+//    row's output indices.
 struct Chunking {
   long long chunk;
   int nchunks;
@@ -2531,7 +2533,7 @@ Chunking chunking(long long rows, long long cols, long long chunk, int nchunks, 
   } else {
     const long long most = k < kWideMaxChunks ? k : kWideMaxChunks;
     long long want = 16LL * k;
-    if (chunk < kShortChunk && want < joined) want = joined;
+    if (want < joined) want = joined;
     if (want < (cols + most - 1) / most) want = (cols + most - 1) / most;
     if (chunk < want && nchunks > 1) {
       chunk = want < cols ? (want + 7) / 8 * 8 : cols;
