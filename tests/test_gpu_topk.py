@@ -311,8 +311,9 @@ def test_many_short_rows_taken_whole(pkg, oracle, dev, dt):
 
 
 def test_joined_short_chunks(pkg, oracle, dev):
-    # the caller's short chunks joined to 8192 or 16384 columns: 80 chunks per row (more heads than a wave holds and
-    # more list entries than one batch: the merge's block floor and streamed lists), a few rows, one row
+    # the caller's short chunks joined to 16384 or 8192 columns: 40 chunks per row (at k = 50 and 64, 80 heads, more
+    # than a wave holds, and at k = 64 2560 list entries, more than one batch: the merge's block floor and streamed
+    # lists), 8 rows of 8 chunks, one row of 16
     g = torch.Generator().manual_seed(46)
     for rows, cols in ((2, 40 * 16384), (8, 128256), (1, 128256)):
         x = torch.randn(rows, cols, generator=g) * 2
