@@ -313,6 +313,8 @@ struct TileSmem {
   u64 top[kSeedMaxK];  // an output row's composites in order (for the fused draw)
   uint32_t red[2][kWaves];
   int cnt[kWaves];
+  alignas(16) uint32_t lm[kThreads];  // a tile's lane maxima (the threshold of a row taken whole)
+  uint32_t thr;
   u64 pick;
   int last;
 };
@@ -354,6 +356,35 @@ __device__ __forceinline__ uint32_t wave_kth32(uint32_t v, bool ok, int k) {
   for (int b = top; b >= 0 && b > top - kThrBits; --b) {
     const uint32_t cand = p | (1u << b);  // >= 1: the lanes without ok (0) never count
     if (__popcll(__ballot(v >= cand)) >= k) p = cand;
+  }
+  return p;
+}
+
+// wave_kth32 over four values per lane (a workgroup's 256 lane maxima, 0 for a lane without elements): a lower bound
+// of the k-th largest with at least k values at or above it, within kThrBits bits below the highest differing one;
+// 0 when fewer than k values are nonzero. Wave-uniform.
+__device__ __forceinline__ uint32_t wave_kth32x4(const uint32_t (&v)[4], int k) {
+  int n = 0;
+  uint32_t hi = 0, lo = 0xffffffffu;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    n += __popcll(__ballot(v[j] != 0u));
+    hi = v[j] > hi ? v[j] : hi;
+    lo = v[j] != 0u && v[j] < lo ? v[j] : lo;
+  }
+  if (n < k) return 0u;
+  const uint32_t mx = wave_ext32<true>(hi);
+  if (k == 1) return mx;
+  const uint32_t mn = wave_ext32<false>(lo);
+  if (mx == mn) return mx;
+  const int top = 31 - __builtin_clz(mx ^ mn);
+  uint32_t p = mx & ~((2u << top) - 1u);
+  for (int b = top; b >= 0 && b > top - kThrBits; --b) {
+    const uint32_t cand = p | (1u << b);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c += __popcll(__ballot(v[j] >= cand));
+    if (c >= k) p = cand;
   }
   return p;
 }
@@ -1487,7 +1518,7 @@ __global__ void __launch_bounds__(kOneThreads)
 // complete and counts its arrival on the caller's counters[row]; the row's last arrival merges the lists (merge_lists)
 // and zeroes the counter for the next launch -- no L2 write-back or invalidate, and no second kernel (the protocol of
 // topk/kernel.cu:411-442, without its __threadfence: see hand_off_arrive).
-template <typename T, bool VEC, bool DRAW>
+template <typename T, bool VEC, bool DRAW, bool WHOLE>
 __global__ void __launch_bounds__(kThreads)
     topk_tile(const T* __restrict__ x, void* __restrict__ values, long long* __restrict__ indices,
               u64* __restrict__ work, unsigned* __restrict__ counters, long long cols, long long chunk, int nchunks,
@@ -1515,9 +1546,27 @@ __global__ void __launch_bounds__(kThreads)
     const uint32_t m = tile.max_key();  // vector by vector as the loads complete
     TOPK_STAGE_AT(1, m);
     TOPK_WAVE_STAGE_AT(m);
-    const uint32_t tw = __popcll(__ballot(has)) >= kw ? wave_kth32(m, has, kw) : 0u;
-    TOPK_STAGE_AT(11, tw);
-    const uint32_t tb = red.min(tw);
+    uint32_t tb;
+    if constexpr (WHOLE) {
+      // a row taken whole (no merge after it): the k-th of the workgroup's 256 lane maxima, found by wave 0, admits
+      // about 56 elements of a randn tile at k = 50 against 76 (512 x 32000: 17.54 -> 16.32 us); for split rows the
+      // per-wave bounds below measured faster
+      s.lm[threadIdx.x] = has ? m : 0u;
+      __syncthreads();
+      if (wave_id() == 0) {
+        const u32x4 q = reinterpret_cast<const u32x4*>(s.lm)[lane_id()];
+        const uint32_t v4[4] = {q.x, q.y, q.z, q.w};
+        const uint32_t tw = wave_kth32x4(v4, k);
+        TOPK_STAGE_AT(11, tw);
+        if (lane_id() == 0) s.thr = tw;
+      }
+      __syncthreads();
+      tb = s.thr;
+    } else {
+      const uint32_t tw = __popcll(__ballot(has)) >= kw ? wave_kth32(m, has, kw) : 0u;
+      TOPK_STAGE_AT(11, tw);
+      tb = red.min(tw);
+    }
     TOPK_STAGE(2);
     thr = tb > thr ? tb : thr;
     L.cnt = __builtin_amdgcn_readfirstlane(L.cnt);
@@ -2565,11 +2614,15 @@ int launch_chunks(const void* x, void* values, void* indices, void* work, void* 
       return (int)hipGetLastError();
     }
     if (sa.out)
-      hipLaunchKernelGGL((topk_tile<T, VEC, true>), dim3((unsigned)nchunks, (unsigned)rows), dim3(kThreads), 0, stream,
+      hipLaunchKernelGGL((topk_tile<T, VEC, true, false>), dim3((unsigned)nchunks, (unsigned)rows), dim3(kThreads), 0,
+                         stream, (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols,
+                         chunk, nchunks, k, sa);
+    else if (nchunks == 1)
+      hipLaunchKernelGGL((topk_tile<T, VEC, false, true>), dim3(1u, (unsigned)rows), dim3(kThreads), 0, stream,
                          (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols, chunk,
                          nchunks, k, sa);
     else
-      hipLaunchKernelGGL((topk_tile<T, VEC, false>), dim3((unsigned)nchunks, (unsigned)rows), dim3(kThreads), 0,
+      hipLaunchKernelGGL((topk_tile<T, VEC, false, false>), dim3((unsigned)nchunks, (unsigned)rows), dim3(kThreads), 0,
                          stream, (const T*)x, values, (long long*)indices, (u64*)work, (unsigned*)counters, cols,
                          chunk, nchunks, k, sa);
     return (int)hipGetLastError();
@@ -2607,7 +2660,8 @@ extern "C" long long plan(long long rows, long long cols, int dtype, int threads
   if (per_cu <= 0) {
     if (occ <= 0) {
       int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_tile<float, true, false>, kThreads, 0) != hipSuccess ||
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, topk_tile<float, true, false, false>, kThreads, 0) !=
+              hipSuccess ||
           n <= 0) {
         (void)hipGetLastError();
         n = 4;
