@@ -344,7 +344,11 @@ constexpr int kThrBits = 12;  // bits resolved by the threshold search below the
 // A lower bound of the k-th largest (1 <= k <= the number of lanes with ok) of the wave's 32-bit values v (one per
 // lane) with at least k of them at or above it: a bitwise search from the highest bit where the valid minimum and
 // maximum differ, keeping the largest prefix with at least k values at or above it (counted with ballots), stopped
-// after kThrBits bits (the bound is then within 2^(top - kThrBits) of the k-th). Wave-uniform.
+// after kThrBits bits (the bound is then within 2^(top - kThrBits) of the k-th). Wave-uniform. The values are shifted
+// so that the searched bits are always bits kThrBits - 1 .. 0 and the loop unrolls into four scalar instructions and
+// one compare per bit (a search that also visits bits above the highest differing one leaves the prefix as it is):
+// C5 k = 50 19.36 -> 18.95 us against the loop over bit positions, whose scalar instructions the CU's one scalar unit
+// issues for every wave of every workgroup in the same phase.
 __device__ __forceinline__ uint32_t wave_kth32(uint32_t v, bool ok, int k) {
   v = ok ? v : 0u;
   const uint32_t mx = wave_ext32<true>(v);
@@ -352,12 +356,15 @@ __device__ __forceinline__ uint32_t wave_kth32(uint32_t v, bool ok, int k) {
   const uint32_t mn = wave_ext32<false>(ok ? v : 0xffffffffu);
   if (mx == mn) return mx;
   const int top = 31 - __builtin_clz(mx ^ mn);
-  uint32_t p = mx & ~((2u << top) - 1u);
-  for (int b = top; b >= 0 && b > top - kThrBits; --b) {
+  const int sh = top >= kThrBits ? top - (kThrBits - 1) : 0;
+  const uint32_t vs = v >> sh;
+  uint32_t p = (mx & ~((2u << top) - 1u)) >> sh;
+#pragma unroll
+  for (int b = kThrBits - 1; b >= 0; --b) {
     const uint32_t cand = p | (1u << b);  // >= 1: the lanes without ok (0) never count
-    if (__popcll(__ballot(v >= cand)) >= k) p = cand;
+    if (__popcll(__ballot(vs >= cand)) >= k) p = cand;
   }
-  return p;
+  return p << sh;
 }
 
 // wave_kth32 over four values per lane (a workgroup's 256 lane maxima, 0 for a lane without elements): a lower bound
@@ -378,15 +385,20 @@ __device__ __forceinline__ uint32_t wave_kth32x4(const uint32_t (&v)[4], int k) 
   const uint32_t mn = wave_ext32<false>(lo);
   if (mx == mn) return mx;
   const int top = 31 - __builtin_clz(mx ^ mn);
-  uint32_t p = mx & ~((2u << top) - 1u);
-  for (int b = top; b >= 0 && b > top - kThrBits; --b) {
+  const int sh = top >= kThrBits ? top - (kThrBits - 1) : 0;
+  uint32_t vs[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) vs[j] = v[j] >> sh;
+  uint32_t p = (mx & ~((2u << top) - 1u)) >> sh;
+#pragma unroll
+  for (int b = kThrBits - 1; b >= 0; --b) {
     const uint32_t cand = p | (1u << b);
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) c += __popcll(__ballot(v[j] >= cand));
+    for (int j = 0; j < 4; ++j) c += __popcll(__ballot(vs[j] >= cand));
     if (c >= k) p = cand;
   }
-  return p;
+  return p << sh;
 }
 
 // Block-wide reductions of wave-uniform values through two alternating rows of LDS slots: one barrier each (a row is
