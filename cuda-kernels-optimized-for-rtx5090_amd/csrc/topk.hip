@@ -307,8 +307,9 @@ constexpr int kStageGroups = 64;  // each wave's staged 8-element groups in a fi
 
 struct TileSmem {
   u64 seg[kWaves][kTileSeg + 2];  // (+ a spare slot for a batch's writes past the end, padded to 16 bytes)
-  u32x4 stage[kWaves][2 * kStageGroups];  // filter_groups: each wave's staged groups, 8 fp32 elements each
-  uint32_t stage_at[kWaves][kStageGroups];  // and the index of each staged group's first element
+  u32x4 stage[kWaves][2 * kStageGroups + 2];  // filter_groups: each wave's staged groups, 8 fp32 elements each (+ a
+                                              // spare group for the writes past the end)
+  uint32_t stage_at[kWaves][kStageGroups + 1];  // and the index of each staged group's first element
   alignas(16) u64 sorted[kTileSort];
   u64 top[kSeedMaxK];  // an output row's composites in order (for the fused draw)
   uint32_t red[2][kWaves];
@@ -967,11 +968,10 @@ struct Tile {
         if (c) {
           const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)n));
-          if (pos < kStageGroups) {
-            stage[2 * pos] = r[2 * g];
-            stage[2 * pos + 1] = r[2 * g + 1];
-            stage_at[pos] = (uint32_t)first(2 * g);
-          }
+          const int at = pos < kStageGroups ? pos : kStageGroups;  // past the end: the spare group
+          stage[2 * at] = r[2 * g];
+          stage[2 * at + 1] = r[2 * g + 1];
+          stage_at[at] = (uint32_t)first(2 * g);
         }
         n += __popcll(m);
       }
@@ -988,7 +988,8 @@ struct Tile {
       const uint32_t u = su[ok ? i : 0];
       const uint32_t at = stage_at[ok ? slot : 0] + (uint32_t)((e >> 2) * NT * W + (e & 3));
       // over a non-negative threshold the key of an admitted element is its bits with the top bit set
-      L.push(((u64)(u | 0x80000000u) << 32) | (u64)(~at), ok && (int)u >= t);
+      const bool keep = ok && (int)u >= t;
+      L.push_mask(__ballot(keep), keep, [&] { return ((u64)(u | 0x80000000u) << 32) | (u64)(~at); });
     }
   }
 
