@@ -348,8 +348,8 @@ constexpr int kThrBits = 12;  // bits resolved by the threshold search below the
 // after kThrBits bits (the bound is then within 2^(top - kThrBits) of the k-th). Wave-uniform. The values are shifted
 // so that the searched bits are always bits kThrBits - 1 .. 0 and the loop unrolls into four scalar instructions and
 // one compare per bit (a search that also visits bits above the highest differing one leaves the prefix as it is):
-// C5 k = 50 19.36 -> 18.95 us against the loop over bit positions, whose scalar instructions the CU's one scalar unit
-// issues for every wave of every workgroup in the same phase.
+// 128 x 128256 k = 50 19.36 -> 18.95 us against the loop over bit positions, whose scalar instructions the CU's one
+// scalar unit issues for every wave of every workgroup in the same phase.
 __device__ __forceinline__ uint32_t wave_kth32(uint32_t v, bool ok, int k) {
   v = ok ? v : 0u;
   const uint32_t mx = wave_ext32<true>(v);
@@ -594,8 +594,8 @@ __device__ __forceinline__ int rank_in(const u64* list, int n16, u64 c) {
 
 // The rank sort of a short list split over the block: for n <= 64 every wave ranks all n entries against a quarter of
 // the list, for n <= 128 each half of the block against a half, so that a thread reads a quarter or a half of the list
-// instead of all of it (below 129 entries one thread per entry would leave two or three waves idle); the partial
-// counts meet behind one barrier. (C5: about 75 candidates per chunk, 60 in the merge; a list of 16 or fewer loses a
+// instead of all of it (below 129 entries one thread per entry would leave two or three waves idle); the partial counts
+// meet behind one barrier. (128 x 128256: about 75 candidates per chunk, 60 in the merge; a list of 16 or fewer loses a
 // little to the barrier, but a separate path for it made the kernel's code larger and every k slower.) rank_pad(n) is
 // the length the list must be zero-padded to (the zeros rank below every composite).
 __device__ __forceinline__ int rank_groups(int n) { return n <= 64 ? 4 : n <= 128 ? 2 : 1; }
@@ -785,8 +785,8 @@ __device__ __forceinline__ void stage_stamp(int slot) {
 // threshold key K with bits t, key(u) >= K iff (int)u >= (int)t when K is a non-negative value, iff u <= t (unsigned)
 // when K is negative.
 // WL: a tile whose vectors are whole but for the last takes them without the per-vector select of the sentinel's
-// address (the k = 1 kernel: C5 13.43 -> 13.25 us, 512 x 32000 12.30 -> 12.11 us; the other kernels measured from
-// 0.1 us faster to 0.3 us slower with it, interleaved on one MI355X).
+// address (the k = 1 kernel: 128 x 128256 13.43 -> 13.25 us, 512 x 32000 12.30 -> 12.11 us; the other kernels
+// measured from 0.1 us faster to 0.3 us slower with it, interleaved on one MI355X).
 template <typename T, bool VEC, int NT = kThreads, int EPL = kTileE, bool WL = false>
 struct Tile {
   static constexpr int W = Fmt<T>::W;
@@ -1732,9 +1732,9 @@ __device__ __forceinline__ void write_ranked_regs(S& s, const u64 (&cin)[NS], co
   // broadcasts rather than scattered reads) and write neighbouring output positions. Every position first, then the
   // stores. A thread's reads are issued together, stage by stage (its entries, their buckets' ranges, the buckets'
   // first four members), with no branch between them but the block-uniform one that skips the entry slots r with
-  // r * kThreads >= m (C5 at k = 65 fills one of the eight): every index stays inside the buffer whether or not the
-  // entry exists (i < kWideList; f + 3 <= m + 3 < kWideCap), and a missing entry's position is discarded. Buckets of
-  // more than four members (rare) are finished after.
+  // r * kThreads >= m (128 x 128256 at k = 65 fills one of the eight): every index stays inside the buffer whether or
+  // not the entry exists (i < kWideList; f + 3 <= m + 3 < kWideCap), and a missing entry's position is discarded.
+  // Buckets of more than four members (rare) are finished after.
   u64 c[P];
   int pos[P], f[P], n[P];
 #pragma unroll
@@ -1847,7 +1847,7 @@ __device__ __forceinline__ u64 cut_publish(S& s, int m, int k, u64* list, uint32
   lo = lo < hi ? lo : hi;
   const uint32_t D = hi - lo;
   const int sh = (D >> 12) ? (32 - __builtin_clz(D)) - 12 : 0;  // D >> sh < kRankBuckets
-  // the candidate slots in use (block-uniform): the rest are skipped as a block (C5 at k = 1024: 2 of 8)
+  // the candidate slots in use (block-uniform): the rest are skipped as a block (128 x 128256 at k = 1024: 2 of 8)
   const int used = (m + kThreads - 1) / kThreads;
   u64 c[P];
   int bk[P];
@@ -2109,15 +2109,15 @@ __device__ __forceinline__ bool hist_bounds(S& s, BlockRed& red, const uint32_t 
 
 // 64 < k <= 1024: one 256-thread workgroup per (chunk, row), the chunk in register tiles as topk_tile. A split row's
 // chunk admits its candidates at an m-bound, m = min(k, 2 ceil(k * chunk / cols) + kListSlack): twice a full chunk's
-// share of the row's k and a margin (C5 at k = 1024: 326 of 16384), so that rows whose largest values cluster in one
-// chunk at up to about twice the density elsewhere need no second look at x. Per tile: each lane's 64 elements form
-// kWideGroups groups; a group's largest element has the group behind it, so the m-th largest of the block's group
+// share of the row's k and a margin (128 x 128256 at k = 1024: 326 of 16384), so that rows whose largest values cluster
+// in one chunk at up to about twice the density elsewhere need no second look at x. Per tile: each lane's 64 elements
+// form kWideGroups groups; a group's largest element has the group behind it, so the m-th largest of the block's group
 // maxima has m distinct elements at or above it: with the m-th of the earlier tiles it is the admission key (about
 // 1.1 m admitted per tile on continuous data). The q-th largest, q = ceil(k / nchunks), gives a q-bound the same way.
-// Admitted elements are appended to an LDS buffer (fp32: through each wave's staging area; else one LDS atomic per
-// wave and 16 elements per lane); a tile that overflows it (ties, adversarial orders) is appended again vector by
-// vector from the buffer's m-th, pruning to m (histogram narrowing) whenever a vector might not fit. An unsplit row
-// keeps k, ranks its candidates (write_ranked) and writes the first k.
+// Admitted elements are appended to an LDS buffer (fp32: through each wave's staging area; else one LDS atomic per wave
+// and 16 elements per lane); a tile that overflows it (ties, adversarial orders) is appended again vector by vector
+// from the buffer's m-th, pruning to m (histogram narrowing) whenever a vector might not fit. An unsplit row keeps k,
+// ranks its candidates (write_ranked) and writes the first k.
 //
 // A split row's chunk writes its list to the caller's work: the row's [nchunks, k] slots hold the nchunks lists of ls
 // entries (zero-padded), then, when m < k, each chunk's separator. When m < k the list is the chunk's candidates at or
@@ -2245,8 +2245,8 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   }
   TOPK_STAGE(3);
   // publish: the list (zero-padded to ls), its separator (m < k) and the header (k-bound key << 32 | q-bound key) in
-  // the row's output. When m < k the list holds the chunk's candidates as they are when they fit ls (C5 at k = 1024:
-  // about 350 of at most 384), else their m largest (cut_publish).
+  // the row's output. When m < k the list holds the chunk's candidates as they are when they fit ls (128 x 128256 at
+  // k = 1024: about 350 of at most 384), else their m largest (cut_publish).
   u64* wr = work + row * (long long)nchunks * k;
   u64* mine = wr + (long long)part * ls;
   if (s.count > kWideList) prune(s, m);
@@ -2290,8 +2290,8 @@ __global__ void __launch_bounds__(kThreads, 4)  // four waves per SIMD: 128 VGPR
   // merge (the row's last arrival): the floor from the headers, then every list's entries at or above it
   auto ld = [&](const u64* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
   const int t = (int)threadIdx.x, lane = lane_id(), wave = wave_id();
-  // Rows whose lists fit the registers (C5: 8 x 384 entries) read them all at once, right after the headers: the
-  // floor's reduction runs while the lists' loads are in flight (loads return in order), and one block scan places
+  // Rows whose lists fit the registers (128 x 128256: 8 x 384 entries) read them all at once, right after the headers:
+  // the floor's reduction runs while the lists' loads are in flight (loads return in order), and one block scan places
   // the entries at or above it.
   constexpr int kGatherAll = 3072;  // list entries the merger reads in one batch
   constexpr int PB = kGatherAll / kThreads;

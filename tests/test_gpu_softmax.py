@@ -137,7 +137,7 @@ def test_long_rows_single_pass_and_stream(pkg, oracle, dev, rows, cols, dtype):
 
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])
 def test_coresident_graph_replay(pkg, oracle, dev, dtype):
-    """A C4-shaped launch (64 x 262144, the co-resident tier) recorded into a HIP graph with torch.cuda.graph and
+    """A 64 x 262144 launch (the co-resident tier) recorded into a HIP graph with torch.cuda.graph and
     replayed on new values of x, with eager launches of other values on the same pair-table slots between some
     replays. Each replay must take fresh tags on the device: with the tags of the capture it would accept the pairs
     the replay before it left. The wait budget is raised to 2^30 ticks (about 10 s), so a replay can only finish

@@ -124,10 +124,10 @@ def test_rmsnorm_matches_torch_path(oracle, dtype):
     _check_rms_against_torch(oracle, x, w, name)
 
 
-def test_rmsnorm_c2_whole_config_equals_torch(oracle, pkg):
-    """The whole C2 config (x [16384, 4096] bf16, w [4096], eps 1e-6): the oracle equals the reference's torch
-    expression (rmsnorm/candidate.py:3-4, weighted as torch's w * y) bit for bit on all 67,108,864 outputs, weighted
-    and plain."""
+def test_rmsnorm_16384x4096_whole_workload_equals_torch(oracle, pkg):
+    """The whole weighted RMSNorm workload (x [16384, 4096] bf16, w [4096], eps 1e-6): the oracle equals the
+    reference's torch expression (rmsnorm/candidate.py:3-4, weighted as torch's w * y) bit for bit on all 67,108,864
+    outputs, weighted and plain."""
     from oracle import torch_paths
     inp = pkg.workloads.rmsnorm_16384x4096()
     x, w, eps = inp["x"], inp["weight"], inp["eps"]
@@ -274,8 +274,8 @@ def test_rope_freq_vs_torch_cache(oracle):
     assert ((of - tf).abs() <= tf.abs() * 2 ** -7 + pair * 2 ** -22).all()
 
 
-def test_rope_c3_on_the_fly_vs_torch_cache_whole_config(oracle, pkg):
-    """The whole C3 config (q [4, 4096, 32, 128] and k [4, 4096, 8, 128] bf16, positions 0..4095, theta 1e4): the
+def test_rope_4x4096_on_the_fly_vs_torch_cache_whole_workload(oracle, pkg):
+    """The whole RoPE workload (q [4, 4096, 32, 128] and k [4, 4096, 8, 128] bf16, positions 0..4095, theta 1e4): the
     on-the-fly form (cos/sin of the fp32 angle, correctly rounded from fp64) against the reference's PyTorch path with
     a cos/sin cache built by torch, over all 83,886,080 outputs. torch's cos/sin differ from the correctly rounded
     values by one fp32 ulp in about 5% of the cache's entries. That moves 349 outputs (274 of q, 75 of k) by at least
