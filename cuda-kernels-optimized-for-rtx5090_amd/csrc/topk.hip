@@ -1578,7 +1578,7 @@ __global__ void __launch_bounds__(kThreads)
     uint32_t tb;
     if constexpr (WHOLE) {
       // a row taken whole (no merge after it): the k-th of the workgroup's 256 lane maxima, found by wave 0, admits
-      // about 56 elements of a randn tile at k = 50 against 76 (512 x 32000: 17.54 -> 16.32 us); for split rows the
+      // about 56 elements of a randn tile at k = 50 against 76 (512 x 32000: 17.6 -> 16.5 us); for split rows the
       // per-wave bounds below measured faster
       s.lm[threadIdx.x] = has ? m : 0u;
       __syncthreads();
